@@ -1,0 +1,197 @@
+#!/usr/bin/env python3
+"""MoE-layer decode benchmark on one MI355X.
+
+Metric: MoE-layer decode tok/s at batch 1, and achieved HBM
+GB/s as a fraction of the 8 TB/s peak.
+
+Workload (default cfg0): one OLMoE-shaped MoE layer (h 2048, 64 experts,
+top-8, SwiGLU intermediate 1024, 4-bit group-64 experts), batch-1 decode.
+To keep the expert weights out of the 256 MB Infinity Cache, R distinct
+layer replicas (R * 216 MiB) are resident and each step runs one token
+through all R of them in order (one HIP graph launch); `value` counts
+layer-tokens per second.  All inputs are resident in HBM before timing.
+
+A step = one token through the MoE block of each of the R replicas
+(router + top-K, expert dispatch, gate/up/SwiGLU, down, combine + residual).
+
+The CPU baseline is the scalar oracle (oracle/, one thread) timed on a
+bounded sample of the same workload, in the same run.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "MoE-layer decode tok/s at batch 1; achieved HBM GB/s as % of peak"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(shape, expert_bytes: int, x_bytes: int, with_residual: bool) -> int:
+    """Bytes one token must move through one MoE layer: the K selected expert
+    blocks, the bf16 router, the input, the residual and the output."""
+    h = shape.hidden
+    return (shape.top_k * expert_bytes + shape.num_experts * h * 2 + h * x_bytes
+            + (h * 4 if with_residual else 0) + h * 4)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="cfg0", choices=["cfg0", "cfg2"])
+    ap.add_argument("--replicas", type=int, default=0,
+                    help="distinct layer replicas (default: enough for >= 2 GiB of experts)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bound on the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--seed", type=int, default=2026)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
+              "(the MoE layer's multi-GPU sharding is a design, not a run). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import m1moe_amd as m
+    from m1moe_amd import synth
+    from m1moe_amd.engine import MoEBlock
+
+    wl = synth.CONFIGS[args.config]
+    one = wl.shape(1)
+    eb = m.expert_bytes(one)
+    layer_bytes = one.num_experts * eb
+    R = args.replicas or max(2, -(-2 * 1024 ** 3 // layer_bytes))
+    shape = wl.shape(R)
+    h, K = shape.hidden, shape.top_k
+    log(f"{wl.description}: {R} replicas x {layer_bytes / 2**20:.0f} MiB")
+
+    ctx = m.HIPContext(shape, device=0)
+    blk = MoEBlock(ctx)
+    t0 = time.time()
+    img0 = router0 = None
+    for r in range(R):
+        img = synth.layer_image(shape, args.seed, r)
+        router = synth.router(shape, args.seed, r)
+        ctx.upload_layer_experts(r, img)
+        ctx.upload_router(r, router)
+        if r == 0:
+            img0, router0 = img, router
+        del img
+    log(f"uploaded {R} layers in {time.time() - t0:.1f}s")
+
+    xs = synth.activations_bf16(shape, args.seed, R)
+    res = synth.residual_f32(shape, args.seed, R)
+    dx = [ctx.to_device(xs[r]) for r in range(R)]
+    dres = [ctx.to_device(res[r]) for r in range(R)]
+    dout = [ctx.alloc(h * 4) for _ in range(R)]
+    didx = ctx.alloc(K * 4)
+
+    # parity of replica 0 before any timing
+    from oracle import oracle as orc
+    oshape = orc.from_moe_shape(shape)
+    blk.forward(0, dx[0], "bf16", dres[0], dout[0], didx, None)
+    ctx.sync()
+    got = dout[0].download(np.float32)
+    want, widx, _, _ = orc.moe_decode(oshape, img0, router0, synth.bf16_to_f32(xs[0]), res[0])
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    idx_ok = bool(np.array_equal(didx.download(np.int32), widx))
+    log(f"parity replica 0: top-K exact={idx_ok} rel L2={rel:.2e}")
+    if not idx_ok or rel > 1e-2:
+        log("parity FAILED; not reporting throughput")
+        return 1
+
+    ctx.graph_begin()
+    for r in range(R):
+        blk.forward(r, dx[r], "bf16", dres[r], dout[r])
+    graph = ctx.graph_end()
+
+    for _ in range(args.warmup):
+        graph.launch()
+    ctx.sync()
+    ev0, ev1 = ctx.event(), ctx.event()
+    ctx.sync()
+    ev0.record()
+    for _ in range(args.steps):
+        graph.launch()
+    ev1.record()
+    ctx.sync()
+    ms = ev0.elapsed_ms(ev1)
+    ms_per_step = ms / args.steps
+    layer_us = ms_per_step * 1e3 / R
+    tok_s = R * args.steps / (ms * 1e-3)
+    bytes_tok = algorithmic_bytes(shape, eb, 2, True)
+    gbs = bytes_tok / (layer_us * 1e-6) / 1e9
+    log(f"{ms_per_step:.4f} ms/step, {layer_us:.3f} us/layer-token, {gbs:.0f} GB/s")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        x32 = synth.bf16_to_f32(xs[0])
+        n, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_seconds:
+            t1 = time.perf_counter()
+            orc.moe_decode(oshape, img0, router0, x32, res[0])
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        cpu = {"value": round(n / t_cpu, 3), "unit": "layer-tok/s", "cores": 1, "kind": "port",
+               "sample": f"{n} tokens of {args.config} replica-0 decode through the scalar "
+                         f"oracle on 1 thread ({t_cpu:.1f}s); host CPU: {cpu_model()}"}
+        log(f"cpu baseline: {cpu['value']} layer-tok/s")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "layer-tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 weights x f16 inputs -> f32",
+        "data": "synthetic (seeded; random-init experts/router)",
+        "config": {"workload": wl.description, "config": args.config, "hidden": h,
+                   "num_experts": shape.num_experts, "top_k": K,
+                   "intermediate": shape.intermediate, "group_size": shape.group_size,
+                   "replicas": R, "tokens_per_step": 1, "x_dtype": "bf16",
+                   "residual": "f32"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "whole MoE block per layer-token (router_topk + gate_up + "
+                               "down_combine)",
+                     "bytes_per_launch": bytes_tok, "us_per_launch": round(layer_us, 4)},
+        "cpu_baseline": cpu,
+        "parity": {"topk_exact": idx_ok, "rel_l2": rel},
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

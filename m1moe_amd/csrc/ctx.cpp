@@ -1,0 +1,634 @@
+// ctx.cpp — the C ABI of libm1moe_hip.so: context, validation, uploads,
+// memory/stream/event/graph plumbing, and the MoE-block entry points.
+//
+// The context replaces the reference's MetalContext (MetalContext.swift:
+// 69-185) for the MoE block: it owns the resident expert arena (every
+// expert of every layer in HBM, replacing the pread dispatch and the K
+// expert slots, InferenceEngine.swift:62-77,271-280, MetalContext.swift:
+// 154-172), the bf16 routers (kept bf16, unlike the f32 pre-conversion at
+// InferenceEngine.swift:99-113) and all scratch.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+#include "m1moe_hip.h"
+
+namespace m1moe {
+
+namespace {
+thread_local std::string g_last_error;
+constexpr int32_t kPrefillCap = 4096;  // tokens per m1moe_moe_prefill call
+}  // namespace
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+Geom make_geom(const m1moe_moe_shape& s) {
+    Geom g{};
+    g.h = s.hidden;
+    g.E = s.num_experts;
+    g.K = s.top_k;
+    g.I = s.intermediate;
+    g.gs = s.group_size;
+    g.L = s.num_layers;
+    g.norm = s.norm_topk_prob;
+    const uint64_t h = (uint64_t)s.hidden, i = (uint64_t)s.intermediate;
+    const uint64_t gs = (uint64_t)s.group_size;
+    const uint64_t gw = i * (h / 8) * 4, gsb = i * (h / gs) * 2;
+    const uint64_t dw = h * (i / 8) * 4, dsb = h * (i / gs) * 2;
+    const uint64_t sizes[9] = {gw, gsb, gsb, gw, gsb, gsb, dw, dsb, dsb};
+    uint64_t o = 0;
+    for (int k = 0; k < 9; ++k) {
+        g.off[k] = o;
+        o += sizes[k];
+    }
+    g.expert_bytes = o;
+    return g;
+}
+
+}  // namespace m1moe
+
+using m1moe::fail;
+
+struct m1moe_event {
+    hipEvent_t ev;
+};
+
+struct m1moe_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+struct m1moe_ctx {
+    int32_t device = 0;
+    m1moe_moe_shape shape{};
+    m1moe::Geom g{};
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    uint8_t* arena = nullptr;        // [L][E] expert blocks
+    uint16_t* routers = nullptr;     // [L][E][h] bf16
+    float* biases = nullptr;         // [L][E]
+    std::vector<bool> has_bias;
+    std::vector<bool> layer_loaded;
+    std::vector<bool> router_loaded;
+    // scratch
+    float* logits = nullptr;         // [cap][E]
+    int32_t* topk_idx = nullptr;     // [cap][K]
+    float* topk_w = nullptr;         // [cap][K]
+    uint32_t* counters = nullptr;    // [cap]
+    float* act = nullptr;            // [K][I]
+    uint32_t* err = nullptr;         // sticky device error flag
+    std::set<void*> allocs;
+};
+
+namespace {
+
+#define HIP_TRY(expr)                                                                        \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return fail(M1MOE_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));      \
+    } while (0)
+
+int32_t device_alloc(void** p, uint64_t bytes, const char* what) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return fail(M1MOE_ERR_OOM, "hipMalloc(%s, %llu bytes) failed: %s", what,
+                    (unsigned long long)bytes, hipGetErrorString(e));
+    }
+    return M1MOE_OK;
+}
+
+int32_t check_ctx(m1moe_ctx_t ctx) {
+    if (!ctx) return fail(M1MOE_ERR_INVALID, "null context");
+    return M1MOE_OK;
+}
+
+int32_t set_device(m1moe_ctx_t ctx) {
+    HIP_TRY(hipSetDevice(ctx->device));
+    return M1MOE_OK;
+}
+
+int32_t check_layer(m1moe_ctx_t ctx, int32_t layer) {
+    if (layer < 0 || layer >= ctx->shape.num_layers)
+        return fail(M1MOE_ERR_INVALID, "layer %d out of range [0, %d)", layer,
+                    ctx->shape.num_layers);
+    return M1MOE_OK;
+}
+
+int32_t check_dev_ptr(const void* p, const char* what, bool nullable) {
+    if (!p) {
+        if (nullable) return M1MOE_OK;
+        return fail(M1MOE_ERR_INVALID, "%s is null", what);
+    }
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+        return fail(M1MOE_ERR_INVALID, "%s must be 16-byte aligned", what);
+    return M1MOE_OK;
+}
+
+int32_t check_dtype(int32_t dt) {
+    if (dt != M1MOE_F32 && dt != M1MOE_BF16)
+        return fail(M1MOE_ERR_INVALID, "x_dtype %d is not M1MOE_F32 or M1MOE_BF16", dt);
+    return M1MOE_OK;
+}
+
+int32_t launched(int rc, const char* what) {
+    if (rc != (int)hipSuccess)
+        return fail(M1MOE_ERR_HIP, "launch of %s failed: %s", what,
+                    hipGetErrorString((hipError_t)rc));
+    return M1MOE_OK;
+}
+
+m1moe::DecodeArgs decode_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32_t x_dtype,
+                              const int32_t* idx, const float* w, const float* residual,
+                              float* out) {
+    const m1moe::Geom& g = ctx->g;
+    m1moe::DecodeArgs a{};
+    a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
+    a.expert_bytes = g.expert_bytes;
+    a.h = g.h;
+    a.E = g.E;
+    a.K = g.K;
+    a.I = g.I;
+    a.gs = g.gs;
+    a.x = x;
+    a.x_bf16 = (x_dtype == M1MOE_BF16);
+    a.topk_idx = idx;
+    a.topk_w = w;
+    a.residual = residual;
+    a.out = out;
+    a.act = ctx->act;
+    a.err = ctx->err;
+    a.gate = {g.off[0], g.off[1], g.off[2], g.I, g.h};
+    a.up = {g.off[3], g.off[4], g.off[5], g.I, g.h};
+    a.down = {g.off[6], g.off[7], g.off[8], g.h, g.I};
+    return a;
+}
+
+int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
+                       int32_t x_dtype, int32_t* uidx, float* uw, float* ulogits) {
+    const m1moe::Geom& g = ctx->g;
+    m1moe::RouterArgs r{};
+    r.router = ctx->routers + (uint64_t)layer * g.E * g.h;
+    r.bias = ctx->has_bias[layer] ? ctx->biases + (uint64_t)layer * g.E : nullptr;
+    r.x = x;
+    r.x_bf16 = (x_dtype == M1MOE_BF16);
+    r.T = T;
+    r.E = g.E;
+    r.h = g.h;
+    r.K = g.K;
+    r.norm = g.norm;
+    r.logits = ctx->logits;
+    r.idx = ctx->topk_idx;
+    r.w = ctx->topk_w;
+    r.user_idx = uidx;
+    r.user_w = uw;
+    r.user_logits = ulogits;
+    r.counters = ctx->counters;
+    return launched(m1moe::launch_router_topk(r, ctx->stream), "router_topk");
+}
+
+int32_t require_loaded(m1moe_ctx_t ctx, int32_t layer, bool router) {
+    if (!ctx->layer_loaded[layer])
+        return fail(M1MOE_ERR_INVALID, "layer %d experts were never uploaded", layer);
+    if (router && !ctx->router_loaded[layer])
+        return fail(M1MOE_ERR_INVALID, "layer %d router was never uploaded", layer);
+    return M1MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t m1moe_abi_version(void) { return M1MOE_ABI_VERSION; }
+
+const char* m1moe_last_error(void) { return m1moe::g_last_error.c_str(); }
+
+int32_t m1moe_check_shape(const m1moe_moe_shape* s) {
+    if (!s) return fail(M1MOE_ERR_INVALID, "null shape");
+    if (s->hidden <= 0 || s->hidden % 64 || s->hidden > 16384)
+        return fail(M1MOE_ERR_INVALID, "hidden=%d must be a positive multiple of 64, <= 16384",
+                    s->hidden);
+    if (s->intermediate <= 0 || s->intermediate % 64 || s->intermediate > 16384)
+        return fail(M1MOE_ERR_INVALID,
+                    "intermediate=%d must be a positive multiple of 64, <= 16384",
+                    s->intermediate);
+    if (s->group_size != 32 && s->group_size != 64 && s->group_size != 128)
+        return fail(M1MOE_ERR_INVALID, "group_size=%d must be 32, 64 or 128", s->group_size);
+    if (s->hidden % s->group_size || s->intermediate % s->group_size)
+        return fail(M1MOE_ERR_INVALID, "group_size=%d must divide hidden=%d and intermediate=%d",
+                    s->group_size, s->hidden, s->intermediate);
+    if (s->num_experts < 1 || s->num_experts > 256)
+        return fail(M1MOE_ERR_INVALID, "num_experts=%d must be in [1, 256]", s->num_experts);
+    if (s->top_k < 1 || s->top_k > s->num_experts || s->top_k > 32)
+        return fail(M1MOE_ERR_INVALID, "top_k=%d must be in [1, min(num_experts, 32)]",
+                    s->top_k);
+    if (s->num_layers < 1)
+        return fail(M1MOE_ERR_INVALID, "num_layers=%d must be >= 1", s->num_layers);
+    if (s->norm_topk_prob != 0 && s->norm_topk_prob != 1)
+        return fail(M1MOE_ERR_INVALID, "norm_topk_prob=%d must be 0 or 1", s->norm_topk_prob);
+    return M1MOE_OK;
+}
+
+int32_t m1moe_expert_bytes(const m1moe_moe_shape* s, uint64_t* out) {
+    int32_t rc = m1moe_check_shape(s);
+    if (rc) return rc;
+    if (!out) return fail(M1MOE_ERR_INVALID, "null output");
+    *out = m1moe::make_geom(*s).expert_bytes;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_expert_offsets(const m1moe_moe_shape* s, uint64_t out[9]) {
+    int32_t rc = m1moe_check_shape(s);
+    if (rc) return rc;
+    if (!out) return fail(M1MOE_ERR_INVALID, "null output");
+    const m1moe::Geom g = m1moe::make_geom(*s);
+    for (int k = 0; k < 9; ++k) out[k] = g.off[k];
+    return M1MOE_OK;
+}
+
+void m1moe_destroy(m1moe_ctx_t ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (void* p : ctx->allocs) (void)hipFree(p);
+    void* owned[] = {ctx->arena,  ctx->routers,  ctx->biases,   ctx->logits, ctx->topk_idx,
+                     ctx->topk_w, ctx->counters, ctx->act, ctx->err};
+    for (void* p : owned)
+        if (p) (void)hipFree(p);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out) {
+    if (!out) return fail(M1MOE_ERR_INVALID, "null output handle");
+    *out = nullptr;
+    int32_t rc = m1moe_check_shape(s);
+    if (rc) return rc;
+    int ndev = 0;
+    HIP_TRY(hipGetDeviceCount(&ndev));
+    if (device < 0 || device >= ndev)
+        return fail(M1MOE_ERR_INVALID, "device %d out of range [0, %d)", device, ndev);
+    m1moe_ctx* c = new (std::nothrow) m1moe_ctx();
+    if (!c) return fail(M1MOE_ERR_OOM, "host allocation failed");
+    c->device = device;
+    c->shape = *s;
+    c->g = m1moe::make_geom(*s);
+    c->has_bias.assign(s->num_layers, false);
+    c->layer_loaded.assign(s->num_layers, false);
+    c->router_loaded.assign(s->num_layers, false);
+    const m1moe::Geom& g = c->g;
+    const uint64_t L = (uint64_t)s->num_layers, E = (uint64_t)g.E;
+    auto cleanup = [&](int32_t code) {
+        m1moe_destroy(c);
+        return code;
+    };
+    if (hipSetDevice(device) != hipSuccess) return cleanup(fail(M1MOE_ERR_HIP, "hipSetDevice"));
+    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess)
+        return cleanup(fail(M1MOE_ERR_HIP, "hipStreamCreate failed"));
+    c->stream = c->own_stream;
+    const uint64_t cap = m1moe::kPrefillCap;
+    if ((rc = device_alloc((void**)&c->arena, L * E * g.expert_bytes, "expert arena")) ||
+        (rc = device_alloc((void**)&c->routers, L * E * g.h * 2, "routers")) ||
+        (rc = device_alloc((void**)&c->biases, L * E * 4, "logit biases")) ||
+        (rc = device_alloc((void**)&c->logits, cap * E * 4, "logits")) ||
+        (rc = device_alloc((void**)&c->topk_idx, cap * g.K * 4, "topk idx")) ||
+        (rc = device_alloc((void**)&c->topk_w, cap * g.K * 4, "topk w")) ||
+        (rc = device_alloc((void**)&c->counters, cap * 4, "counters")) ||
+        (rc = device_alloc((void**)&c->act, (uint64_t)g.K * g.I * 4, "act")) ||
+        (rc = device_alloc((void**)&c->err, 4, "error flag")))
+        return cleanup(rc);
+    if (hipMemset(c->counters, 0, cap * 4) != hipSuccess ||
+        hipMemset(c->err, 0, 4) != hipSuccess || hipMemset(c->biases, 0, L * E * 4) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess)
+        return cleanup(fail(M1MOE_ERR_HIP, "scratch initialisation failed"));
+    *out = c;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_upload_layer_experts(m1moe_ctx_t ctx, int32_t layer, const void* host_image,
+                                   uint64_t bytes) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if (!host_image) return fail(M1MOE_ERR_INVALID, "null layer image");
+    const uint64_t want = (uint64_t)ctx->g.E * ctx->g.expert_bytes;
+    if (bytes != want)
+        return fail(M1MOE_ERR_INVALID,
+                    "layer %d image is %llu bytes; num_experts * expert_bytes = %llu", layer,
+                    (unsigned long long)bytes, (unsigned long long)want);
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->arena + (uint64_t)layer * want, host_image, bytes,
+                           hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    ctx->layer_loaded[layer] = true;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_upload_router(m1moe_ctx_t ctx, int32_t layer, const uint16_t* host_router,
+                            uint64_t count) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if (!host_router) return fail(M1MOE_ERR_INVALID, "null router");
+    const uint64_t want = (uint64_t)ctx->g.E * ctx->g.h;
+    if (count != want)
+        return fail(M1MOE_ERR_INVALID, "router count %llu != num_experts * hidden = %llu",
+                    (unsigned long long)count, (unsigned long long)want);
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->routers + (uint64_t)layer * want, host_router, want * 2,
+                           hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    ctx->router_loaded[layer] = true;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_set_logit_bias(m1moe_ctx_t ctx, int32_t layer, const float* host_bias,
+                             int32_t count) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if (!host_bias) {
+        ctx->has_bias[layer] = false;
+        return M1MOE_OK;
+    }
+    if (count != ctx->g.E)
+        return fail(M1MOE_ERR_INVALID, "bias count %d != num_experts %d", count, ctx->g.E);
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->biases + (uint64_t)layer * ctx->g.E, host_bias,
+                           (uint64_t)count * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    ctx->has_bias[layer] = true;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_expert_block(m1moe_ctx_t ctx, int32_t layer, int32_t expert, void** dev_ptr) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if (expert < 0 || expert >= ctx->g.E)
+        return fail(M1MOE_ERR_INVALID, "expert %d out of range [0, %d)", expert, ctx->g.E);
+    if (!dev_ptr) return fail(M1MOE_ERR_INVALID, "null output");
+    *dev_ptr = ctx->arena + ((uint64_t)layer * ctx->g.E + (uint64_t)expert) * ctx->g.expert_bytes;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_alloc(m1moe_ctx_t ctx, uint64_t bytes, void** dev_ptr) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!dev_ptr) return fail(M1MOE_ERR_INVALID, "null output");
+    if ((rc = set_device(ctx))) return rc;
+    if ((rc = device_alloc(dev_ptr, bytes, "m1moe_alloc"))) return rc;
+    ctx->allocs.insert(*dev_ptr);
+    return M1MOE_OK;
+}
+
+int32_t m1moe_free(m1moe_ctx_t ctx, void* dev_ptr) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!dev_ptr) return M1MOE_OK;
+    auto it = ctx->allocs.find(dev_ptr);
+    if (it == ctx->allocs.end())
+        return fail(M1MOE_ERR_INVALID, "pointer was not allocated by m1moe_alloc on this context");
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(dev_ptr));
+    ctx->allocs.erase(it);
+    return M1MOE_OK;
+}
+
+static int32_t copy_common(m1moe_ctx_t ctx, void* dst, const void* src, uint64_t bytes,
+                           hipMemcpyKind kind) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (bytes == 0) return M1MOE_OK;
+    if (!dst || !src) return fail(M1MOE_ERR_INVALID, "null copy pointer");
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return M1MOE_OK;
+}
+
+int32_t m1moe_copy_h2d(m1moe_ctx_t ctx, void* d, const void* h, uint64_t n) {
+    return copy_common(ctx, d, h, n, hipMemcpyHostToDevice);
+}
+int32_t m1moe_copy_d2h(m1moe_ctx_t ctx, void* h, const void* d, uint64_t n) {
+    return copy_common(ctx, h, d, n, hipMemcpyDeviceToHost);
+}
+int32_t m1moe_copy_d2d(m1moe_ctx_t ctx, void* d, const void* s, uint64_t n) {
+    return copy_common(ctx, d, s, n, hipMemcpyDeviceToDevice);
+}
+
+int32_t m1moe_set_stream(m1moe_ctx_t ctx, void* hip_stream) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_get_stream(m1moe_ctx_t ctx, void** hip_stream) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!hip_stream) return fail(M1MOE_ERR_INVALID, "null output");
+    *hip_stream = ctx->stream;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_sync(m1moe_ctx_t ctx) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = set_device(ctx))) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    uint32_t flag = 0;
+    HIP_TRY(hipMemcpy(&flag, ctx->err, 4, hipMemcpyDeviceToHost));
+    if (flag) {
+        HIP_TRY(hipMemset(ctx->err, 0, 4));
+        HIP_TRY(hipDeviceSynchronize());
+        return fail(M1MOE_ERR_DEVICE,
+                    "a kernel saw an expert index outside [0, %d) (device flag 0x%x)", ctx->g.E,
+                    flag);
+    }
+    return M1MOE_OK;
+}
+
+int32_t m1moe_event_create(m1moe_ctx_t ctx, m1moe_event_t* out) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = set_device(ctx))) return rc;
+    if (!out) return fail(M1MOE_ERR_INVALID, "null output");
+    m1moe_event* e = new (std::nothrow) m1moe_event();
+    if (!e) return fail(M1MOE_ERR_OOM, "host allocation failed");
+    if (hipEventCreate(&e->ev) != hipSuccess) {
+        delete e;
+        return fail(M1MOE_ERR_HIP, "hipEventCreate failed");
+    }
+    *out = e;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_event_record(m1moe_ctx_t ctx, m1moe_event_t ev) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!ev) return fail(M1MOE_ERR_INVALID, "null event");
+    HIP_TRY(hipEventRecord(ev->ev, ctx->stream));
+    return M1MOE_OK;
+}
+
+int32_t m1moe_event_elapsed_ms(m1moe_event_t start, m1moe_event_t end, float* ms) {
+    if (!start || !end || !ms) return fail(M1MOE_ERR_INVALID, "null argument");
+    HIP_TRY(hipEventSynchronize(end->ev));
+    HIP_TRY(hipEventElapsedTime(ms, start->ev, end->ev));
+    return M1MOE_OK;
+}
+
+void m1moe_event_destroy(m1moe_event_t ev) {
+    if (!ev) return;
+    (void)hipEventDestroy(ev->ev);
+    delete ev;
+}
+
+int32_t m1moe_graph_begin(m1moe_ctx_t ctx) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = set_device(ctx))) return rc;
+    HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return M1MOE_OK;
+}
+
+int32_t m1moe_graph_end(m1moe_ctx_t ctx, m1moe_graph_t* out) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!out) return fail(M1MOE_ERR_INVALID, "null output");
+    m1moe_graph* gr = new (std::nothrow) m1moe_graph();
+    if (!gr) return fail(M1MOE_ERR_OOM, "host allocation failed");
+    hipError_t e = hipStreamEndCapture(ctx->stream, &gr->graph);
+    if (e != hipSuccess) {
+        delete gr;
+        return fail(M1MOE_ERR_HIP, "hipStreamEndCapture failed: %s", hipGetErrorString(e));
+    }
+    e = hipGraphInstantiate(&gr->exec, gr->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(gr->graph);
+        delete gr;
+        return fail(M1MOE_ERR_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+    }
+    *out = gr;
+    return M1MOE_OK;
+}
+
+int32_t m1moe_graph_launch(m1moe_ctx_t ctx, m1moe_graph_t graph) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx))) return rc;
+    if (!graph) return fail(M1MOE_ERR_INVALID, "null graph");
+    HIP_TRY(hipGraphLaunch(graph->exec, ctx->stream));
+    return M1MOE_OK;
+}
+
+void m1moe_graph_destroy(m1moe_graph_t graph) {
+    if (!graph) return;
+    (void)hipGraphExecDestroy(graph->exec);
+    (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
+int32_t m1moe_router_topk(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_x,
+                          int32_t x_dtype, int32_t* d_topk_idx, float* d_topk_w,
+                          float* d_logits) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if (T < 1 || T > m1moe::kPrefillCap)
+        return fail(M1MOE_ERR_INVALID, "T=%d must be in [1, %d]", T, m1moe::kPrefillCap);
+    if ((rc = check_dtype(x_dtype)) || (rc = check_dev_ptr(d_x, "d_x", false)) ||
+        (rc = check_dev_ptr(d_topk_idx, "d_topk_idx", false)) ||
+        (rc = check_dev_ptr(d_topk_w, "d_topk_w", false)) ||
+        (rc = check_dev_ptr(d_logits, "d_logits", true)))
+        return rc;
+    if (!ctx->router_loaded[layer])
+        return fail(M1MOE_ERR_INVALID, "layer %d router was never uploaded", layer);
+    if ((rc = set_device(ctx))) return rc;
+    return enqueue_router(ctx, layer, T, d_x, x_dtype, d_topk_idx, d_topk_w, d_logits);
+}
+
+int32_t m1moe_moe_decode_given_topk(m1moe_ctx_t ctx, int32_t layer, const void* d_x,
+                                    int32_t x_dtype, const int32_t* d_topk_idx,
+                                    const float* d_topk_w, const float* d_residual,
+                                    float* d_out) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if ((rc = check_dtype(x_dtype)) || (rc = check_dev_ptr(d_x, "d_x", false)) ||
+        (rc = check_dev_ptr(d_topk_idx, "d_topk_idx", false)) ||
+        (rc = check_dev_ptr(d_topk_w, "d_topk_w", false)) ||
+        (rc = check_dev_ptr(d_residual, "d_residual", true)) ||
+        (rc = check_dev_ptr(d_out, "d_out", false)))
+        return rc;
+    if ((rc = require_loaded(ctx, layer, false))) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    const m1moe::DecodeArgs a =
+        decode_args(ctx, layer, d_x, x_dtype, d_topk_idx, d_topk_w, d_residual, d_out);
+    if ((rc = launched(m1moe::launch_decode_gate_up(a, ctx->stream), "decode gate/up"))) return rc;
+    return launched(m1moe::launch_decode_down_combine(a, ctx->stream), "decode down/combine");
+}
+
+int32_t m1moe_moe_decode(m1moe_ctx_t ctx, int32_t layer, const void* d_x, int32_t x_dtype,
+                         const float* d_residual, float* d_out, int32_t* d_topk_idx,
+                         float* d_topk_w) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if ((rc = check_dtype(x_dtype)) || (rc = check_dev_ptr(d_x, "d_x", false)) ||
+        (rc = check_dev_ptr(d_residual, "d_residual", true)) ||
+        (rc = check_dev_ptr(d_out, "d_out", false)) ||
+        (rc = check_dev_ptr(d_topk_idx, "d_topk_idx", true)) ||
+        (rc = check_dev_ptr(d_topk_w, "d_topk_w", true)))
+        return rc;
+    if ((rc = require_loaded(ctx, layer, true))) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    if ((rc = enqueue_router(ctx, layer, 1, d_x, x_dtype, d_topk_idx, d_topk_w, nullptr)))
+        return rc;
+    const m1moe::DecodeArgs a =
+        decode_args(ctx, layer, d_x, x_dtype, ctx->topk_idx, ctx->topk_w, d_residual, d_out);
+    if ((rc = launched(m1moe::launch_decode_gate_up(a, ctx->stream), "decode gate/up"))) return rc;
+    return launched(m1moe::launch_decode_down_combine(a, ctx->stream), "decode down/combine");
+}
+
+int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_x,
+                          int32_t x_dtype, const float* d_residual, float* d_out,
+                          int32_t* d_topk_idx, float* d_topk_w) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    (void)T;
+    (void)d_x;
+    (void)x_dtype;
+    (void)d_residual;
+    (void)d_out;
+    (void)d_topk_idx;
+    (void)d_topk_w;
+    return fail(M1MOE_ERR_INVALID, "m1moe_moe_prefill is not built yet");
+}
+
+int32_t m1moe_dequant_debug(m1moe_ctx_t ctx, int32_t layer, int32_t expert, int32_t proj,
+                            float* d_out) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if (expert < 0 || expert >= ctx->g.E)
+        return fail(M1MOE_ERR_INVALID, "expert %d out of range [0, %d)", expert, ctx->g.E);
+    if (proj < 0 || proj > 2) return fail(M1MOE_ERR_INVALID, "proj %d must be 0, 1 or 2", proj);
+    if ((rc = check_dev_ptr(d_out, "d_out", false))) return rc;
+    if ((rc = require_loaded(ctx, layer, false))) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    const m1moe::Geom& g = ctx->g;
+    const uint8_t* blk = ctx->arena + ((uint64_t)layer * g.E + (uint64_t)expert) * g.expert_bytes;
+    const m1moe::ProjView p = {g.off[3 * proj], g.off[3 * proj + 1], g.off[3 * proj + 2],
+                               g.rows(proj), g.cols(proj)};
+    return launched(m1moe::launch_dequant(blk, p, g.gs, d_out, ctx->stream), "dequant");
+}
+
+}  // extern "C"

@@ -1,0 +1,138 @@
+"""Seeded synthetic workloads of the benchmark configurations.
+
+All tensors come from the library's counter-based generator
+(m1moe_synth_*), so the same (seed, tensor id, index) gives the same value
+on every machine and any slice can be regenerated on its own.
+
+Distributions (2, 3):
+  expert nibbles  uniform 0..15, 8 per u32 (reference packing)
+  expert scales   bf16 |N(0, 0.02)|
+  expert biases   bf16 N(0, 0.01)
+  router          bf16 N(0, 0.02)   [E x h]
+  x               bf16 N(0, 1)      [T x h]
+  residual        f32  N(0, 1)      [T x h]
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from ._lib import MoEShape, check
+from .engine import expert_bytes, make_shape
+
+SCALE_SIGMA = 0.02
+BIAS_SIGMA = 0.01
+ROUTER_SIGMA = 0.02
+
+# tensor-id namespaces of the non-expert tensors
+_TID_ROUTER = 2 << 56
+_TID_X = 3 << 56
+_TID_RESIDUAL = 4 << 56
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    shape_kwargs: dict
+    T: int = 1             # tokens per call (1 = decode)
+    zipf_s: float = 0.0    # router logit bias for a Zipf(s) expert load; 0 = none
+    description: str = ""
+
+    def shape(self, num_layers: int = 1) -> MoEShape:
+        return make_shape(num_layers=num_layers, **self.shape_kwargs)
+
+
+CONFIGS = {
+    "cfg0": Workload("cfg0", dict(hidden=2048, num_experts=64, top_k=8, intermediate=1024,
+                                  group_size=64, norm_topk_prob=False),
+                     description="OLMoE-shaped MoE layer, batch-1 decode (h2048 E64 top-8 I1024)"),
+    "cfg2": Workload("cfg2", dict(hidden=4096, num_experts=8, top_k=2, intermediate=14336,
+                                  group_size=64, norm_topk_prob=True),
+                     description="Mixtral-shaped MoE layer, batch-1 decode (h4096 E8 top-2 "
+                                 "renorm I14336)"),
+    "cfg3": Workload("cfg3", dict(hidden=2048, num_experts=64, top_k=8, intermediate=1024,
+                                  group_size=64, norm_topk_prob=False),
+                     T=512, zipf_s=1.1,
+                     description="OLMoE-shaped MoE layer prefill, 512 tokens, Zipf(1.1) loads"),
+    # small shapes for tests
+    "tiny": Workload("tiny", dict(hidden=128, num_experts=8, top_k=2, intermediate=64,
+                                  group_size=64, norm_topk_prob=False)),
+    "tiny_renorm": Workload("tiny_renorm", dict(hidden=256, num_experts=16, top_k=4,
+                                                intermediate=128, group_size=32,
+                                                norm_topk_prob=True)),
+}
+
+
+def _threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def layer_image(shape: MoEShape, seed: int, layer: int) -> np.ndarray:
+    """One layer_NN.bin image (E expert blocks) as uint8."""
+    nbytes = shape.num_experts * expert_bytes(shape)
+    out = np.empty(nbytes, dtype=np.uint8)
+    check(_lib.load().m1moe_synth_layer_image(
+        ctypes.byref(shape), ctypes.c_uint64(seed), int(layer), ctypes.c_float(SCALE_SIGMA),
+        ctypes.c_float(BIAS_SIGMA), ctypes.c_void_p(out.ctypes.data), ctypes.c_uint64(nbytes),
+        _threads()), "m1moe_synth_layer_image")
+    return out
+
+
+def normal_bf16(seed: int, tensor_id: int, n: int, sigma: float, absval: bool = False) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    check(_lib.load().m1moe_synth_normal_bf16(ctypes.c_uint64(seed), ctypes.c_uint64(tensor_id),
+                                              ctypes.c_uint64(n), ctypes.c_float(sigma),
+                                              1 if absval else 0, ctypes.c_void_p(out.ctypes.data)),
+          "m1moe_synth_normal_bf16")
+    return out
+
+
+def normal_f32(seed: int, tensor_id: int, n: int, sigma: float) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    check(_lib.load().m1moe_synth_normal_f32(ctypes.c_uint64(seed), ctypes.c_uint64(tensor_id),
+                                             ctypes.c_uint64(n), ctypes.c_float(sigma),
+                                             ctypes.c_void_p(out.ctypes.data)),
+          "m1moe_synth_normal_f32")
+    return out
+
+
+def router(shape: MoEShape, seed: int, layer: int) -> np.ndarray:
+    """bf16 router [E x h] as uint16."""
+    n = shape.num_experts * shape.hidden
+    return normal_bf16(seed, _TID_ROUTER | layer, n, ROUTER_SIGMA).reshape(shape.num_experts,
+                                                                           shape.hidden)
+
+
+def activations_bf16(shape: MoEShape, seed: int, T: int, stream: int = 0) -> np.ndarray:
+    """x bf16 N(0,1) [T x h] as uint16."""
+    return normal_bf16(seed, _TID_X | stream, T * shape.hidden, 1.0).reshape(T, shape.hidden)
+
+
+def residual_f32(shape: MoEShape, seed: int, T: int, stream: int = 0) -> np.ndarray:
+    return normal_f32(seed, _TID_RESIDUAL | stream, T * shape.hidden, 1.0).reshape(T, shape.hidden)
+
+
+def zipf_logit_bias(num_experts: int, s: float) -> Optional[np.ndarray]:
+    """Per-expert logit bias -s*ln(rank) (rank = expert index + 1): with the
+    router's own logits added, expert loads follow roughly a Zipf(s) law."""
+    if s <= 0:
+        return None
+    ranks = np.arange(1, num_experts + 1, dtype=np.float64)
+    return (-s * np.log(ranks)).astype(np.float32)
+
+
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    """Exact bf16 (uint16 bits) -> f32."""
+    return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(a: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even f32 -> bf16 bits (scripts/extract_olmoe.py:104-111)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = u + 0x7FFF + ((u >> 16) & 1)
+    return (u >> 16).astype(np.uint16)

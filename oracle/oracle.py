@@ -1,0 +1,231 @@
+"""ctypes wrapper of the scalar CPU oracle (oracle/liboracle_m1moe.so).
+
+TEST INFRASTRUCTURE ONLY: the checker the HIP path is compared against.
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may
+import this module.  The reference arithmetic it restates is cited per
+function in m1moe_oracle.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from ctypes import POINTER, c_float, c_int32, c_uint16, c_uint32, c_uint8
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle_m1moe.so")
+
+KEY_LOGIT = 0
+KEY_PROB = 1
+
+
+class OrcShape(ctypes.Structure):
+    _fields_ = [("hidden", c_int32), ("num_experts", c_int32), ("top_k", c_int32),
+                ("intermediate", c_int32), ("group_size", c_int32), ("norm_topk_prob", c_int32)]
+
+
+class OrcOffsets(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in
+                ("gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s",
+                 "down_b", "expert_bytes")]
+
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-B", "-C", HERE], check=True, stdout=subprocess.DEVNULL)
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = ctypes.CDLL(LIB_PATH)
+    P = ctypes.c_void_p
+    sig = {
+        "orc_bf16_to_f32": (c_float, [c_uint16]),
+        "orc_expert_offsets": (None, [POINTER(OrcShape), POINTER(OrcOffsets)]),
+        "orc_dequant_proj": (None, [POINTER(OrcShape), P, c_int32, P]),
+        "orc_matvec4bit": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
+        "orc_matvec4bit_f64": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
+        "orc_swiglu": (None, [P, P, P, c_int32]),
+        "orc_router_logits": (None, [P, P, c_int32, c_int32, P]),
+        "orc_router_logits_seq_f32": (None, [P, P, c_int32, c_int32, P]),
+        "orc_softmax": (None, [P, c_int32, P]),
+        "orc_select_topk": (None, [P, P, c_int32, c_int32, c_int32, c_int32, P, P]),
+        "orc_combine": (None, [P, P, P, P, c_int32, c_int32]),
+        "orc_expert_forward": (None, [POINTER(OrcShape), P, P, P]),
+        "orc_moe_decode": (c_int32, [POINTER(OrcShape), P, P, P, P, P, P, P, P, P]),
+        "orc_moe_decode_given_topk": (c_int32, [POINTER(OrcShape), P, P, P, P, P, P]),
+        "orc_moe_prefill": (c_int32, [POINTER(OrcShape), P, P, P, c_int32, P, P, P, P, P,
+                                      c_int32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _p(a):
+    if a is None:
+        return None
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("oracle inputs must be C-contiguous")
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def shape(hidden, num_experts, top_k, intermediate, group_size=64, norm_topk_prob=False):
+    return OrcShape(hidden, num_experts, top_k, intermediate, group_size,
+                    1 if norm_topk_prob else 0)
+
+
+def from_moe_shape(s) -> OrcShape:
+    """From an m1moe_amd MoEShape (or anything with the same field names)."""
+    return OrcShape(s.hidden, s.num_experts, s.top_k, s.intermediate, s.group_size,
+                    s.norm_topk_prob)
+
+
+def offsets(s: OrcShape) -> OrcOffsets:
+    o = OrcOffsets()
+    load().orc_expert_offsets(ctypes.byref(s), ctypes.byref(o))
+    return o
+
+
+def dequant_proj(s: OrcShape, block: np.ndarray, proj: int) -> np.ndarray:
+    rows = s.hidden if proj == 2 else s.intermediate
+    cols = s.intermediate if proj == 2 else s.hidden
+    out = np.empty((rows, cols), dtype=np.float32)
+    load().orc_dequant_proj(ctypes.byref(s), _p(block), proj, _p(out))
+    return out
+
+
+def matvec4bit(w, sc, bi, x, out_dim, in_dim, gs) -> np.ndarray:
+    y = np.empty(out_dim, dtype=np.float32)
+    load().orc_matvec4bit(_p(w), _p(sc), _p(bi), _p(np.ascontiguousarray(x, np.float32)), _p(y),
+                          out_dim, in_dim, gs)
+    return y
+
+
+def matvec4bit_f64(w, sc, bi, x, out_dim, in_dim, gs) -> np.ndarray:
+    y = np.empty(out_dim, dtype=np.float64)
+    load().orc_matvec4bit_f64(_p(w), _p(sc), _p(bi), _p(np.ascontiguousarray(x, np.float32)),
+                              _p(y), out_dim, in_dim, gs)
+    return y
+
+
+def swiglu(g, u) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    out = np.empty_like(g)
+    load().orc_swiglu(_p(g), _p(u), _p(out), g.size)
+    return out
+
+
+def router_logits(router_bf16, x, seq_f32=False) -> np.ndarray:
+    r = np.ascontiguousarray(router_bf16, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    E, h = r.shape
+    out = np.empty(E, dtype=np.float32)
+    fn = load().orc_router_logits_seq_f32 if seq_f32 else load().orc_router_logits
+    fn(_p(r), _p(x), E, h, _p(out))
+    return out
+
+
+def softmax(logits) -> np.ndarray:
+    lg = np.ascontiguousarray(logits, np.float32)
+    out = np.empty_like(lg)
+    load().orc_softmax(_p(lg), lg.size, _p(out))
+    return out
+
+
+def select_topk(logits, probs, k, norm, key_mode=KEY_LOGIT):
+    lg = np.ascontiguousarray(logits, np.float32)
+    pr = np.ascontiguousarray(probs, np.float32)
+    idx = np.empty(k, dtype=np.int32)
+    w = np.empty(k, dtype=np.float32)
+    load().orc_select_topk(_p(lg), _p(pr), lg.size, k, 1 if norm else 0, key_mode, _p(idx), _p(w))
+    return idx, w
+
+
+def combine(expert_outs, w, residual) -> np.ndarray:
+    eo = np.ascontiguousarray(expert_outs, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    K, h = eo.shape
+    out = np.empty(h, dtype=np.float32)
+    res = None if residual is None else np.ascontiguousarray(residual, np.float32)
+    load().orc_combine(_p(eo), _p(w), _p(res), _p(out), K, h)
+    return out
+
+
+def expert_forward(s: OrcShape, block: np.ndarray, x) -> np.ndarray:
+    out = np.empty(s.hidden, dtype=np.float32)
+    load().orc_expert_forward(ctypes.byref(s), _p(block), _p(np.ascontiguousarray(x, np.float32)),
+                              _p(out))
+    return out
+
+
+def moe_decode(s: OrcShape, image, router_bf16, x, residual=None, logit_bias=None):
+    """Returns (out [h], idx [K], w [K], logits [E])."""
+    out = np.empty(s.hidden, dtype=np.float32)
+    idx = np.empty(s.top_k, dtype=np.int32)
+    w = np.empty(s.top_k, dtype=np.float32)
+    lg = np.empty(s.num_experts, dtype=np.float32)
+    r = np.ascontiguousarray(router_bf16, np.uint16)
+    res = None if residual is None else np.ascontiguousarray(residual, np.float32)
+    bias = None if logit_bias is None else np.ascontiguousarray(logit_bias, np.float32)
+    rc = load().orc_moe_decode(ctypes.byref(s), _p(image), _p(r), _p(bias),
+                               _p(np.ascontiguousarray(x, np.float32)), _p(res), _p(out), _p(idx),
+                               _p(w), _p(lg))
+    if rc:
+        raise ValueError(f"orc_moe_decode returned {rc}")
+    return out, idx, w, lg
+
+
+def moe_decode_given_topk(s: OrcShape, image, x, idx, w, residual=None) -> np.ndarray:
+    out = np.empty(s.hidden, dtype=np.float32)
+    res = None if residual is None else np.ascontiguousarray(residual, np.float32)
+    rc = load().orc_moe_decode_given_topk(ctypes.byref(s), _p(image),
+                                          _p(np.ascontiguousarray(x, np.float32)),
+                                          _p(np.ascontiguousarray(idx, np.int32)),
+                                          _p(np.ascontiguousarray(w, np.float32)), _p(res), _p(out))
+    if rc:
+        raise ValueError(f"orc_moe_decode_given_topk returned {rc}")
+    return out
+
+
+def moe_prefill(s: OrcShape, image, router_bf16, x, residual=None, logit_bias=None, nthreads=1):
+    """x [T x h] f32; returns (out [T x h], idx [T x K], w [T x K])."""
+    x = np.ascontiguousarray(x, np.float32)
+    T = x.shape[0]
+    out = np.empty((T, s.hidden), dtype=np.float32)
+    idx = np.empty((T, s.top_k), dtype=np.int32)
+    w = np.empty((T, s.top_k), dtype=np.float32)
+    r = np.ascontiguousarray(router_bf16, np.uint16)
+    res = None if residual is None else np.ascontiguousarray(residual, np.float32)
+    bias = None if logit_bias is None else np.ascontiguousarray(logit_bias, np.float32)
+    rc = load().orc_moe_prefill(ctypes.byref(s), _p(image), _p(r), _p(bias), T, _p(x), _p(res),
+                                _p(out), _p(idx), _p(w), int(nthreads))
+    if rc:
+        raise ValueError(f"orc_moe_prefill returned {rc}")
+    return out, idx, w
+
+
+def proj_arrays(s: OrcShape, block: np.ndarray, proj: int):
+    """(words u32 [rows, cols/8], scales u16 [rows, groups], biases u16) views of a block."""
+    o = offsets(s)
+    rows = s.hidden if proj == 2 else s.intermediate
+    cols = s.intermediate if proj == 2 else s.hidden
+    base = [(o.gate_w, o.gate_s, o.gate_b), (o.up_w, o.up_s, o.up_b),
+            (o.down_w, o.down_s, o.down_b)][proj]
+    g = cols // s.group_size
+    w = block[base[0]:base[0] + rows * cols // 2].view(np.uint32).reshape(rows, cols // 8)
+    sc = block[base[1]:base[1] + rows * g * 2].view(np.uint16).reshape(rows, g)
+    bi = block[base[2]:base[2] + rows * g * 2].view(np.uint16).reshape(rows, g)
+    return w, sc, bi

@@ -1,0 +1,69 @@
+"""Shared set-up of seeded MoE-layer cases for the GPU parity tests."""
+from __future__ import annotations
+
+import sys
+from dataclasses import dataclass, field
+
+import numpy as np
+
+import m1moe_amd as m
+from m1moe_amd import synth
+from oracle import oracle as orc
+
+REL_L2_TOL = 1e-2  # layer outputs vs the oracle
+
+
+def rel_l2(got, want) -> float:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-300))
+
+
+def say(msg: str) -> None:
+    """Names the case before a GPU step (flushed, in case the step never returns)."""
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@dataclass
+class Case:
+    name: str
+    shape: m.MoEShape
+    seed: int
+    ctx: m.HIPContext
+    images: list
+    routers: list
+    biases: list = field(default_factory=list)
+
+    @property
+    def oshape(self):
+        return orc.from_moe_shape(self.shape)
+
+    def x_bf16(self, T: int, stream: int = 0) -> np.ndarray:
+        return synth.activations_bf16(self.shape, self.seed, T, stream)
+
+    def residual(self, T: int, stream: int = 0) -> np.ndarray:
+        return synth.residual_f32(self.shape, self.seed, T, stream)
+
+    def close(self):
+        self.ctx.close()
+
+
+def make_case(name: str, seed: int = 1234, num_layers: int = 1, router_override=None,
+              bias=None) -> Case:
+    wl = synth.CONFIGS[name]
+    shape = wl.shape(num_layers)
+    say(f"create context {name} seed={seed} layers={num_layers}")
+    ctx = m.HIPContext(shape)
+    images, routers, biases = [], [], []
+    for layer in range(num_layers):
+        img = synth.layer_image(shape, seed, layer)
+        r = synth.router(shape, seed, layer) if router_override is None else router_override
+        ctx.upload_layer_experts(layer, img)
+        ctx.upload_router(layer, r)
+        if bias is not None:
+            ctx.set_logit_bias(layer, bias)
+        images.append(img)
+        routers.append(np.ascontiguousarray(r))
+        biases.append(bias)
+    return Case(name, shape, seed, ctx, images, routers, biases)

@@ -1,0 +1,278 @@
+"""GPU parity of the batch-1 MoE decode path against the CPU oracle.
+
+Bar: dequantised weights and top-K expert
+indices bit-exact, ties to the lower index; layer outputs within 1e-2
+relative L2 of the oracle.  Every call goes through the C ABI.
+"""
+import numpy as np
+import pytest
+
+import m1moe_amd as m
+from m1moe_amd import _lib, synth
+from m1moe_amd.engine import MoEBlock
+from oracle import oracle as orc
+
+from cases import REL_L2_TOL, make_case, rel_l2, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cfg0():
+    c = make_case("cfg0", seed=1234, num_layers=2)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def cfg2():
+    c = make_case("cfg2", seed=99)
+    yield c
+    c.close()
+
+
+# ---- dequant ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["cfg0", "tiny", "tiny_renorm"])
+def test_dequant_bit_exact(name):
+    c = make_case(name, seed=7)
+    try:
+        blk = MoEBlock(c.ctx)
+        s = c.oshape
+        eb = c.ctx.expert_bytes
+        for e in sorted({0, c.shape.num_experts // 2, c.shape.num_experts - 1}):
+            for proj in range(3):
+                say(f"dequant {name} expert={e} proj={proj}")
+                want = orc.dequant_proj(s, c.images[0][e * eb:(e + 1) * eb], proj)
+                buf = c.ctx.alloc(want.nbytes)
+                blk.dequant(0, e, proj, buf)
+                c.ctx.sync()
+                got = buf.download(np.float32).reshape(want.shape)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (e, proj)
+                buf.free()
+    finally:
+        c.close()
+
+
+# ---- router / top-K ----------------------------------------------------------------
+
+def _router_check(c, T, x_dtype="bf16", layer=0):
+    blk = MoEBlock(c.ctx)
+    K, E = c.shape.top_k, c.shape.num_experts
+    xb = c.x_bf16(T, stream=layer + 11)
+    x32 = synth.bf16_to_f32(xb)
+    xin = xb if x_dtype == "bf16" else np.ascontiguousarray(x32)
+    dx = c.ctx.to_device(xin)
+    didx, dw, dl = c.ctx.alloc(T * K * 4), c.ctx.alloc(T * K * 4), c.ctx.alloc(T * E * 4)
+    say(f"router_topk {c.name} T={T} x={x_dtype} layer={layer}")
+    blk.router_topk(layer, T, dx, x_dtype, didx, dw, dl)
+    c.ctx.sync()
+    gi = didx.download(np.int32).reshape(T, K)
+    gw = dw.download(np.float32).reshape(T, K)
+    gl = dl.download(np.float32).reshape(T, E)
+    s = c.oshape
+    for t in range(T):
+        lg = orc.router_logits(c.routers[layer], x32[t])
+        if c.biases[layer] is not None:
+            lg = (lg + c.biases[layer]).astype(np.float32)
+        p = orc.softmax(lg)
+        idx, w = orc.select_topk(lg, p, K, bool(s.norm_topk_prob))
+        assert np.array_equal(gl[t].view(np.uint32), lg.view(np.uint32)), f"logits t={t}"
+        assert np.array_equal(gi[t], idx), f"top-K t={t}: {gi[t]} vs {idx}"
+        assert np.allclose(gw[t], w, rtol=2e-6, atol=1e-9), f"weights t={t}"
+    for b in (dx, didx, dw, dl):
+        b.free()
+
+
+def test_router_topk_cfg0_exact(cfg0):
+    _router_check(cfg0, T=64)
+    _router_check(cfg0, T=8, x_dtype="f32", layer=1)
+
+
+def test_router_topk_cfg2_renorm_exact(cfg2):
+    _router_check(cfg2, T=32)
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_renorm"])
+def test_router_topk_small_exact(name):
+    c = make_case(name, seed=5)
+    try:
+        _router_check(c, T=100)
+    finally:
+        c.close()
+
+
+def test_router_ties_go_to_lower_index():
+    wl = synth.CONFIGS["tiny"]
+    shape = wl.shape()
+    r = synth.router(shape, 3, 0).copy()
+    r[5] = r[1]       # experts 1 and 5 always tie
+    r[7] = r[2]       # experts 2 and 7 always tie
+    r[6] = r[1]
+    c = make_case("tiny", seed=3, router_override=r)
+    try:
+        _router_check(c, T=64)
+    finally:
+        c.close()
+
+
+def test_router_logit_bias():
+    E = synth.CONFIGS["tiny_renorm"].shape().num_experts
+    bias = synth.zipf_logit_bias(E, 1.1)
+    c = make_case("tiny_renorm", seed=8, bias=bias)
+    try:
+        _router_check(c, T=64)
+    finally:
+        c.close()
+
+
+# ---- decode ------------------------------------------------------------------------
+
+def _decode_check(c, tokens, x_dtype="bf16", with_residual=True, given=False, layer=0):
+    blk = MoEBlock(c.ctx)
+    K, h = c.shape.top_k, c.shape.hidden
+    s = c.oshape
+    xb = c.x_bf16(tokens, stream=100 + layer)
+    x32 = synth.bf16_to_f32(xb)
+    res = c.residual(tokens, stream=100 + layer)
+    worst = 0.0
+    out = c.ctx.alloc(h * 4)
+    didx, dw = c.ctx.alloc(K * 4), c.ctx.alloc(K * 4)
+    for t in range(tokens):
+        xin = xb[t] if x_dtype == "bf16" else np.ascontiguousarray(x32[t])
+        dx = c.ctx.to_device(xin)
+        dres = c.ctx.to_device(res[t]) if with_residual else None
+        want, idx, w, _ = orc.moe_decode(s, c.images[layer], c.routers[layer], x32[t],
+                                         res[t] if with_residual else None, c.biases[layer])
+        say(f"decode {c.name} t={t} x={x_dtype} residual={with_residual} given={given}")
+        if given:
+            didx.upload(idx)
+            dw.upload(w)
+            blk.forward_given_topk(layer, dx, x_dtype, didx, dw, dres, out)
+            c.ctx.sync()
+        else:
+            blk.forward(layer, dx, x_dtype, dres, out, didx, dw)
+            c.ctx.sync()
+            assert np.array_equal(didx.download(np.int32), idx)
+            assert np.allclose(dw.download(np.float32), w, rtol=2e-6)
+        got = out.download(np.float32)
+        err = rel_l2(got, want)
+        worst = max(worst, err)
+        assert err <= REL_L2_TOL, f"t={t} rel L2 {err:.3e}"
+        dx.free()
+        if dres is not None:
+            dres.free()
+    print(f"[result] {c.name} decode x={x_dtype} residual={with_residual} given={given}: "
+          f"worst rel L2 {worst:.3e} over {tokens} tokens", flush=True)
+    for b in (out, didx, dw):
+        b.free()
+    return worst
+
+
+def test_decode_given_topk_cfg0(cfg0):
+    _decode_check(cfg0, 3, given=True)
+
+
+def test_decode_cfg0_bf16(cfg0):
+    w = _decode_check(cfg0, 4)
+    assert w < 1e-3   # f16 input rounding gives ~1e-4; anything larger is a bug
+
+
+def test_decode_cfg0_f32_no_residual_layer1(cfg0):
+    _decode_check(cfg0, 2, x_dtype="f32", with_residual=False, layer=1)
+
+
+def test_decode_cfg2(cfg2):
+    w = _decode_check(cfg2, 2)
+    assert w < 1e-3
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_renorm"])
+def test_decode_small(name):
+    c = make_case(name, seed=21)
+    try:
+        _decode_check(c, 8)
+        _decode_check(c, 4, x_dtype="f32", with_residual=False)
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("kw", [
+    dict(hidden=1024, num_experts=16, top_k=4, intermediate=512, group_size=128),
+    dict(hidden=3072, num_experts=32, top_k=6, intermediate=768, group_size=64),
+    dict(hidden=512, num_experts=128, top_k=8, intermediate=192, group_size=32),
+    dict(hidden=64, num_experts=4, top_k=1, intermediate=64, group_size=32),
+])
+def test_decode_ragged_shapes(kw):
+    # lane maps with idle lanes (C not a divisor of 64), several chunks per lane,
+    # gs 32/128, E > 64, K = 1
+    synth.CONFIGS["_ragged"] = synth.Workload("_ragged", dict(kw, norm_topk_prob=False))
+    c = make_case("_ragged", seed=77)
+    try:
+        _decode_check(c, 3)
+    finally:
+        c.close()
+        del synth.CONFIGS["_ragged"]
+
+
+def test_decode_is_deterministic(cfg0):
+    blk = MoEBlock(cfg0.ctx)
+    h = cfg0.shape.hidden
+    dx = cfg0.ctx.to_device(cfg0.x_bf16(1, stream=7)[0])
+    out = cfg0.ctx.alloc(h * 4)
+    runs = []
+    for _ in range(3):
+        say("decode determinism run")
+        blk.forward(0, dx, "bf16", None, out)
+        cfg0.ctx.sync()
+        runs.append(out.download(np.float32))
+    assert all(np.array_equal(runs[0].view(np.uint32), r.view(np.uint32)) for r in runs[1:])
+
+
+def test_bad_expert_index_is_reported_not_read(cfg0):
+    blk = MoEBlock(cfg0.ctx)
+    K, h, E = cfg0.shape.top_k, cfg0.shape.hidden, cfg0.shape.num_experts
+    dx = cfg0.ctx.to_device(cfg0.x_bf16(1)[0])
+    out = cfg0.ctx.alloc(h * 4)
+    idx = np.arange(K, dtype=np.int32)
+    idx[3] = E          # out of range: kernels skip it and raise the device flag
+    didx = cfg0.ctx.to_device(idx)
+    dw = cfg0.ctx.to_device(np.full(K, 0.125, np.float32))
+    say("decode_given_topk with an out-of-range expert index")
+    blk.forward_given_topk(0, dx, "bf16", didx, dw, None, out)
+    with pytest.raises(m.M1MoEError) as ei:
+        cfg0.ctx.sync()
+    assert ei.value.code == _lib.M1MOE_ERR_DEVICE
+    # the flag is cleared and the context keeps working
+    blk.forward(0, dx, "bf16", None, out)
+    cfg0.ctx.sync()
+
+
+def test_graph_replay_matches_eager(cfg0):
+    blk = MoEBlock(cfg0.ctx)
+    h = cfg0.shape.hidden
+    xs = cfg0.x_bf16(2, stream=55)
+    dx = [cfg0.ctx.to_device(xs[i]) for i in range(2)]
+    outs = [cfg0.ctx.alloc(h * 4) for _ in range(2)]
+    eager = []
+    for i in range(2):
+        blk.forward(i, dx[i], "bf16", None, outs[i])
+        cfg0.ctx.sync()
+        eager.append(outs[i].download(np.float32))
+    say("graph capture of two layers")
+    cfg0.ctx.graph_begin()
+    for i in range(2):
+        blk.forward(i, dx[i], "bf16", None, outs[i])
+    g = cfg0.ctx.graph_end()
+    for rep in range(3):
+        for o in outs:
+            o.upload(np.zeros(h, np.float32))
+        say(f"graph replay {rep}")
+        g.launch()
+        cfg0.ctx.sync()
+        for i in range(2):
+            assert np.array_equal(outs[i].download(np.float32).view(np.uint32),
+                                  eager[i].view(np.uint32)), (rep, i)
+        # eager work between replays
+        blk.forward(0, dx[1], "bf16", None, outs[0])
+        cfg0.ctx.sync()

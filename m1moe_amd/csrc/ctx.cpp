@@ -12,7 +12,6 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
-#include <mutex>
 #include <new>
 #include <set>
 #include <string>
@@ -92,6 +91,8 @@ struct m1moe_ctx {
     float* topk_w = nullptr;         // [cap][K]
     uint32_t* counters = nullptr;    // [cap]
     float* act = nullptr;            // [K][I]
+    uint8_t* sync = nullptr;         // decode hand-off state: slots | act_cnt | seen
+    uint64_t sync_bytes = 0, sync_act_cnt = 0, sync_seen = 0;
     uint32_t* err = nullptr;         // sticky device error flag
     std::set<void*> allocs;
 };
@@ -155,29 +156,32 @@ int32_t launched(int rc, const char* what) {
     return M1MOE_OK;
 }
 
-m1moe::DecodeArgs decode_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32_t x_dtype,
-                              const int32_t* idx, const float* w, const float* residual,
-                              float* out) {
+constexpr int32_t kSpinLimit = 1 << 20;  // bounded waits in the decode kernel (~1 s)
+
+m1moe::FusedArgs fused_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32_t x_dtype,
+                            const float* residual, float* out) {
     const m1moe::Geom& g = ctx->g;
-    m1moe::DecodeArgs a{};
+    m1moe::FusedArgs a{};
     a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
     a.expert_bytes = g.expert_bytes;
+    a.router = ctx->routers + (uint64_t)layer * g.E * g.h;
+    a.bias = ctx->has_bias[layer] ? ctx->biases + (uint64_t)layer * g.E : nullptr;
+    a.x = x;
+    a.residual = residual;
+    a.out = out;
+    a.slots = reinterpret_cast<unsigned long long*>(ctx->sync);
+    a.act = ctx->act;
+    a.act_cnt = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_act_cnt);
+    a.seen = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_seen);
+    a.err = ctx->err;
     a.h = g.h;
     a.E = g.E;
     a.K = g.K;
     a.I = g.I;
     a.gs = g.gs;
-    a.x = x;
+    a.norm = g.norm;
     a.x_bf16 = (x_dtype == M1MOE_BF16);
-    a.topk_idx = idx;
-    a.topk_w = w;
-    a.residual = residual;
-    a.out = out;
-    a.act = ctx->act;
-    a.err = ctx->err;
-    a.gate = {g.off[0], g.off[1], g.off[2], g.I, g.h};
-    a.up = {g.off[3], g.off[4], g.off[5], g.I, g.h};
-    a.down = {g.off[6], g.off[7], g.off[8], g.h, g.I};
+    a.spin_limit = kSpinLimit;
     return a;
 }
 
@@ -268,8 +272,8 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (void* p : ctx->allocs) (void)hipFree(p);
-    void* owned[] = {ctx->arena,  ctx->routers,  ctx->biases,   ctx->logits, ctx->topk_idx,
-                     ctx->topk_w, ctx->counters, ctx->act, ctx->err};
+    void* owned[] = {ctx->arena,  ctx->routers,  ctx->biases, ctx->logits, ctx->topk_idx,
+                     ctx->topk_w, ctx->counters, ctx->act,    ctx->sync,   ctx->err};
     for (void* p : owned)
         if (p) (void)hipFree(p);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -304,6 +308,20 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         return cleanup(fail(M1MOE_ERR_HIP, "hipStreamCreate failed"));
     c->stream = c->own_stream;
     const uint64_t cap = m1moe::kPrefillCap;
+    {
+        // hand-off state of the fused decode kernel: E logit slots, K x kActSub
+        // padded completion counters, one launch counter per workgroup
+        m1moe::FusedArgs fa{};
+        fa.h = g.h;
+        fa.E = g.E;
+        fa.K = g.K;
+        fa.I = g.I;
+        const int grid = m1moe::decode_grid(fa);
+        c->sync_act_cnt = 4096;
+        c->sync_seen =
+            c->sync_act_cnt + (uint64_t)g.K * m1moe::kActSub * m1moe::kActCntStride * 4;
+        c->sync_bytes = c->sync_seen + ((uint64_t)grid * 4 + 255) / 256 * 256;
+    }
     if ((rc = device_alloc((void**)&c->arena, L * E * g.expert_bytes, "expert arena")) ||
         (rc = device_alloc((void**)&c->routers, L * E * g.h * 2, "routers")) ||
         (rc = device_alloc((void**)&c->biases, L * E * 4, "logit biases")) ||
@@ -312,10 +330,12 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         (rc = device_alloc((void**)&c->topk_w, cap * g.K * 4, "topk w")) ||
         (rc = device_alloc((void**)&c->counters, cap * 4, "counters")) ||
         (rc = device_alloc((void**)&c->act, (uint64_t)g.K * g.I * 4, "act")) ||
+        (rc = device_alloc((void**)&c->sync, c->sync_bytes, "decode hand-off state")) ||
         (rc = device_alloc((void**)&c->err, 4, "error flag")))
         return cleanup(rc);
     if (hipMemset(c->counters, 0, cap * 4) != hipSuccess ||
         hipMemset(c->err, 0, 4) != hipSuccess || hipMemset(c->biases, 0, L * E * 4) != hipSuccess ||
+        hipMemset(c->sync, 0, c->sync_bytes) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
         return cleanup(fail(M1MOE_ERR_HIP, "scratch initialisation failed"));
     *out = c;
@@ -453,11 +473,17 @@ int32_t m1moe_sync(m1moe_ctx_t ctx) {
     uint32_t flag = 0;
     HIP_TRY(hipMemcpy(&flag, ctx->err, 4, hipMemcpyDeviceToHost));
     if (flag) {
+        // a failed launch leaves the workgroups' launch counters out of step:
+        // restart them all from zero
         HIP_TRY(hipMemset(ctx->err, 0, 4));
+        HIP_TRY(hipMemset(ctx->sync, 0, ctx->sync_bytes));
         HIP_TRY(hipDeviceSynchronize());
+        if (flag & 1u)
+            return fail(M1MOE_ERR_DEVICE,
+                        "a kernel saw an expert index outside [0, %d) (device flag 0x%x)",
+                        ctx->g.E, flag);
         return fail(M1MOE_ERR_DEVICE,
-                    "a kernel saw an expert index outside [0, %d) (device flag 0x%x)", ctx->g.E,
-                    flag);
+                    "a decode hand-off wait timed out (device flag 0x%x); state was reset", flag);
     }
     return M1MOE_OK;
 }
@@ -572,10 +598,10 @@ int32_t m1moe_moe_decode_given_topk(m1moe_ctx_t ctx, int32_t layer, const void* 
         return rc;
     if ((rc = require_loaded(ctx, layer, false))) return rc;
     if ((rc = set_device(ctx))) return rc;
-    const m1moe::DecodeArgs a =
-        decode_args(ctx, layer, d_x, x_dtype, d_topk_idx, d_topk_w, d_residual, d_out);
-    if ((rc = launched(m1moe::launch_decode_gate_up(a, ctx->stream), "decode gate/up"))) return rc;
-    return launched(m1moe::launch_decode_down_combine(a, ctx->stream), "decode down/combine");
+    m1moe::FusedArgs a = fused_args(ctx, layer, d_x, x_dtype, d_residual, d_out);
+    a.given_idx = d_topk_idx;
+    a.given_w = d_topk_w;
+    return launched(m1moe::launch_moe_decode(a, ctx->stream), "moe_decode (given routing)");
 }
 
 int32_t m1moe_moe_decode(m1moe_ctx_t ctx, int32_t layer, const void* d_x, int32_t x_dtype,
@@ -591,12 +617,10 @@ int32_t m1moe_moe_decode(m1moe_ctx_t ctx, int32_t layer, const void* d_x, int32_
         return rc;
     if ((rc = require_loaded(ctx, layer, true))) return rc;
     if ((rc = set_device(ctx))) return rc;
-    if ((rc = enqueue_router(ctx, layer, 1, d_x, x_dtype, d_topk_idx, d_topk_w, nullptr)))
-        return rc;
-    const m1moe::DecodeArgs a =
-        decode_args(ctx, layer, d_x, x_dtype, ctx->topk_idx, ctx->topk_w, d_residual, d_out);
-    if ((rc = launched(m1moe::launch_decode_gate_up(a, ctx->stream), "decode gate/up"))) return rc;
-    return launched(m1moe::launch_decode_down_combine(a, ctx->stream), "decode down/combine");
+    m1moe::FusedArgs a = fused_args(ctx, layer, d_x, x_dtype, d_residual, d_out);
+    a.user_idx = d_topk_idx;
+    a.user_w = d_topk_w;
+    return launched(m1moe::launch_moe_decode(a, ctx->stream), "moe_decode");
 }
 
 int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_x,

@@ -93,23 +93,150 @@ __device__ __forceinline__ void pow2_scale(float maxabs, float& scale, float& in
     inv = ldexpf(1.f, e - 14);
 }
 
-template <typename T>
-__device__ __forceinline__ T shfl_xor(T v, int m) {
-    return __shfl_xor(v, m, 64);
+// ---- cross-lane reductions on DPP (full-rate VALU lane moves) ---------------
+// gfx9 DPP controls: quad_perm [1,0,3,2] / [2,3,0,1], rotate right within a
+// row of 16 lanes by 4 / 8, broadcast lane 15 of each row to the next row,
+// broadcast lane 31 to rows 2 and 3.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRor4 = 0x124, kDppRor8 = 0x128;
+constexpr int kDppBcast15 = 0x142, kDppBcast31 = 0x143;
+
+// Lanes of rows outside ROWS get `old`.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_f32(float old, float v) {
+    return __uint_as_float(dpp_u32<CTRL, ROWS>(__float_as_uint(old), __float_as_uint(v)));
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_f64(double old, double v) {
+    const unsigned long long o = __double_as_longlong(old), x = __double_as_longlong(v);
+    const uint32_t lo = dpp_u32<CTRL, ROWS>((uint32_t)o, (uint32_t)x);
+    const uint32_t hi = dpp_u32<CTRL, ROWS>((uint32_t)(o >> 32), (uint32_t)(x >> 32));
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
 }
 
-// Butterfly sum inside aligned segments of `seg` lanes (seg a power of two).
+// Sum over aligned segments of `seg` lanes (a power of two, 2..64).  The
+// segment's total lands in its last lane (lane % seg == seg - 1); other lanes
+// keep partial sums.  The order is fixed, so results are deterministic.
 __device__ __forceinline__ float seg_sum(float v, int seg) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1)
-        if (o < seg) v += shfl_xor(v, o);
+    v += dpp_f32<kDppXor1>(v, v);
+    if (seg >= 4) v += dpp_f32<kDppXor2>(v, v);
+    if (seg >= 8) v += dpp_f32<kDppRor4>(v, v);
+    if (seg >= 16) v += dpp_f32<kDppRor8>(v, v);
+    if (seg >= 32) v += dpp_f32<kDppBcast15, 0xA>(0.f, v);
+    if (seg >= 64) v += dpp_f32<kDppBcast31, 0xC>(0.f, v);
     return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
+// Sum over the wave, total in lane 63.
+__device__ __forceinline__ double wave_sum_f64_last(double v) {
+    v += dpp_f64<kDppXor1>(v, v);
+    v += dpp_f64<kDppXor2>(v, v);
+    v += dpp_f64<kDppRor4>(v, v);
+    v += dpp_f64<kDppRor8>(v, v);
+    v += dpp_f64<kDppBcast15, 0xA>(0.0, v);
+    v += dpp_f64<kDppBcast31, 0xC>(0.0, v);
     return v;
+}
+
+// Sum over the wave, returned to every lane (uniform).
+__device__ __forceinline__ float wave_sum(float v) {
+    return readlane_f32(seg_sum(v, 64), 63);
+}
+
+// Max over the wave, returned to every lane (uniform).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<kDppXor1>(v, v));
+    v = fmaxf(v, dpp_f32<kDppXor2>(v, v));
+    v = fmaxf(v, dpp_f32<kDppRor4>(v, v));
+    v = fmaxf(v, dpp_f32<kDppRor8>(v, v));
+    v = fmaxf(v, dpp_f32<kDppBcast15, 0xA>(v, v));
+    v = fmaxf(v, dpp_f32<kDppBcast31, 0xC>(v, v));
+    return readlane_f32(v, 63);
+}
+
+// (value desc, index asc) maximum over the wave, returned to every lane.
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+#define M1MOE_ARGMAX_STEP(CTRL)                                                   \
+    {                                                                             \
+        const float ov = dpp_f32<CTRL>(bv, bv);                                   \
+        const int oi = (int)dpp_u32<CTRL>((uint32_t)bi, (uint32_t)bi);            \
+        if (ov > bv || (ov == bv && oi < bi)) {                                   \
+            bv = ov;                                                              \
+            bi = oi;                                                              \
+        }                                                                         \
+    }
+    M1MOE_ARGMAX_STEP(kDppXor1)
+    M1MOE_ARGMAX_STEP(kDppXor2)
+    M1MOE_ARGMAX_STEP(kDppRor4)
+    M1MOE_ARGMAX_STEP(kDppRor8)
+#undef M1MOE_ARGMAX_STEP
+    // every lane of a row now holds the row's best; combine the four rows
+    float v = readlane_f32(bv, 0);
+    int i = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+    for (int r = 1; r < 4; ++r) {
+        const float rv = readlane_f32(bv, 16 * r);
+        const int ri = __builtin_amdgcn_readlane(bi, 16 * r);
+        if (rv > v || (rv == v && ri < i)) {
+            v = rv;
+            i = ri;
+        }
+    }
+    bv = v;
+    bi = i;
+}
+
+// Ranks the logits of up to 256 experts held 4 per lane (expert lane + 64j;
+// pass -inf beyond E) by descending value with ties to the lower index, and
+// computes softmax weights over all E experts (InferenceEngine.swift:501-506),
+// renormalised over the selection when `norm` (:514-517, summed in slot
+// order).  Lane r < K receives slot r's expert and weight.
+__device__ __forceinline__ void topk_softmax(const float (&v)[4], int E, int K, int norm, int lane,
+                                             int& my_idx, float& my_w) {
+    bool taken[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) taken[j] = (lane + 64 * j >= E);
+    float my_val = -INFINITY, mx = -INFINITY;
+    my_idx = 0;
+    for (int r = 0; r < K; ++r) {
+        float bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ee = lane + 64 * j;
+            if (!taken[j] && (v[j] > bv || (v[j] == bv && ee < bi))) {
+                bv = v[j];
+                bi = ee;
+            }
+        }
+        wave_argmax(bv, bi);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j == bi) taken[j] = true;
+        if (r == 0) mx = bv;
+        if (lane == r) {
+            my_idx = bi;
+            my_val = bv;
+        }
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < E) sum += expf(v[j] - mx);
+    const float inv = 1.0f / wave_sum(sum);
+    const float p = (lane < K) ? expf(my_val - mx) * inv : 0.f;
+    my_w = p;
+    if (norm) {
+        float ssum = 0.f;
+        for (int r = 0; r < K; ++r) ssum = ssum + readlane_f32(p, r);
+        my_w = p / ssum;
+    }
 }
 
 __device__ __forceinline__ void flag_error(uint32_t* err, uint32_t code) {

@@ -23,28 +23,49 @@ Geom make_geom(const m1moe_moe_shape& s);
 // Records a printf-style message as the thread's last error; returns code.
 int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
-// Kernel-side view of one projection: packed words, scales, biases are
-// reached from the expert block base by the byte offsets below.
+// One projection of an expert block: packed words, scales and biases are
+// reached from the block base by these byte offsets.
 struct ProjView {
     uint64_t w_off, s_off, b_off;
     int32_t rows, cols;
 };
 
-// Arguments shared by the decode kernels.
-struct DecodeArgs {
+// Arguments of the fused decode kernel (one token through one layer).  The
+// nine sub-block offsets of an expert block are derived in the kernel from
+// (h, I, gs) rather than passed.
+struct FusedArgs {
     const uint8_t* layer_base;   // first expert block of the layer
     uint64_t expert_bytes;
-    int32_t h, E, K, I, gs;
+    const uint16_t* router;      // [E][h] bf16
+    const float* bias;           // [E] or null
     const void* x;               // [h] f32 or bf16
-    int32_t x_bf16;
-    const int32_t* topk_idx;     // [K]
-    const float* topk_w;         // [K]
     const float* residual;       // [h] or null
     float* out;                  // [h]
-    float* act;                  // [K][I] scratch
+    const int32_t* given_idx;    // [K] routing supplied by the caller, or null
+    const float* given_w;        // [K]
+    int32_t* user_idx;           // optional copies of the routing
+    float* user_w;
+    // hand-off state.  It starts at zero and is never reset between launches:
+    // every workgroup counts its own launches in seen[wg], so all workgroups
+    // agree on the launch number without communicating.
+    unsigned long long* slots;   // [E] published logits, tagged with the launch number
+    float* act;                  // [K][I]
+    uint32_t* act_cnt;           // [K][kActSub] monotonic, kActCntStride apart
+    uint32_t* seen;              // [grid] launches completed by each workgroup
     uint32_t* err;               // sticky device error flag
-    ProjView gate, up, down;
+    int32_t h, E, K, I, gs, norm, x_bf16, spin_limit;
+    // work decomposition (decode_grid)
+    int32_t n_gu, gu_per_slot, n_dn;
+    int32_t Cg, rpi_g;           // gate/up: 32-column chunks per row, rows per wave step
+    int32_t Cd, rpi_d, Sc;       // down: chunks per row, rows per step, column slices
 };
+
+constexpr int kActSub = 8;             // completion sub-counters per slot
+constexpr int kActCntStride = 32;      // u32 words between counters (128 B)
+
+// Fills the work decomposition of the fused decode kernel for a shape and
+// returns its grid size (workgroups).
+int decode_grid(FusedArgs& a);
 
 struct RouterArgs {
     const uint16_t* router;      // [E][h] bf16
@@ -63,8 +84,7 @@ struct RouterArgs {
 
 // launchers (defined next to their kernels); return a hipError_t as int
 int launch_router_topk(const RouterArgs& a, void* stream);
-int launch_decode_gate_up(const DecodeArgs& a, void* stream);
-int launch_decode_down_combine(const DecodeArgs& a, void* stream);
+int launch_moe_decode(const FusedArgs& a, void* stream);
 int launch_dequant(const uint8_t* expert_base, const ProjView& p, int32_t gs, float* out,
                    void* stream);
 

@@ -26,12 +26,6 @@ constexpr int kRouterWaves = 4;  // experts (waves) per block
 constexpr int kMaxE = 256;       // 4 logits per lane in the ranking wave
 constexpr int kMaxK = 32;  // one selection per lane
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
 __global__ __launch_bounds__(256) void router_topk_kernel(RouterArgs a, int blocks_per_token) {
     const int t = blockIdx.x / blocks_per_token;
     const int b = blockIdx.x - t * blocks_per_token;
@@ -62,8 +56,8 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterArgs a, int bloc
                 for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv, i) * (double)xs[i];
             }
         }
-        acc = wave_sum_f64(acc);
-        if (lane == 0) {
+        acc = wave_sum_f64_last(acc);
+        if (lane == 63) {
             float l = (float)acc;
             if (a.bias) l = l + a.bias[e];
             a.logits[(size_t)t * E + e] = l;
@@ -85,7 +79,6 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterArgs a, int bloc
 
     const float* lg = a.logits + (size_t)t * E;
     float v[4];
-    bool taken[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int ee = lane + 64 * j;
@@ -95,59 +88,11 @@ __global__ __launch_bounds__(256) void router_topk_kernel(RouterArgs a, int bloc
             if (x != x) x = -INFINITY;  // NaN ranks last
         }
         v[j] = x;
-        taken[j] = (ee >= E);
     }
 
-    // K rounds of a wave-wide argmax on (logit desc, index asc); lane r keeps
-    // the r-th selection.  Every lane sees each round's winner.
-    int my_idx = 0;
-    float my_val = -INFINITY, mx = -INFINITY;
-    for (int r = 0; r < K; ++r) {
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int ee = lane + 64 * j;
-            if (!taken[j] && (v[j] > bv || (v[j] == bv && ee < bi))) {
-                bv = v[j];
-                bi = ee;
-            }
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j == bi) taken[j] = true;
-        if (r == 0) mx = bv;  // the largest logit
-        if (lane == r) {
-            my_idx = bi;
-            my_val = bv;
-        }
-    }
-
-    // softmax denominator over all experts
-    float sum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (lane + 64 * j < E) sum += expf(v[j] - mx);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    const float inv = 1.0f / sum;
-
-    const float p = (lane < K) ? expf(my_val - mx) * inv : 0.f;
-    float wr = p;
-    if (a.norm) {
-        float ssum = 0.f;  // sequential in slot order, as the reference's reduce
-        for (int r = 0; r < K; ++r) ssum = ssum + __shfl(p, r, 64);
-        wr = p / ssum;
-    }
+    int my_idx;
+    float wr;
+    topk_softmax(v, E, K, a.norm, lane, my_idx, wr);
     if (lane < K) {
         a.idx[(size_t)t * K + lane] = my_idx;
         a.w[(size_t)t * K + lane] = wr;

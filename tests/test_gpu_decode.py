@@ -215,6 +215,31 @@ def test_decode_ragged_shapes(kw):
         del synth.CONFIGS["_ragged"]
 
 
+def test_given_and_routed_launches_interleave(cfg0):
+    # launches with caller-supplied routing and launches that route on the GPU
+    # share the context's hand-off state and must stay in step
+    blk = MoEBlock(cfg0.ctx)
+    K, h = cfg0.shape.top_k, cfg0.shape.hidden
+    s = cfg0.oshape
+    xb = cfg0.x_bf16(4, stream=31)
+    out = cfg0.ctx.alloc(h * 4)
+    didx = cfg0.ctx.to_device(np.arange(K, dtype=np.int32))
+    dw = cfg0.ctx.to_device(np.full(K, 1.0 / K, np.float32))
+    for t in range(4):
+        x32 = synth.bf16_to_f32(xb[t])
+        dx = cfg0.ctx.to_device(xb[t])
+        say(f"interleaved launch t={t} given={t % 2 == 0}")
+        if t % 2 == 0:
+            blk.forward_given_topk(0, dx, "bf16", didx, dw, None, out)
+            want = orc.moe_decode_given_topk(s, cfg0.images[0], x32, np.arange(K, dtype=np.int32),
+                                             np.full(K, 1.0 / K, np.float32))
+        else:
+            blk.forward(0, dx, "bf16", None, out)
+            want = orc.moe_decode(s, cfg0.images[0], cfg0.routers[0], x32)[0]
+        cfg0.ctx.sync()
+        assert rel_l2(out.download(np.float32), want) <= REL_L2_TOL
+
+
 def test_decode_is_deterministic(cfg0):
     blk = MoEBlock(cfg0.ctx)
     h = cfg0.shape.hidden

@@ -58,6 +58,19 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def copy_calibration(m, nbytes: int, reps: int) -> int:
+    """Plain device-to-device copies of a known size, so a profiler's
+    FETCH_SIZE / WRITE_SIZE for this copy kernel give the counter's scale."""
+    shape = m.make_shape(64, 1, 1, 64, 64)
+    with m.HIPContext(shape) as ctx:
+        a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+        for _ in range(reps):
+            ctx.lib.m1moe_copy_d2d(ctx.handle, b.ptr, a.ptr, nbytes)
+        ctx.sync()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": reps}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -69,6 +82,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU-baseline sample (0 disables it)")
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run device-to-device copies of BYTES bytes (to scale HBM "
+                         "byte counters against a plain copy of known size), then exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -80,6 +96,9 @@ def main() -> int:
     import m1moe_amd as m
     from m1moe_amd import synth
     from m1moe_amd.engine import MoEBlock
+
+    if args.copy_calibration:
+        return copy_calibration(m, args.copy_calibration, max(1, args.steps))
 
     wl = synth.CONFIGS[args.config]
     one = wl.shape(1)
@@ -162,6 +181,14 @@ def main() -> int:
                          f"oracle on 1 thread ({t_cpu:.1f}s); host CPU: {cpu_model()}"}
         log(f"cpu baseline: {cpu['value']} layer-tok/s")
 
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            rec = json.load(f).get(args.config)
+        if rec:  # measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, copy-calibrated
+            traffic = int(rec["hbm_bytes_per_launch"])
+
     line = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -181,9 +208,9 @@ def main() -> int:
                    "replicas": R, "tokens_per_step": 1, "x_dtype": "bf16",
                    "residual": "f32"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "whole MoE block per layer-token (router_topk + gate_up + "
-                               "down_combine)",
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "kernel": "moe_decode_kernel (the whole MoE block, one launch per "
+                               "layer-token)",
                      "bytes_per_launch": bytes_tok, "us_per_launch": round(layer_us, 4)},
         "cpu_baseline": cpu,
         "parity": {"topk_exact": idx_ok, "rel_l2": rel},

@@ -301,3 +301,35 @@ def test_graph_replay_matches_eager(cfg0):
         # eager work between replays
         blk.forward(0, dx[1], "bf16", None, outs[0])
         cfg0.ctx.sync()
+
+
+# ---- golden fixtures ---------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["tiny.npz", "tiny_renorm.npz"])
+def test_golden_fixture_on_gpu(name):
+    import os
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name),
+                allow_pickle=False)
+    h, E, K, I, gs, norm = (int(v) for v in f["shape"])
+    shape = m.make_shape(h, E, K, I, gs, 1, bool(norm))
+    say(f"golden {name}")
+    with m.HIPContext(shape) as ctx:
+        ctx.upload_layer_experts(0, f["image"])
+        ctx.upload_router(0, f["router"])
+        if "logit_bias" in f.files:
+            ctx.set_logit_bias(0, f["logit_bias"])
+        blk = MoEBlock(ctx)
+        out, didx, dw = ctx.alloc(h * 4), ctx.alloc(K * 4), ctx.alloc(K * 4)
+        for t in range(f["x_bf16"].shape[0]):
+            dx, dres = ctx.to_device(f["x_bf16"][t]), ctx.to_device(f["residual"][t])
+            blk.forward(0, dx, "bf16", dres, out, didx, dw)
+            ctx.sync()
+            assert np.array_equal(didx.download(np.int32), f["topk_idx"][t])
+            assert np.allclose(dw.download(np.float32), f["topk_w"][t], rtol=2e-6)
+            assert rel_l2(out.download(np.float32), f["out"][t]) <= REL_L2_TOL
+        e = int(f["dequant_expert"][0])
+        for p, key in enumerate(["dequant_gate", "dequant_up", "dequant_down"]):
+            buf = ctx.alloc(f[key].nbytes)
+            blk.dequant(0, e, p, buf)
+            ctx.sync()
+            assert np.array_equal(buf.download(np.uint32), f[key].view(np.uint32).ravel())

@@ -91,8 +91,8 @@ struct m1moe_ctx {
     float* topk_w = nullptr;         // [cap][K]
     uint32_t* counters = nullptr;    // [cap]
     float* act = nullptr;            // [K][I]
-    uint8_t* sync = nullptr;         // decode hand-off state: slots | act_cnt | seen
-    uint64_t sync_bytes = 0, sync_act_cnt = 0, sync_seen = 0;
+    uint8_t* sync = nullptr;         // decode hand-off state: slots | gu_cnt | seen
+    uint64_t sync_bytes = 0, sync_gu_cnt = 0, sync_seen = 0;
     uint32_t* err = nullptr;         // sticky device error flag
     std::set<void*> allocs;
 };
@@ -171,7 +171,7 @@ m1moe::FusedArgs fused_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32
     a.out = out;
     a.slots = reinterpret_cast<unsigned long long*>(ctx->sync);
     a.act = ctx->act;
-    a.act_cnt = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_act_cnt);
+    a.gu_cnt = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_gu_cnt);
     a.seen = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_seen);
     a.err = ctx->err;
     a.h = g.h;
@@ -309,17 +309,18 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
     c->stream = c->own_stream;
     const uint64_t cap = m1moe::kPrefillCap;
     {
-        // hand-off state of the fused decode kernel: E logit slots, K x kActSub
-        // padded completion counters, one launch counter per workgroup
+        // hand-off state of the fused decode kernel: kNRep replicas of the
+        // tagged logits, K x kSub padded tile counters, one launch counter per
+        // workgroup
         m1moe::FusedArgs fa{};
         fa.h = g.h;
         fa.E = g.E;
         fa.K = g.K;
         fa.I = g.I;
         const int grid = m1moe::decode_grid(fa);
-        c->sync_act_cnt = 4096;
+        c->sync_gu_cnt = (uint64_t)m1moe::kNRep * m1moe::kRepStride * 8;
         c->sync_seen =
-            c->sync_act_cnt + (uint64_t)g.K * m1moe::kActSub * m1moe::kActCntStride * 4;
+            c->sync_gu_cnt + (uint64_t)g.K * m1moe::kSub * m1moe::kCntStride * 4;
         c->sync_bytes = c->sync_seen + ((uint64_t)grid * 4 + 255) / 256 * 256;
     }
     if ((rc = device_alloc((void**)&c->arena, L * E * g.expert_bytes, "expert arena")) ||

@@ -7,34 +7,43 @@
 // Metal dispatches (matvec4bit x3 + swiGLU per slot, then moeCombine:
 // InferenceEngine.swift:401-478, Shaders.metal:39-92,138-149,360-376).
 //
-// Roles (by workgroup id; lower ids are dispatched first, and a workgroup
-// only waits for lower-id workgroups or for router logits, which the lowest
-// ids produce before they wait for anything, so the grid cannot deadlock):
+// Roles by workgroup id (lower ids are dispatched first; a workgroup only
+// waits for lower-id workgroups or for router logits, which the lowest ids
+// publish before they wait for anything, so the grid cannot deadlock):
 //   [0, n_gu)          gate/up workgroups: (slot k, block of rows) of the
-//                      k-th selected expert -> act[k][rows] = silu(g)*u
-//   [n_gu, n_gu+n_dn)  down workgroups: a block of output rows for all K
-//                      slots; they load their down-weight tiles as soon as
-//                      the routing is known, then wait for act[k].
-//   Workgroup e < E (wave 0) first publishes router logit e.
+//                      k-th selected expert, slot-major.  All of a
+//                      workgroup's weight loads are issued at once (for a
+//                      few-MB working set the whole layer must be in flight
+//                      to cover the loaded HBM latency); it writes
+//                      act[k][rows] = silu(g) * u, then bumps one of kSub
+//                      spread counters of slot k.
+//   [n_gu, grid)       down workgroups: Rd output rows for all K slots.  Each
+//                      lane owns one (slot, 32-column chunk) of the down
+//                      projection; its weights for all Rd rows are loaded as
+//                      soon as the routing is known, then it waits for its
+//                      slot's counters, converts its chunk of act once and
+//                      sweeps the rows.  Slots are combined in slot order in
+//                      LDS (deterministic, no atomics), plus the residual.
+//   Workgroup e < E first publishes router logit e (all four waves).
 //
-// Cross-workgroup hand-off uses relaxed agent-scope atomics (sc1 loads and
-// stores, coherent across the XCDs' L2s), never release/acquire fences
-// (their L2 write-back/invalidate costs microseconds per use).  Logits are
-// published as (launch tag, value) pairs that consumers poll directly.
-// Finished gate/up workgroups bump one of kActSub spread counters of their
-// slot after their act stores have completed (s_waitcnt), so no address sees
-// more than a handful of atomics per launch.  Nothing is reset between
-// launches: every workgroup counts its own launches (seen[wg]), so all agree
-// on the launch number `tag` and on the counters' targets (graph replay
-// needs no memset).  Every wait is bounded: on timeout the workgroup raises
-// the device error flag and skips its work, so a broken hand-off ends the
-// kernel instead of hanging it.
+// Hand-off.  Relaxed agent-scope atomics and 128-bit sc1 loads of act (sc1
+// accesses are coherent across the XCDs' L2s), never release/acquire fences
+// (an L2 write-back or invalidate costs microseconds).  Logits are published as (launch tag,
+// value) pairs into kNRep replicas, and a workgroup polls replica
+// wg % kNRep, so no cache line has more than a few dozen pollers.  Nothing is
+// reset between launches: every workgroup counts its own launches (seen[wg]),
+// so all agree on the launch number `tag` and on the counters' targets
+// (graph replay needs no memset).  Every wait is bounded: on timeout the
+// workgroup raises the device error flag and skips its work but still does
+// all of its counter updates, so the kernel always ends and the counters stay
+// in step.
 //
 // Matvec arithmetic: sum_c (n_c*s_g + b_g) x_c is evaluated as
 // sum_g [ s_g * sum_{c in g} n_c x_c + b_g * sum_{c in g} x_c ], the inner
 // nibble sums on v_dot2_f32_f16 (exact f16*f16 products, f32 accumulation).
-// The input vector is scaled by a power of two (largest element in
-// [2^13, 2^14)) and rounded to f16 once; results are scaled back exactly.
+// Each lane scales its 32-element input chunk by a power of two (largest
+// element in [2^13, 2^14)) and rounds it to f16 once; its partial sum is
+// scaled back exactly before the cross-lane reduction.
 #include <hip/hip_runtime.h>
 
 #include "device.hpp"
@@ -43,10 +52,14 @@
 namespace m1moe {
 namespace {
 
-constexpr int kWaves = 4;  // waves per workgroup
+constexpr int kWaves = kDecodeWaves;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxK = 32;
 constexpr int kMaxE = 256;
-constexpr int kRS = 2;     // down: wave steps per tile
+constexpr int kRT = 4;          // down rows per sub-tile
+constexpr int kDnTarget = 256;  // down workgroups
+
+static_assert(kWaves >= 4, "the router splits a logit over four waves");
 
 // ---- hand-off primitives ------------------------------------------------------
 
@@ -100,40 +113,9 @@ struct Layout {
     }
 };
 
-// ---- lane maps -------------------------------------------------------------------
-
-struct LaneMap {
-    int q;        // row slot within one wave step
-    int c0;       // first chunk index
-    bool ok;      // lane participates
-    int seg;      // reduction segment width (power of two)
-    bool writer;  // last lane of its segment: holds the row total
-    int wq;       // row slot whose total the writer holds
-};
-
-// Chunk = 32 columns = one 128-bit load of nibbles.  C = chunks per row; a
-// row with C < 64 dividing 64 shares a wave step with rpi-1 others.
-__device__ __forceinline__ LaneMap lane_map(int lane, int C, int rpi) {
-    LaneMap m;
-    if (C >= 64) {
-        m.q = 0;
-        m.c0 = lane;
-        m.ok = true;
-        m.seg = 64;
-    } else {
-        m.q = lane / C;
-        m.c0 = lane - m.q * C;
-        m.ok = m.q < rpi;
-        m.seg = (rpi > 1) ? C : 64;
-    }
-    m.writer = (lane & (m.seg - 1)) == m.seg - 1;
-    m.wq = (m.seg < 64) ? lane / m.seg : 0;
-    return m;
-}
-
 // Loads 32-element chunk c of an f32 or bf16 vector as f32.  The caller
 // passes an in-range chunk index (clamped for idle lanes) so the loads are
-// unconditional and can all be in flight together; ok = false zeroes them.
+// unconditional; ok = false zeroes them.
 __device__ __forceinline__ void load_chunk(const void* x, int x_bf16, int c, bool ok,
                                            float (&v)[32]) {
     if (x_bf16) {
@@ -160,44 +142,54 @@ __device__ __forceinline__ void load_chunk(const void* x, int x_bf16, int c, boo
     }
 }
 
-// f32 chunk written by other workgroups in this launch: coherent 64-bit loads
-// (same in-range/ok convention as load_chunk).
+// f32 chunk written by other workgroups in this launch: eight 128-bit
+// agent-coherent loads (sc1: they bypass the non-coherent L2 copies), all in
+// flight together, then one wait (which also covers this wave's earlier
+// loads).  The chunk address must be in range; ok = false zeroes the values.
 __device__ __forceinline__ void load_chunk_coherent(const float* x, int c, bool ok,
                                                     float (&v)[32]) {
-    const unsigned long long* p = reinterpret_cast<const unsigned long long*>(x + c * 32);
-    unsigned long long u[16];
+    const float* p = x + c * 32;
+    float4 q0, q1, q2, q3, q4, q5, q6, q7;
+    asm volatile(
+        "global_load_dwordx4 %0, %8, off sc1\n\t"
+        "global_load_dwordx4 %1, %8, off offset:16 sc1\n\t"
+        "global_load_dwordx4 %2, %8, off offset:32 sc1\n\t"
+        "global_load_dwordx4 %3, %8, off offset:48 sc1\n\t"
+        "global_load_dwordx4 %4, %8, off offset:64 sc1\n\t"
+        "global_load_dwordx4 %5, %8, off offset:80 sc1\n\t"
+        "global_load_dwordx4 %6, %8, off offset:96 sc1\n\t"
+        "global_load_dwordx4 %7, %8, off offset:112 sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3), "=&v"(q4), "=&v"(q5), "=&v"(q6),
+          "=&v"(q7)
+        : "v"(p)
+        : "memory");
+    const float4 q[8] = {q0, q1, q2, q3, q4, q5, q6, q7};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) u[i] = ld_u64(p + i);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        v[2 * i] = ok ? __uint_as_float((uint32_t)u[i]) : 0.f;
-        v[2 * i + 1] = ok ? __uint_as_float((uint32_t)(u[i] >> 32)) : 0.f;
+    for (int i = 0; i < 8; ++i) {
+        v[4 * i + 0] = ok ? q[i].x : 0.f;
+        v[4 * i + 1] = ok ? q[i].y : 0.f;
+        v[4 * i + 2] = ok ? q[i].z : 0.f;
+        v[4 * i + 3] = ok ? q[i].w : 0.f;
     }
 }
 
-// Scale and bias of one group as the aligned dword holding the bf16 (a 32-bit
-// load keeps the compiler from merging halves with ordered d16 loads).
-struct SBIdx {
-    uint32_t word;  // byte offset of the dword
-    bool hi;        // the bf16 is the upper half
-};
-__device__ __forceinline__ SBIdx sb_index(uint32_t elem) {
-    return SBIdx{(elem >> 1) << 2, (elem & 1u) != 0};
-}
-__device__ __forceinline__ float sb_pick(uint32_t w, bool hi) {
-    return hi ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
-}
+// Scale and bias of one group, loaded as the aligned dword holding the bf16
+// (a 32-bit load keeps the compiler from merging halves with ordered d16
+// loads); `elem` is the bf16 index in the row-major [rows][groups] array.
+__device__ __forceinline__ uint32_t sb_word(uint32_t elem) { return (elem >> 1) << 2; }
+__device__ __forceinline__ uint32_t sb_sel(uint32_t elem) { return (elem & 1u) ? kSelHi : kSelLo; }
 
-// Scale a lane's chunks by the wave-wide power of two and convert to the f16
-// pairs of the nibble dot product.  All 64 lanes must call it.
+// Scales each of a lane's chunks by one power of two (its largest element
+// into [2^13, 2^14)) and converts them to the f16 pairs of the nibble dot
+// product.  Returns the inverse scale.
 template <int N>
-__device__ __forceinline__ float scale_and_prep(float (&v)[N][32], XChunk (&xc)[N]) {
+__device__ __forceinline__ float lane_scale_prep(float (&v)[N][32], XChunk (&xc)[N]) {
     float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < N; ++j)
 #pragma unroll
         for (int e = 0; e < 32; ++e) mx = fmaxf(mx, fabsf(v[j][e]));
-    mx = wave_max(mx);
     float scale, inv;
     pow2_scale(mx, scale, inv);
 #pragma unroll
@@ -209,300 +201,500 @@ __device__ __forceinline__ float scale_and_prep(float (&v)[N][32], XChunk (&xc)[
     return inv;
 }
 
+// One 32-column chunk of one row: s * sum(n x) + b * sum(x), in the lane's
+// scaled units.
+__device__ __forceinline__ float chunk_term(const uint4& w, uint32_t sw, uint32_t bw,
+                                            uint32_t sel, const XChunk& xc, const NibK& nk) {
+    const float d = nib_dot32(w, xc, nk) - xc.off;
+    return fmaf(bf16_pick(sw, sel), d, bf16_pick(bw, sel) * xc.xs);
+}
+
 // ---- router --------------------------------------------------------------------
 
-template <bool XBF16>
-__device__ __forceinline__ double logit_partial(const FusedArgs& a, const uint16_t* wr, int lane) {
-    double acc = 0.0;
-    // 8 columns per lane per step; 4 steps' loads in flight at once
-    for (int d0 = lane * 8; d0 < a.h; d0 += 4 * 512) {
-        uint4 wv[4];
-        uint4 xb[4];
-        float4 xf[4][2];
+// Logit e: exact bf16*x products summed in f64, rounded once to f32, plus the
+// bias.  Wave w < 4 sums columns 8w..8w+7 of every 32-column chunk; the wave
+// partials are added in wave order.  Published to every replica as
+// (tag << 32 | bits).  Every thread of the workgroup calls it; s_tag must be
+// visible (a barrier after it was written) before the call.
+__device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, const uint32_t* s_tag,
+                              double* s_lp) {
+    if (wave < 4) {
+        const uint16_t* wr = a.router + (size_t)e * a.h;
+        const int C = a.h / 32;
+        double acc = 0.0;
+        for (int c = lane; c < C; c += 64) {
+            const int d = c * 32 + wave * 8;
+            const uint4 wv = *reinterpret_cast<const uint4*>(wr + d);
+            float xv[8];
+            if (a.x_bf16) {
+                const uint4 xb = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + d);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int d = min(d0 + s * 512, a.h - 8);
-            wv[s] = *reinterpret_cast<const uint4*>(wr + d);
-            if (XBF16) {
-                xb[s] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + d);
+                for (int i = 0; i < 8; ++i) xv[i] = bf16x8_at(xb, i);
             } else {
                 const float* xr = static_cast<const float*>(a.x) + d;
-                xf[s][0] = *reinterpret_cast<const float4*>(xr);
-                xf[s][1] = *reinterpret_cast<const float4*>(xr + 4);
+                const float4 x0 = *reinterpret_cast<const float4*>(xr);
+                const float4 x1 = *reinterpret_cast<const float4*>(xr + 4);
+                xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
+                xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
             }
-        }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            if (d0 + s * 512 < a.h) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    float xv;
-                    if (XBF16) {
-                        xv = bf16x8_at(xb[s], i);
-                    } else {
-                        const float4 q = xf[s][i >> 2];
-                        xv = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
-                    }
-                    acc += (double)bf16x8_at(wv[s], i) * (double)xv;
-                }
-            }
+            for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv, i) * (double)xv[i];
         }
+        acc = wave_sum_f64_last(acc);
+        if (lane == 63) s_lp[wave] = acc;
     }
-    return acc;
-}
-
-// Logit e (exact bf16*x products, f64 sum, one rounding, + bias), published
-// by lane 0 as (tag << 32 | bits).  seen_raw: this workgroup's launch count as
-// loaded by lane 0 (the load stays in flight behind the logit's own loads).
-__device__ __forceinline__ void produce_logit(const FusedArgs& a, int e, int lane,
-                                              uint32_t seen_raw) {
-    const uint16_t* wr = a.router + (size_t)e * a.h;
-    double acc = a.x_bf16 ? logit_partial<true>(a, wr, lane) : logit_partial<false>(a, wr, lane);
-    acc = wave_sum_f64_last(acc);
-    const uint32_t tag = __builtin_amdgcn_readfirstlane(seen_raw) + 1u;
-    if (lane == 63) {
-        float l = (float)acc;
+    __syncthreads();
+    if (wave == 0 && lane < kNRep) {
+        double t = s_lp[0];
+        t += s_lp[1];
+        t += s_lp[2];
+        t += s_lp[3];
+        float l = (float)t;
         if (a.bias) l = l + a.bias[e];
-        st_u64(a.slots + e, ((unsigned long long)tag << 32) | __float_as_uint(l));
+        st_u64(a.slots + (size_t)lane * kRepStride + e,
+               ((unsigned long long)*s_tag << 32) | __float_as_uint(l));
     }
+    __syncthreads();  // s_lp is reused by the next logit
 }
 
-// Wave 0: obtain the routing (poll the published logits, rank, softmax) or
-// read the given one; writes s_idx/s_w.  Returns false on timeout.
-__device__ bool routing(const FusedArgs& a, int lane, uint32_t tag, int* s_idx, float* s_w) {
+// Routing state shared by the workgroup.
+struct RouteLDS {
+    alignas(16) float v[kMaxE];  // logits, NaN as -inf (kMaxE is a multiple of 16)
+    int rk[kWaves][kMaxE];    // partial ranks
+    int idx[kMaxK];           // expert of each slot (-1: invalid)
+    float w[kMaxK];           // probability of each slot (not renormalised)
+    int ok;
+};
+
+// Obtains the routing (wave 0 polls the published logits; the ranks are
+// counted by all waves; wave 0 ranks and computes the softmax) or reads the
+// given one.  Every thread calls it; r.idx / r.w / r.ok are valid after it.
+__device__ void routing(const FusedArgs& a, int wg, int wave, int lane, uint32_t tag,
+                        RouteLDS& r) {
     const int E = a.E, K = a.K;
     if (a.given_idx) {
-        if (lane < K) {
-            int e = a.given_idx[lane];
+        if (threadIdx.x < (unsigned)K) {
+            int e = a.given_idx[threadIdx.x];
             if (e < 0 || e >= E) {
                 flag_error(a.err, 1u);
                 e = -1;
             }
-            s_idx[lane] = e;
-            s_w[lane] = a.given_w[lane];
+            r.idx[threadIdx.x] = e;
+            r.w[threadIdx.x] = a.given_w[threadIdx.x];
         }
-        return true;
+        if (threadIdx.x == 0) r.ok = 1;
+        __syncthreads();
+        return;
     }
-    float v[4];
-    bool have[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        have[j] = (lane + 64 * j >= E);
-        v[j] = -INFINITY;
-    }
-    for (int it = 0;; ++it) {
-        bool all = true;
+    if (wave == 0) {
+        const unsigned long long* rep = a.slots + (size_t)(wg & (kNRep - 1)) * kRepStride;
+        float v[4];
+        bool have[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            if (!have[j]) {
-                const unsigned long long u = ld_u64(a.slots + lane + 64 * j);
-                if ((uint32_t)(u >> 32) == tag) {
-                    have[j] = true;
-                    const float f = __uint_as_float((uint32_t)u);
-                    v[j] = (f != f) ? -INFINITY : f;  // NaN ranks last
-                } else {
-                    all = false;
+            have[j] = (lane + 64 * j >= E);
+            v[j] = -INFINITY;
+        }
+        bool ok = true;
+        for (int it = 0;; ++it) {
+            bool all = true;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (!have[j]) {
+                    const unsigned long long u = ld_u64(rep + lane + 64 * j);
+                    if ((uint32_t)(u >> 32) == tag) {
+                        have[j] = true;
+                        const float f = __uint_as_float((uint32_t)u);
+                        v[j] = (f != f) ? -INFINITY : f;  // NaN ranks last
+                    } else {
+                        all = false;
+                    }
                 }
             }
+            if (__all(all)) break;
+            if (it >= a.spin_limit) {
+                flag_error(a.err, 2u);
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
         }
-        if (__all(all)) break;
-        if (it >= a.spin_limit) {
-            flag_error(a.err, 2u);
-            return false;
-        }
-        __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.v[lane + 64 * j] = v[j];  // -inf beyond E
+        if (lane == 0) r.ok = ok ? 1 : 0;
     }
-    int my_idx;
-    float w;
-    topk_softmax(v, E, K, a.norm, lane, my_idx, w);
+    __syncthreads();
+    // rank of expert i = experts ahead of it (descending logit, ties to the
+    // lower index); wave w counts over experts [j0, j1)
+    // (windows of 16 logits, read four at a time into registers)
+    for (int j0 = wave * 16; j0 < E; j0 += kWaves * 16) {
+        float4 win[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) win[q] = *reinterpret_cast<const float4*>(&r.v[j0 + 4 * q]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int i = lane + 64 * m;
+            if (i < E) {
+                const float my = r.v[i];
+                int cnt = j0 == wave * 16 ? 0 : r.rk[wave][i];
+                // padding beyond E is -inf at an index above i: never ahead
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float wv[4] = {win[q].x, win[q].y, win[q].z, win[q].w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int j = j0 + 4 * q + t;
+                        cnt += (int)(wv[t] > my) | ((int)(wv[t] == my) & (int)(j < i));
+                    }
+                }
+                r.rk[wave][i] = cnt;
+            }
+        }
+    }
+    if (wave * 16 >= E)
+        for (int m = 0; m < 4; ++m)
+            if (lane + 64 * m < E) r.rk[wave][lane + 64 * m] = 0;
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int i = lane + 64 * m;
+            if (i < E) {
+                int rank = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) rank += r.rk[w][i];
+                if (rank < K) r.idx[rank] = i;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Softmax probabilities of the selected experts (InferenceEngine.swift:
+// 501-506) into r.w, from the logits left in r.v by routing().  Wave 0 of
+// the workgroups that need the weights calls it (a barrier must follow before
+// other waves read r.w); given weights are kept as supplied.
+__device__ void routing_weights(const FusedArgs& a, int lane, RouteLDS& r) {
+    if (a.given_idx) return;
+    const int E = a.E, K = a.K;
+    float v[4], mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        v[m] = (lane + 64 * m < E) ? r.v[lane + 64 * m] : -INFINITY;
+        mx = fmaxf(mx, v[m]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) sum += (lane + 64 * m < E) ? expf(v[m] - mx) : 0.f;
+    const float inv = 1.0f / wave_sum(sum);
     if (lane < K) {
-        s_idx[lane] = my_idx;
-        s_w[lane] = w;
+        const int e = r.idx[lane];
+        r.w[lane] = expf(r.v[e] - mx) * inv;
     }
-    return true;
+}
+
+// Weight of slot k: the probability, renormalised over the selection in slot
+// order when norm_topk_prob is set (InferenceEngine.swift:514-517).  Given
+// weights are used as supplied.
+__device__ __forceinline__ float slot_weight(const FusedArgs& a, const float* s_w, int k) {
+    if (!a.norm || a.given_idx) return s_w[k];
+    float ssum = 0.f;
+    for (int r = 0; r < a.K; ++r) ssum = ssum + s_w[r];
+    return s_w[k] / ssum;
 }
 
 // ---- gate/up ---------------------------------------------------------------------
 
-// GSL = log2(group_size / 32): group of chunk c is c >> GSL.
-template <int CPL, int U, int GSL>
-__device__ void gate_up_role(const FusedArgs& a, const Layout& L, int k, int rb, int wave,
-                             int lane, const XChunk (&xc)[CPL], float inv, int e) {
-    const uint8_t* blk = a.layer_base + (uint64_t)e * a.expert_bytes;
-    const uint8_t* gw_p = blk + L.gate_w;
-    const uint8_t* uw_p = blk + L.up_w;
-    const uint8_t* gs_p = blk + L.gate_s;
-    const uint8_t* gb_p = blk + L.gate_b;
-    const uint8_t* us_p = blk + L.up_s;
-    const uint8_t* ub_p = blk + L.up_b;
-    const LaneMap m = lane_map(lane, a.Cg, a.rpi_g);
+// Lane geometry of a gate/up row: rows of C >= 64 chunks give a lane chunks
+// lane, lane+64, ...; shorter rows share a wave step, seg lanes (a power of
+// two) per row.
+struct GUGeo {
+    int q;       // row slot within a wave step
+    int c0;      // first chunk
+    bool ok;     // lane has a chunk
+    bool writer; // last lane of its segment (holds the row total)
+};
+__device__ __forceinline__ GUGeo gu_geo(int lane, int C, int seg) {
+    GUGeo m;
+    m.q = lane / seg;
+    m.c0 = lane - m.q * seg;
+    m.ok = m.c0 < C;
+    m.writer = (lane & (seg - 1)) == seg - 1;
+    return m;
+}
+
+template <int CPL, int UG>
+struct GUTile {
+    uint4 gw[UG][CPL], uw[UG][CPL];
+    uint32_t gs[UG][CPL], gb[UG][CPL], us[UG][CPL], ub[UG][CPL];
+};
+
+// GSL = log2(group_size / 32): the group of chunk c is c >> GSL.
+template <int CPL, int UG, int GSL>
+__device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int e, int row0,
+                                        const GUGeo& m, GUTile<CPL, UG>& t) {
+    // e is wave-uniform: keep the sub-block bases in scalar registers and
+    // address with 32-bit lane offsets
+    const uint8_t* blk = a.layer_base + (uint64_t)__builtin_amdgcn_readfirstlane(e) * a.expert_bytes;
+    const uint8_t* gw_b = blk + L.gate_w;
+    const uint8_t* uw_b = blk + L.up_w;
+    const uint8_t* gs_b = blk + L.gate_s;
+    const uint8_t* gb_b = blk + L.gate_b;
+    const uint8_t* us_b = blk + L.up_s;
+    const uint8_t* ub_b = blk + L.up_b;
     const uint32_t groups = (uint32_t)a.h >> (5 + GSL);
     const uint32_t row_bytes = (uint32_t)a.h / 2;
-    const int row0 = (rb * kWaves + wave) * U * a.rpi_g + m.q;
-
-    uint4 gw[U][CPL], uw[U][CPL];
-    uint32_t gsc[U][CPL], gbi[U][CPL], usc[U][CPL], ubi[U][CPL];
-    bool okv[U][CPL], hi[U][CPL];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < UG; ++u) {
+        const uint32_t rc = (uint32_t)min(row0 + u * a.rpi_g, a.I - 1);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t cc = (uint32_t)min(m.c0 + 64 * j, a.Cg - 1);
+            const uint32_t wo = rc * row_bytes + cc * 16u;
+            const uint32_t sbw = sb_word(rc * groups + (cc >> GSL));
+            t.gw[u][j] = *reinterpret_cast<const uint4*>(gw_b + wo);
+            t.uw[u][j] = *reinterpret_cast<const uint4*>(uw_b + wo);
+            t.gs[u][j] = *reinterpret_cast<const uint32_t*>(gs_b + sbw);
+            t.gb[u][j] = *reinterpret_cast<const uint32_t*>(gb_b + sbw);
+            t.us[u][j] = *reinterpret_cast<const uint32_t*>(us_b + sbw);
+            t.ub[u][j] = *reinterpret_cast<const uint32_t*>(ub_b + sbw);
+        }
+    }
+}
+
+template <int CPL, int UG, int GSL>
+__device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, const GUGeo& m,
+                                           const GUTile<CPL, UG>& t, const XChunk (&xc)[CPL],
+                                           float inv) {
+    const uint32_t groups = (uint32_t)a.h >> (5 + GSL);
+    const NibK nk = nib_consts();
+#pragma unroll
+    for (int u = 0; u < UG; ++u) {
         const int row = row0 + u * a.rpi_g;
         const uint32_t rc = (uint32_t)min(row, a.I - 1);
+        float pg = 0.f, pu = 0.f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = m.c0 + 64 * j;
             const uint32_t cc = (uint32_t)min(c, a.Cg - 1);
-            okv[u][j] = m.ok && row < a.I && c < a.Cg;
-            const uint64_t wo = (uint64_t)(rc * row_bytes + cc * 16u);
-            const SBIdx sb = sb_index(rc * groups + (cc >> GSL));
-            hi[u][j] = sb.hi;
-            gw[u][j] = *reinterpret_cast<const uint4*>(gw_p + wo);
-            uw[u][j] = *reinterpret_cast<const uint4*>(uw_p + wo);
-            gsc[u][j] = *reinterpret_cast<const uint32_t*>(gs_p + sb.word);
-            gbi[u][j] = *reinterpret_cast<const uint32_t*>(gb_p + sb.word);
-            usc[u][j] = *reinterpret_cast<const uint32_t*>(us_p + sb.word);
-            ubi[u][j] = *reinterpret_cast<const uint32_t*>(ub_p + sb.word);
+            const uint32_t sel = sb_sel(rc * groups + (cc >> GSL));
+            const float tg = chunk_term(t.gw[u][j], t.gs[u][j], t.gb[u][j], sel, xc[j], nk);
+            const float tu = chunk_term(t.uw[u][j], t.us[u][j], t.ub[u][j], sel, xc[j], nk);
+            const bool ok = m.ok && c < a.Cg;
+            pg += ok ? tg : 0.f;
+            pu += ok ? tu : 0.f;
         }
+        pg = seg_sum(pg * inv, a.seg_g);
+        pu = seg_sum(pu * inv, a.seg_g);
+        if (m.writer && row < a.I)
+            st_f32(a.act + (size_t)k * a.I + row, (pg / (1.0f + expf(-pg))) * pu);  // Shaders.metal:148
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        float pg = 0.f, pu = 0.f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const float dg = nib_dot32(gw[u][j], xc[j]) - xc[j].off;
-            const float du = nib_dot32(uw[u][j], xc[j]) - xc[j].off;
-            const float tg = fmaf(sb_pick(gsc[u][j], hi[u][j]), dg,
-                                  sb_pick(gbi[u][j], hi[u][j]) * xc[j].xs);
-            const float tu = fmaf(sb_pick(usc[u][j], hi[u][j]), du,
-                                  sb_pick(ubi[u][j], hi[u][j]) * xc[j].xs);
-            pg += okv[u][j] ? tg : 0.f;
-            pu += okv[u][j] ? tu : 0.f;
-        }
-        pg = seg_sum(pg, m.seg);
-        pu = seg_sum(pu, m.seg);
-        // the segment's total is in its last lane; that lane's row slot is
-        // m.q when rows share the wave, else 0
-        const int row = row0 - m.q + m.wq + u * a.rpi_g;
-        if (m.writer && row < a.I) {
-            const float gv = pg * inv, uv = pu * inv;
-            st_f32(a.act + (size_t)k * a.I + row, (gv / (1.0f + expf(-gv))) * uv);  // Shaders.metal:148
-        }
+}
+
+// Number of row blocks rb in [0, n) with rb % kSub == j.
+__device__ __forceinline__ uint32_t count_mod(int n, int j) {
+    return n > j ? (uint32_t)((n - j + kSub - 1) / kSub) : 0u;
+}
+
+// gate/up workgroup (slot k, row block rb): all loads at once, then compute,
+// then one completion count on sub-counter (k, rb % kSub).
+template <int CPL, int UG, int GSL>
+__device__ void gu_role(const FusedArgs& a, const Layout& L, int k, int rb, int wave, int lane,
+                        int e, const XChunk (&xc)[CPL], float inv) {
+    const GUGeo m = gu_geo(lane, a.Cg, a.seg_g);
+    const int row0 = rb * a.rows_tile + wave * a.rpi_g * UG + m.q;
+    if (e >= 0) {
+        GUTile<CPL, UG> t;
+        gu_load<CPL, UG, GSL>(a, L, e, row0, m, t);
+        gu_compute<CPL, UG, GSL>(a, k, row0, m, t, xc, inv);
     }
+    wait_all_mem();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        add_u32(a.gu_cnt + ((size_t)k * kSub + (rb & (kSub - 1))) * kCntStride, 1u);
 }
 
 // ---- down + combine ----------------------------------------------------------------
 
-struct DownTile {
-    uint4 w[kRS];
-    uint32_t s[kRS], b[kRS];
-    bool hi[kRS], ok[kRS];
+struct DNTile {
+    uint4 w[kRT];
+    uint32_t s[kRT], b[kRT];
 };
 
-// task t = (slot k = t / Sc, column slice j = t % Sc) over this block's rows;
-// loads are unconditional at clamped addresses, invalid lanes masked later
+// Lane geometry of one 64-lane unit of the down projection: the unit covers
+// spu whole slots of Cp (< 64) padded chunks, or 64-chunk block `blk` of one
+// slot (Cp >= 64).
+struct DNUnit {
+    int k;        // slot
+    int blk;      // 64-chunk block within the slot
+    int c;        // chunk
+    bool ok;      // real (slot, chunk)
+    bool writer;  // last lane of its segment
+};
+__device__ __forceinline__ DNUnit dn_unit(const FusedArgs& a, int u, int lane) {
+    DNUnit d;
+    if (a.Cp < 64) {
+        d.k = u * a.spu + (lane >> a.cp_log2);
+        d.blk = 0;
+        d.c = lane & (a.Cp - 1);
+    } else {
+        d.k = u / a.nb;
+        d.blk = u - d.k * a.nb;
+        d.c = d.blk * 64 + lane;
+    }
+    d.ok = d.k < a.K && d.c < a.Cd;
+    d.writer = (lane & (a.seg_d - 1)) == a.seg_d - 1;
+    return d;
+}
+
 template <int GSL>
-__device__ __forceinline__ void load_down_tile(const FusedArgs& a, const Layout& L, int t, int T,
-                                               int row_base, const LaneMap& m, const int* s_idx,
-                                               DownTile& d) {
-    const int tt = min(t, T - 1);
-    const int k = tt / a.Sc, j = tt - k * a.Sc;
-    const int e = s_idx[k];
-    const int c = m.c0 + 64 * j;
-    const uint32_t cc = (uint32_t)min(c, a.Cd - 1);
-    const bool ok0 = (t < T) && (e >= 0) && m.ok && c < a.Cd;
+__device__ __forceinline__ void dn_load(const FusedArgs& a, const Layout& L, const DNUnit& d,
+                                        int e, int row0, DNTile& t) {
     const uint8_t* blk = a.layer_base + (uint64_t)(e < 0 ? 0 : e) * a.expert_bytes;
-    const uint8_t* w_p = blk + L.down_w;
-    const uint8_t* s_p = blk + L.down_s;
-    const uint8_t* b_p = blk + L.down_b;
     const uint32_t groups = (uint32_t)a.I >> (5 + GSL);
     const uint32_t row_bytes = (uint32_t)a.I / 2;
+    const uint32_t cc = (uint32_t)min(d.c, a.Cd - 1);
 #pragma unroll
-    for (int s = 0; s < kRS; ++s) {
-        const int row = row_base + s * a.rpi_d + m.q;
-        const uint32_t rc = (uint32_t)min(row, a.h - 1);
-        d.ok[s] = ok0 && row < a.h;
-        const SBIdx sb = sb_index(rc * groups + (cc >> GSL));
-        d.hi[s] = sb.hi;
-        d.w[s] = *reinterpret_cast<const uint4*>(w_p + (uint64_t)(rc * row_bytes + cc * 16u));
-        d.s[s] = *reinterpret_cast<const uint32_t*>(s_p + sb.word);
-        d.b[s] = *reinterpret_cast<const uint32_t*>(b_p + sb.word);
+    for (int r = 0; r < kRT; ++r) {
+        const uint32_t rc = (uint32_t)min(row0 + r, a.h - 1);
+        const uint32_t sbw = sb_word(rc * groups + (cc >> GSL));
+        t.w[r] = *reinterpret_cast<const uint4*>(blk + L.down_w + (uint64_t)rc * row_bytes + cc * 16u);
+        t.s[r] = *reinterpret_cast<const uint32_t*>(blk + L.down_s + sbw);
+        t.b[r] = *reinterpret_cast<const uint32_t*>(blk + L.down_b + sbw);
     }
 }
 
-// Waits until every gate/up workgroup of slot k has finished: sub-counter i
-// gains the number of those workgroups with rb % kActSub == i per launch.
-__device__ __forceinline__ bool wait_slot(const FusedArgs& a, int k, int lane, uint32_t tag) {
-    const uint32_t n = (uint32_t)a.gu_per_slot;
-    const uint32_t per = n / kActSub + ((uint32_t)lane < n % kActSub ? 1u : 0u);
-    const uint32_t want = tag * per;
-    const uint32_t* p = a.act_cnt + ((size_t)k * kActSub + (lane & (kActSub - 1))) * kActCntStride;
-    for (int it = 0;; ++it) {
-        const bool done = lane >= kActSub || ld_u32(p) == want;
-        if (__all(done)) return true;
-        if (it >= a.spin_limit) return false;
-        __builtin_amdgcn_s_sleep(4);
-    }
-}
-
-__device__ __forceinline__ void compute_down_tile(const FusedArgs& a, int t, int lane,
-                                                  const LaneMap& m, const int* s_idx,
-                                                  const DownTile& d, float* s_part, uint32_t tag,
-                                                  bool& ok_run) {
-    const int k = t / a.Sc, j = t - k * a.Sc;
-    const int R2 = kRS * a.rpi_d;
-    float* part = s_part + (k * a.Sc + j) * R2;
-    if (s_idx[k] < 0 || !ok_run || !wait_slot(a, k, lane, tag)) {
-        if (ok_run && s_idx[k] >= 0) {
-            flag_error(a.err, 4u);
-            ok_run = false;
+// Waits until every gate/up tile of slots [k0, k0 + n) has been counted.
+__device__ bool wait_slots(const FusedArgs& a, int k0, int n, int lane, uint32_t tag) {
+    for (int base = 0; base < n; base += 64 / kSub) {
+        const int k = k0 + base + lane / kSub, j = lane & (kSub - 1);
+        const bool mine = (base + lane / kSub) < n && k < a.K;
+        const uint32_t want = mine ? tag * count_mod(a.tiles_per_slot, j) : 0u;
+        const uint32_t* p = a.gu_cnt + ((size_t)j * kCntStride) + (size_t)(mine ? k : 0) * kSub * kCntStride;
+        for (int it = 0;; ++it) {
+            const bool done = !mine || ld_u32(p) == want;
+            if (__all(done)) break;
+            if (it >= a.spin_limit) return false;
+            __builtin_amdgcn_s_sleep(2);
         }
-        for (int r = lane; r < R2; r += 64) part[r] = 0.f;
-        return;
     }
-    const int c = m.c0 + 64 * j;
-    float v[1][32];
-    load_chunk_coherent(a.act + (size_t)k * a.I, min(c, a.Cd - 1), m.ok && c < a.Cd, v[0]);
-    XChunk xc[1];
-    const float inv = scale_and_prep<1>(v, xc);
-#pragma unroll
-    for (int s = 0; s < kRS; ++s) {
-        const float dd = nib_dot32(d.w[s], xc[0]) - xc[0].off;
-        float p = fmaf(sb_pick(d.s[s], d.hi[s]), dd, sb_pick(d.b[s], d.hi[s]) * xc[0].xs);
-        p = d.ok[s] ? p : 0.f;
-        p = seg_sum(p, m.seg);
-        if (m.writer) part[s * a.rpi_d + m.wq] = p * inv;
-    }
+    return true;
 }
+
+// Position of an item (unit, sub-tile) in a wave's sequence: items run
+// through the wave's units (wave, wave + kWaves, ...) and, within a unit,
+// through the nsub sub-tiles of kRT rows.
+struct ItemPos {
+    int u, st;
+    __device__ void next(int nsub) {
+        if (++st == nsub) {
+            st = 0;
+            u += kWaves;
+        }
+    }
+};
 
 template <int GSL>
-__device__ void down_role(const FusedArgs& a, const Layout& L, int dblk, int wave, int lane,
-                          const int* s_idx, const float* s_w, float* s_part, uint32_t tag,
-                          bool ok_run) {
-    const int R2 = kRS * a.rpi_d;
-    const int row_base = dblk * R2;
-    const int T = a.K * a.Sc;
-    const LaneMap m = lane_map(lane, a.Cd, a.rpi_d);
-    // two tiles in flight per wave: tasks wave, wave+4, wave+8, ...
-    DownTile A, B;
-    load_down_tile<GSL>(a, L, wave, T, row_base, m, s_idx, A);
-    load_down_tile<GSL>(a, L, wave + kWaves, T, row_base, m, s_idx, B);
-    for (int t = wave; t < T; t += 2 * kWaves) {
-        compute_down_tile(a, t, lane, m, s_idx, A, s_part, tag, ok_run);
-        load_down_tile<GSL>(a, L, t + 2 * kWaves, T, row_base, m, s_idx, A);
-        if (t + kWaves < T) {
-            compute_down_tile(a, t + kWaves, lane, m, s_idx, B, s_part, tag, ok_run);
-            load_down_tile<GSL>(a, L, t + 3 * kWaves, T, row_base, m, s_idx, B);
+__device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave, int lane,
+                        RouteLDS& r, float* s_part, uint32_t tag) {
+    const bool ok_run = r.ok != 0;
+    const int row_base = dblk * a.Rd;
+    const int nsub = a.Rd / kRT;
+    const int my_units = (a.units - wave + kWaves - 1) / kWaves;
+    const int n_items = my_units * nsub;
+    const uint32_t groups = (uint32_t)a.I >> (5 + GSL);
+    auto expert_at = [&](const DNUnit& d) {
+        const int e = d.ok ? r.idx[d.k] : -1;
+        return (ok_run && e >= 0) ? e : -1;
+    };
+    // two items in flight: the first two are loaded as soon as the routing is known
+    DNTile A, B;
+    ItemPos pa{wave, 0}, pb{wave, 0};
+    pb.next(nsub);
+    if (n_items > 0) {
+        const DNUnit d = dn_unit(a, pa.u, lane);
+        dn_load<GSL>(a, L, d, expert_at(d), row_base, A);
+    }
+    if (n_items > 1) {
+        const DNUnit d = dn_unit(a, pb.u, lane);
+        dn_load<GSL>(a, L, d, expert_at(d), row_base + pb.st * kRT, B);
+    }
+    // keep the weight loads above the waits below (the compiler may otherwise
+    // sink them to their first use)
+    asm volatile("" ::: "memory");
+    if (wave == 0) routing_weights(a, lane, r);  // read by the combine after a barrier
+    float res = 0.f;
+    if ((int)threadIdx.x < a.Rd && row_base + (int)threadIdx.x < a.h && a.residual)
+        res = a.residual[row_base + threadIdx.x];
+    const NibK nk = nib_consts();
+    int cur = -1;
+    DNUnit d{};
+    XChunk xc[1];
+    float inv = 1.f;
+    bool live = false;  // this lane's unit is ready and routed
+    auto process = [&](const ItemPos& p, const DNTile& t) {
+        if (p.u != cur) {
+            cur = p.u;
+            d = dn_unit(a, p.u, lane);
+            int k0, n;
+            if (a.Cp < 64) {
+                k0 = p.u * a.spu;
+                n = min(a.spu, a.K - k0);
+            } else {
+                k0 = d.k;
+                n = 1;
+            }
+            bool ready = ok_run;
+            if (ready && !wait_slots(a, k0, n, lane, tag)) {
+                flag_error(a.err, 4u);
+                ready = false;
+            }
+            live = ready && expert_at(d) >= 0;
+            float v[1][32];
+            load_chunk_coherent(a.act + (size_t)(d.k < a.K ? d.k : 0) * a.I,
+                                min(d.c, a.Cd - 1), live, v[0]);
+            inv = lane_scale_prep<1>(v, xc);
+        }
+        const uint32_t cc = (uint32_t)min(d.c, a.Cd - 1);
+        float* part = s_part + (d.k * a.nb + d.blk) * a.Rd + p.st * kRT;
+#pragma unroll
+        for (int rr = 0; rr < kRT; ++rr) {
+            const uint32_t rc = (uint32_t)min(row_base + p.st * kRT + rr, a.h - 1);
+            float q = chunk_term(t.w[rr], t.s[rr], t.b[rr], sb_sel(rc * groups + (cc >> GSL)), xc[0], nk) * inv;
+            q = live ? q : 0.f;
+            q = seg_sum(q, a.seg_d);
+            if (d.writer && d.k < a.K) part[rr] = q;
+        }
+    };
+    for (int i = 0; i < n_items; i += 2) {
+        process(pa, A);
+        pa.next(nsub);
+        pa.next(nsub);
+        if (i + 2 < n_items) {
+            const DNUnit dn = dn_unit(a, pa.u, lane);
+            dn_load<GSL>(a, L, dn, expert_at(dn), row_base + pa.st * kRT, A);
+        }
+        if (i + 1 < n_items) {
+            process(pb, B);
+            pb.next(nsub);
+            pb.next(nsub);
+            if (i + 3 < n_items) {
+                const DNUnit dn = dn_unit(a, pb.u, lane);
+                dn_load<GSL>(a, L, dn, expert_at(dn), row_base + pb.st * kRT, B);
+            }
         }
     }
     __syncthreads();
-    // combine in slot order, column slices summed in order (Shaders.metal:371-374)
-    for (int r = threadIdx.x; r < R2; r += blockDim.x) {
-        const int row = row_base + r;
+    // combine in slot order, 64-chunk blocks summed in order (Shaders.metal:371-374)
+    for (int rr = threadIdx.x; rr < a.Rd; rr += kThreads) {
+        const int row = row_base + rr;
         if (row >= a.h) continue;
-        float acc = a.residual ? a.residual[row] : 0.f;
+        float acc = (rr == (int)threadIdx.x) ? res : (a.residual ? a.residual[row] : 0.f);
         for (int k = 0; k < a.K; ++k) {
             float y = 0.f;
-            for (int j = 0; j < a.Sc; ++j) y += s_part[(k * a.Sc + j) * R2 + r];
-            acc = fmaf(s_w[k], y, acc);
+            for (int b = 0; b < a.nb; ++b) y += s_part[(k * a.nb + b) * a.Rd + rr];
+            acc = fmaf(slot_weight(a, r.w, k), y, acc);
         }
         a.out[row] = acc;
     }
@@ -510,67 +702,54 @@ __device__ void down_role(const FusedArgs& a, const Layout& L, int dblk, int wav
 
 // ---- the kernel --------------------------------------------------------------------
 
-template <int CPL, int U, int GSL>
-__global__ __launch_bounds__(256, CPL == 1 ? 4 : 1) void moe_decode_kernel(FusedArgs a) {
-    __shared__ int s_idx[kMaxK];
-    __shared__ float s_w[kMaxK];
-    __shared__ int s_ok;
+template <int CPL, int UG, int GSL>
+__global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
+    __shared__ RouteLDS r;
     __shared__ uint32_t s_tag;
-    extern __shared__ float s_part[];  // down role: [K][Sc][R2]
+    __shared__ double s_lp[4];
+    extern __shared__ float s_part[];  // down role: [K][nb][Rd]
     const int wg = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const bool is_gu = wg < a.n_gu;
 
     // this launch's number, as counted by this workgroup (all agree)
-    uint32_t tag = 0;
-    if (wave == 0) {
-        uint32_t s = 0;
-        if (lane == 0) s = ld_u32(a.seen + wg);
-        if (!a.given_idx)
-            for (int e = wg; e < a.E; e += gridDim.x) produce_logit(a, e, lane, s);
-        tag = __builtin_amdgcn_readfirstlane(s) + 1u;
-    }
+    if (threadIdx.x == 0) s_tag = ld_u32(a.seen + wg) + 1u;
+    __syncthreads();
+    const uint32_t tag = s_tag;
+    if (!a.given_idx)
+        for (int e = wg; e < a.E; e += gridDim.x) produce_logit(a, e, wave, lane, &s_tag, s_lp);
 
     // the input vector does not depend on the routing: prepare it meanwhile
     XChunk xc[CPL];
     float inv = 1.f;
     if (is_gu) {
-        const LaneMap m = lane_map(lane, a.Cg, a.rpi_g);
+        const GUGeo m = gu_geo(lane, a.Cg, a.seg_g);
         float v[CPL][32];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = m.c0 + 64 * j;
             load_chunk(a.x, a.x_bf16, min(c, a.Cg - 1), m.ok && c < a.Cg, v[j]);
         }
-        inv = scale_and_prep<CPL>(v, xc);
+        inv = lane_scale_prep<CPL>(v, xc);
     }
 
-    if (wave == 0) {
-        const bool ok = routing(a, lane, tag, s_idx, s_w);
-        if (lane == 0) {
-            s_ok = ok ? 1 : 0;
-            s_tag = tag;
-        }
-        if (ok && wg == 0 && lane < a.K) {
-            if (a.user_idx) a.user_idx[lane] = s_idx[lane];
-            if (a.user_w) a.user_w[lane] = s_w[lane];
-        }
-    }
-    __syncthreads();
-    const bool ok_run = s_ok != 0;
-    tag = s_tag;
-    const Layout L(a.h, a.I, a.gs);
-
-    if (is_gu) {
-        const int k = wg / a.gu_per_slot, rb = wg - k * a.gu_per_slot;
-        const int e = s_idx[k];
-        if (ok_run && e >= 0) gate_up_role<CPL, U, GSL>(a, L, k, rb, wave, lane, xc, inv, e);
-        wait_all_mem();
+    routing(a, wg, wave, lane, tag, r);
+    const bool ok_run = r.ok != 0;
+    if (wg == 0 && ok_run && (a.user_idx || a.user_w)) {
+        if (wave == 0) routing_weights(a, lane, r);
         __syncthreads();
-        if (threadIdx.x == 0)
-            add_u32(a.act_cnt + ((size_t)k * kActSub + (rb & (kActSub - 1))) * kActCntStride, 1u);
+        if ((int)threadIdx.x < a.K) {
+            if (a.user_idx) a.user_idx[threadIdx.x] = r.idx[threadIdx.x];
+            if (a.user_w) a.user_w[threadIdx.x] = slot_weight(a, r.w, threadIdx.x);
+        }
+    }
+    const Layout L(a.h, a.I, a.gs);
+    if (is_gu) {
+        const int k = wg / a.tiles_per_slot, rb = wg - k * a.tiles_per_slot;
+        const int e = ok_run ? r.idx[k] : -1;
+        gu_role<CPL, UG, GSL>(a, L, k, rb, wave, lane, e, xc, inv);
     } else {
-        down_role<GSL>(a, L, wg - a.n_gu, wave, lane, s_idx, s_w, s_part, tag, ok_run);
+        dn_role<GSL>(a, L, wg - a.n_gu, wave, lane, r, s_part, tag);
     }
     if (threadIdx.x == 0) st_u32(a.seen + wg, tag);
 }
@@ -594,18 +773,20 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* blk, ProjVi
     }
 }
 
-// Several rows share a wave step only when the row's chunk count divides 64
-// (a power of two), so each row owns an aligned power-of-two lane segment.
-inline int rows_per_step(int C) { return (C < 64 && 64 % C == 0) ? 64 / C : 1; }
-constexpr int gu_steps(int cpl) { return cpl == 1 ? 4 : cpl == 2 ? 2 : 1; }
+inline int pow2_ceil(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+// gate/up rows per wave: about eight 128-bit weight loads per lane
+constexpr int gu_rows(int cpl) { return cpl == 1 ? 4 : cpl == 2 ? 2 : 1; }
 
 template <int CPL, int GSL>
 int launch_shape(const FusedArgs& a, hipStream_t st) {
-    const int R2 = kRS * a.rpi_d;
-    const size_t lds = sizeof(float) * (size_t)a.K * a.Sc * R2;
+    const size_t lds = sizeof(float) * (size_t)a.K * a.nb * a.Rd;
     if (lds > 64 * 1024) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL((moe_decode_kernel<CPL, gu_steps(CPL), GSL>),
-                       dim3((unsigned)(a.n_gu + a.n_dn)), dim3(64 * kWaves), lds, st, a);
+    hipLaunchKernelGGL((moe_decode_kernel<CPL, gu_rows(CPL), GSL>),
+                       dim3((unsigned)(a.n_gu + a.n_dn)), dim3(kThreads), lds, st, a);
     return (int)hipGetLastError();
 }
 
@@ -622,17 +803,38 @@ int launch_cpl(const FusedArgs& a, hipStream_t st) {
 }  // namespace
 
 int decode_grid(FusedArgs& a) {
-    const int cpl = (a.h / 32 + 63) / 64;
+    // gate/up
     a.Cg = a.h / 32;
-    a.rpi_g = rows_per_step(a.Cg);
-    const int rows_gu = kWaves * gu_steps(cpl) * a.rpi_g;
-    a.gu_per_slot = (a.I + rows_gu - 1) / rows_gu;
-    a.n_gu = a.K * a.gu_per_slot;
+    if (a.Cg >= 64) {
+        a.seg_g = 64;
+        a.rpi_g = 1;
+    } else {
+        a.seg_g = pow2_ceil(a.Cg);
+        a.rpi_g = 64 / a.seg_g;
+    }
+    const int cpl = (a.Cg + 63) / 64;
+    a.rows_tile = kWaves * a.rpi_g * gu_rows(cpl);
+    a.tiles_per_slot = (a.I + a.rows_tile - 1) / a.rows_tile;
+    a.n_gu = a.K * a.tiles_per_slot;
+    // down
     a.Cd = a.I / 32;
-    a.rpi_d = rows_per_step(a.Cd);
-    a.Sc = a.Cd >= 64 ? (a.Cd + 63) / 64 : 1;
-    const int R2 = kRS * a.rpi_d;
-    a.n_dn = (a.h + R2 - 1) / R2;
+    if (a.Cd < 64) {
+        a.Cp = pow2_ceil(a.Cd);
+        a.cp_log2 = __builtin_ctz(a.Cp);
+        a.seg_d = a.Cp;
+        a.nb = 1;
+        a.spu = 64 / a.Cp;
+        a.units = (a.K + a.spu - 1) / a.spu;
+    } else {
+        a.Cp = (a.Cd + 63) / 64 * 64;
+        a.seg_d = 64;
+        a.nb = a.Cp / 64;
+        a.spu = 1;
+        a.units = a.K * a.nb;
+    }
+    const int nsub = max(1, (a.h + kDnTarget * kRT - 1) / (kDnTarget * kRT));
+    a.Rd = kRT * nsub;
+    a.n_dn = (a.h + a.Rd - 1) / a.Rd;
     return a.n_gu + a.n_dn;
 }
 

@@ -63,20 +63,40 @@ __device__ __forceinline__ void prep_chunk(const float* v, XChunk& c) {
     c.xs = xs;
 }
 
+// Masks and the f16 magic of the nibble expansion, held in registers so that
+// each expansion is one v_and_or_b32 (masks in SGPRs, magic in a VGPR; with
+// literal operands the compiler emits a separate AND and OR).
+struct NibK {
+    uint32_t lo, hi, mg;
+};
+__device__ __forceinline__ NibK nib_consts() {
+    NibK k;
+    k.lo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+    k.hi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(k.mg));
+    return k;
+}
+
 // sum over 32 columns of (1024+n)*x-pairs, i.e. sum n_c x_c + c.off
-__device__ __forceinline__ float nib_dot32(const uint4& w, const XChunk& c) {
-    constexpr uint32_t kLo = 0x000F000Fu, kHi = 0x00F000F0u, kMagic = 0x64006400u;
+__device__ __forceinline__ float nib_dot32(const uint4& w, const XChunk& c, const NibK& k) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t v = ws[i], v8 = v >> 8;
-        a0 = dot2_f16((v & kLo) | kMagic, c.X[4 * i + 0], a0);
-        a1 = dot2_f16((v & kHi) | kMagic, c.X[4 * i + 1], a1);
-        a0 = dot2_f16((v8 & kLo) | kMagic, c.X[4 * i + 2], a0);
-        a1 = dot2_f16((v8 & kHi) | kMagic, c.X[4 * i + 3], a1);
+        a0 = dot2_f16((v & k.lo) | k.mg, c.X[4 * i + 0], a0);
+        a1 = dot2_f16((v & k.hi) | k.mg, c.X[4 * i + 1], a1);
+        a0 = dot2_f16((v8 & k.lo) | k.mg, c.X[4 * i + 2], a0);
+        a1 = dot2_f16((v8 & k.hi) | k.mg, c.X[4 * i + 3], a1);
     }
     return a0 + a1;
+}
+
+// v_perm_b32 selectors that move the low / high bf16 of a dword into the
+// upper half of an f32 and zero the lower half (selector byte 0x0C = 0x00).
+constexpr uint32_t kSelLo = 0x01000C0Cu, kSelHi = 0x03020C0Cu;
+__device__ __forceinline__ float bf16_pick(uint32_t w, uint32_t sel) {
+    return __uint_as_float(__builtin_amdgcn_perm(w, w, sel));
 }
 
 // Power-of-two scale that maps max|x| into [2^13, 2^14), so every scaled
@@ -123,13 +143,30 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
 // Sum over aligned segments of `seg` lanes (a power of two, 2..64).  The
 // segment's total lands in its last lane (lane % seg == seg - 1); other lanes
 // keep partial sums.  The order is fixed, so results are deterministic.
+// Branch-free: every step runs and the steps beyond `seg` add a term masked
+// to +0 (a run-time width would otherwise compile to a branch per step).
 __device__ __forceinline__ float seg_sum(float v, int seg) {
+    const uint32_t m4 = seg >= 4 ? ~0u : 0u, m8 = seg >= 8 ? ~0u : 0u;
+    const uint32_t m16 = seg >= 16 ? ~0u : 0u, m32 = seg >= 32 ? ~0u : 0u;
+    const uint32_t m64 = seg >= 64 ? ~0u : 0u;
     v += dpp_f32<kDppXor1>(v, v);
-    if (seg >= 4) v += dpp_f32<kDppXor2>(v, v);
-    if (seg >= 8) v += dpp_f32<kDppRor4>(v, v);
-    if (seg >= 16) v += dpp_f32<kDppRor8>(v, v);
-    if (seg >= 32) v += dpp_f32<kDppBcast15, 0xA>(0.f, v);
-    if (seg >= 64) v += dpp_f32<kDppBcast31, 0xC>(0.f, v);
+    v += __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v), __float_as_uint(v)) & m4);
+    v += __uint_as_float(dpp_u32<kDppRor4>(__float_as_uint(v), __float_as_uint(v)) & m8);
+    v += __uint_as_float(dpp_u32<kDppRor8>(__float_as_uint(v), __float_as_uint(v)) & m16);
+    v += __uint_as_float(dpp_u32<kDppBcast15, 0xA>(0u, __float_as_uint(v)) & m32);
+    v += __uint_as_float(dpp_u32<kDppBcast31, 0xC>(0u, __float_as_uint(v)) & m64);
+    return v;
+}
+
+// Sum over aligned segments of SEG lanes, SEG known at compile time.
+template <int SEG>
+__device__ __forceinline__ float seg_sum_c(float v) {
+    v += dpp_f32<kDppXor1>(v, v);
+    if (SEG >= 4) v += dpp_f32<kDppXor2>(v, v);
+    if (SEG >= 8) v += dpp_f32<kDppRor4>(v, v);
+    if (SEG >= 16) v += dpp_f32<kDppRor8>(v, v);
+    if (SEG >= 32) v += dpp_f32<kDppBcast15, 0xA>(0.f, v);
+    if (SEG >= 64) v += dpp_f32<kDppBcast31, 0xC>(0.f, v);
     return v;
 }
 
@@ -146,7 +183,7 @@ __device__ __forceinline__ double wave_sum_f64_last(double v) {
 
 // Sum over the wave, returned to every lane (uniform).
 __device__ __forceinline__ float wave_sum(float v) {
-    return readlane_f32(seg_sum(v, 64), 63);
+    return readlane_f32(seg_sum_c<64>(v), 63);
 }
 
 // Max over the wave, returned to every lane (uniform).

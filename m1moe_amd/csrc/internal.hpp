@@ -47,21 +47,29 @@ struct FusedArgs {
     float* user_w;
     // hand-off state.  It starts at zero and is never reset between launches:
     // every workgroup counts its own launches in seen[wg], so all workgroups
-    // agree on the launch number without communicating.
-    unsigned long long* slots;   // [E] published logits, tagged with the launch number
-    float* act;                  // [K][I]
-    uint32_t* act_cnt;           // [K][kActSub] monotonic, kActCntStride apart
+    // agree on the launch number ("tag") without communicating.
+    unsigned long long* slots;   // [kNRep][kRepStride] logits tagged with the launch number
+    float* act;                  // [K][I] silu(gate) * up
+    uint32_t* gu_cnt;            // [K][kSub] monotonic tile counters, kCntStride apart
     uint32_t* seen;              // [grid] launches completed by each workgroup
     uint32_t* err;               // sticky device error flag
     int32_t h, E, K, I, gs, norm, x_bf16, spin_limit;
-    // work decomposition (decode_grid)
-    int32_t n_gu, gu_per_slot, n_dn;
-    int32_t Cg, rpi_g;           // gate/up: 32-column chunks per row, rows per wave step
-    int32_t Cd, rpi_d, Sc;       // down: chunks per row, rows per step, column slices
+    // work decomposition (filled by decode_grid)
+    int32_t n_gu;                // gate/up workgroups (persistent over all slots)
+    int32_t Cg, seg_g, rpi_g;    // gate/up: 32-column chunks per row, lanes per row, rows per wave step
+    int32_t rows_tile, tiles_per_slot;
+    int32_t n_dn, Rd;            // down workgroups, rows per down workgroup
+    int32_t Cd, Cp, seg_d, nb;   // down: chunks per row, padded chunks per slot, lanes per
+                                 // segment, 64-lane blocks per slot (Cp >= 64)
+    int32_t spu, units;          // slots per 64-lane unit (Cp < 64), units per row block
+    int32_t cp_log2;             // log2(Cp) when Cp < 64
 };
 
-constexpr int kActSub = 8;             // completion sub-counters per slot
-constexpr int kActCntStride = 32;      // u32 words between counters (128 B)
+constexpr int kNRep = 8;           // replicas of the published logits
+constexpr int kRepStride = 512;    // u64 words between replicas (4 KiB)
+constexpr int kSub = 8;            // completion sub-counters per slot
+constexpr int kCntStride = 32;     // u32 words between counters (128 B)
+constexpr int kDecodeWaves = 4;    // waves per decode workgroup
 
 // Fills the work decomposition of the fused decode kernel for a shape and
 // returns its grid size (workgroups).

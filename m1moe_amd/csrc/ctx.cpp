@@ -94,6 +94,17 @@ struct m1moe_ctx {
     uint8_t* sync = nullptr;         // decode hand-off state: slots | gu_cnt | seen
     uint64_t sync_bytes = 0, sync_gu_cnt = 0, sync_seen = 0;
     uint32_t* err = nullptr;         // sticky device error flag
+    // prefill scratch, grown on demand to the largest T seen (pf_cap tokens)
+    int32_t pf_cap = 0;
+    _Float16* pf_xq = nullptr;       // [cap][h]
+    float* pf_xinv = nullptr;        // [cap]
+    int32_t* pf_pos = nullptr;       // [cap*K]
+    int32_t* pf_sorted = nullptr;    // [cap*K]
+    int32_t* pf_eoff = nullptr;      // [E+1]
+    int32_t* pf_toff = nullptr;      // [E+1]
+    int32_t* pf_texp = nullptr;      // [cap*K/kPfTN + E + 1]
+    _Float16* pf_act = nullptr;      // [cap*K][I]
+    float* pf_y = nullptr;           // [cap*K][h]
     std::set<void*> allocs;
 };
 
@@ -208,6 +219,37 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
     return launched(m1moe::launch_router_topk(r, ctx->stream), "router_topk");
 }
 
+// Grows the prefill scratch to at least T tokens (the whole cap at once, so a
+// graph captured after one call at the largest T never allocates).
+int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
+    if (T <= ctx->pf_cap) return M1MOE_OK;
+    const m1moe::Geom& g = ctx->g;
+    void** bufs[] = {(void**)&ctx->pf_xq,   (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
+                     (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,
+                     (void**)&ctx->pf_texp, (void**)&ctx->pf_act,  (void**)&ctx->pf_y};
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    for (void** b : bufs) {
+        if (*b) (void)hipFree(*b);
+        *b = nullptr;
+    }
+    ctx->pf_cap = 0;
+    const uint64_t t = (uint64_t)T, P = t * (uint64_t)g.K, E = (uint64_t)g.E;
+    int32_t rc;
+    if ((rc = device_alloc((void**)&ctx->pf_xq, t * g.h * 2, "prefill x")) ||
+        (rc = device_alloc((void**)&ctx->pf_xinv, t * 4, "prefill x scales")) ||
+        (rc = device_alloc((void**)&ctx->pf_pos, P * 4, "prefill positions")) ||
+        (rc = device_alloc((void**)&ctx->pf_sorted, P * 4, "prefill sorted tokens")) ||
+        (rc = device_alloc((void**)&ctx->pf_eoff, (E + 1) * 4, "prefill expert offsets")) ||
+        (rc = device_alloc((void**)&ctx->pf_toff, (E + 1) * 4, "prefill tile offsets")) ||
+        (rc = device_alloc((void**)&ctx->pf_texp, (P / m1moe::kPfTN + E + 1) * 4,
+                           "prefill tile experts")) ||
+        (rc = device_alloc((void**)&ctx->pf_act, P * g.I * 2, "prefill act")) ||
+        (rc = device_alloc((void**)&ctx->pf_y, P * g.h * 4, "prefill expert outputs")))
+        return rc;
+    ctx->pf_cap = T;
+    return M1MOE_OK;
+}
+
 int32_t require_loaded(m1moe_ctx_t ctx, int32_t layer, bool router) {
     if (!ctx->layer_loaded[layer])
         return fail(M1MOE_ERR_INVALID, "layer %d experts were never uploaded", layer);
@@ -272,8 +314,10 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (void* p : ctx->allocs) (void)hipFree(p);
-    void* owned[] = {ctx->arena,  ctx->routers,  ctx->biases, ctx->logits, ctx->topk_idx,
-                     ctx->topk_w, ctx->counters, ctx->act,    ctx->sync,   ctx->err};
+    void* owned[] = {ctx->arena,   ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
+                     ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
+                     ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
+                     ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y};
     for (void* p : owned)
         if (p) (void)hipFree(p);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -483,6 +527,10 @@ int32_t m1moe_sync(m1moe_ctx_t ctx) {
             return fail(M1MOE_ERR_DEVICE,
                         "a kernel saw an expert index outside [0, %d) (device flag 0x%x)",
                         ctx->g.E, flag);
+        if (flag & 8u)
+            return fail(M1MOE_ERR_DEVICE,
+                        "prefill met a group scale with |s| >= 0.25, outside its f16 "
+                        "dequantisation range (device flag 0x%x)", flag);
         return fail(M1MOE_ERR_DEVICE,
                     "a decode hand-off wait timed out (device flag 0x%x); state was reset", flag);
     }
@@ -629,14 +677,46 @@ int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void*
                           int32_t* d_topk_idx, float* d_topk_w) {
     int32_t rc;
     if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
-    (void)T;
-    (void)d_x;
-    (void)x_dtype;
-    (void)d_residual;
-    (void)d_out;
-    (void)d_topk_idx;
-    (void)d_topk_w;
-    return fail(M1MOE_ERR_INVALID, "m1moe_moe_prefill is not built yet");
+    if (T < 1 || T > m1moe::kPrefillCap)
+        return fail(M1MOE_ERR_INVALID, "T=%d must be in [1, %d]", T, m1moe::kPrefillCap);
+    if ((rc = check_dtype(x_dtype)) || (rc = check_dev_ptr(d_x, "d_x", false)) ||
+        (rc = check_dev_ptr(d_residual, "d_residual", true)) ||
+        (rc = check_dev_ptr(d_out, "d_out", false)) ||
+        (rc = check_dev_ptr(d_topk_idx, "d_topk_idx", true)) ||
+        (rc = check_dev_ptr(d_topk_w, "d_topk_w", true)))
+        return rc;
+    if ((rc = require_loaded(ctx, layer, true))) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    if ((rc = ensure_prefill_scratch(ctx, T))) return rc;
+    if ((rc = enqueue_router(ctx, layer, T, d_x, x_dtype, d_topk_idx, d_topk_w, nullptr)))
+        return rc;
+    const m1moe::Geom& g = ctx->g;
+    m1moe::PrefillArgs a{};
+    a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
+    a.expert_bytes = g.expert_bytes;
+    a.x = d_x;
+    a.x_bf16 = (x_dtype == M1MOE_BF16);
+    a.residual = d_residual;
+    a.out = d_out;
+    a.idx = ctx->topk_idx;
+    a.w = ctx->topk_w;
+    a.T = T;
+    a.h = g.h;
+    a.E = g.E;
+    a.K = g.K;
+    a.I = g.I;
+    a.gs = g.gs;
+    a.xq = ctx->pf_xq;
+    a.xinv = ctx->pf_xinv;
+    a.pos = ctx->pf_pos;
+    a.sorted_tok = ctx->pf_sorted;
+    a.expert_off = ctx->pf_eoff;
+    a.tile_off = ctx->pf_toff;
+    a.tile_expert = ctx->pf_texp;
+    a.act = ctx->pf_act;
+    a.y = ctx->pf_y;
+    a.err = ctx->err;
+    return launched(m1moe::launch_prefill(a, ctx->stream), "moe_prefill");
 }
 
 int32_t m1moe_dequant_debug(m1moe_ctx_t ctx, int32_t layer, int32_t expert, int32_t proj,

@@ -276,6 +276,27 @@ __device__ __forceinline__ void topk_softmax(const float (&v)[4], int E, int K, 
     }
 }
 
+// Byte offsets of the planar sub-blocks (ModelSpec.swift:36-52,
+// InferenceEngine.swift:84-97), from the MoE dimensions.
+struct Layout {
+    uint64_t gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b;
+    __device__ Layout(int h, int I, int gs) {
+        const uint64_t gw = (uint64_t)I * (uint64_t)(h / 2);
+        const uint64_t gsb = (uint64_t)I * (uint64_t)(h / gs) * 2;
+        const uint64_t dw = (uint64_t)h * (uint64_t)(I / 2);
+        const uint64_t dsb = (uint64_t)h * (uint64_t)(I / gs) * 2;
+        gate_w = 0;
+        gate_s = gw;
+        gate_b = gate_s + gsb;
+        up_w = gate_b + gsb;
+        up_s = up_w + gw;
+        up_b = up_s + gsb;
+        down_w = up_b + gsb;
+        down_s = down_w + dw;
+        down_b = down_s + dsb;
+    }
+};
+
 __device__ __forceinline__ void flag_error(uint32_t* err, uint32_t code) {
     if (err) atomicOr(err, code);
 }

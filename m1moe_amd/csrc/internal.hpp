@@ -90,9 +90,37 @@ struct RouterArgs {
     uint32_t* counters;          // [T] zero-initialised, self-resetting
 };
 
+// Arguments of the prefill kernels (T tokens through one layer).
+struct PrefillArgs {
+    const uint8_t* layer_base;   // first expert block of the layer
+    uint64_t expert_bytes;
+    const void* x;               // [T][h] f32 or bf16
+    int32_t x_bf16;
+    const float* residual;       // [T][h] or null
+    float* out;                  // [T][h]
+    const int32_t* idx;          // [T][K] routing
+    const float* w;              // [T][K]
+    int32_t T, h, E, K, I, gs;
+    // scratch
+    _Float16* xq;                // [T][h] x * 2^e_t in f16
+    float* xinv;                 // [T] 2^-e_t
+    int32_t* pos;                // [T*K] sorted position of pair (t, k)
+    int32_t* sorted_tok;         // [T*K] token of each sorted position
+    int32_t* expert_off;         // [E+1] first sorted position of each expert
+    int32_t* tile_off;           // [E+1] first N-tile of each expert
+    int32_t* tile_expert;        // [T*K/kPfTN + E] expert of each N-tile
+    _Float16* act;               // [T*K][I] silu(gate)*up per sorted pair
+    float* y;                    // [T*K][h] expert outputs per sorted pair
+    uint32_t* err;               // sticky device error flag
+};
+
+constexpr int kPfTM = 64;   // prefill GEMM: weight rows per workgroup tile
+constexpr int kPfTN = 64;   // prefill GEMM: (token, slot) pairs per workgroup tile
+
 // launchers (defined next to their kernels); return a hipError_t as int
 int launch_router_topk(const RouterArgs& a, void* stream);
 int launch_moe_decode(const FusedArgs& a, void* stream);
+int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_dequant(const uint8_t* expert_base, const ProjView& p, int32_t gs, float* out,
                    void* stream);
 

@@ -81,7 +81,7 @@ def main() -> int:
     ap.add_argument("--config", default="cfg0", choices=["cfg0", "cfg2", "cfg3"],
                     help="cfg0/cfg2: batch-1 decode; cfg3: 512-token prefill")
     ap.add_argument("--replicas", type=int, default=0,
-                    help="distinct layer replicas (default: enough for >= 2 GiB of experts)")
+                    help="distinct layer replicas (default: >= 1 GiB of selected experts per pass)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU-baseline sample (0 disables it)")
     ap.add_argument("--seed", type=int, default=2026)
@@ -110,7 +110,10 @@ def main() -> int:
     one = wl.shape(1)
     eb = m.expert_bytes(one)
     layer_bytes = one.num_experts * eb
-    R = args.replicas or max(2, -(-2 * 1024 ** 3 // layer_bytes))
+    # enough replicas that the expert blocks one pass touches (R * K blocks)
+    # are far beyond the 256 MB Infinity Cache
+    touched = one.top_k * eb
+    R = args.replicas or max(2, -(-1024 ** 3 // touched))
     shape = wl.shape(R)
     h, K = shape.hidden, shape.top_k
     log(f"{wl.description}: {R} replicas x {layer_bytes / 2**20:.0f} MiB")

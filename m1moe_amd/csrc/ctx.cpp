@@ -354,7 +354,7 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
     const uint64_t cap = m1moe::kPrefillCap;
     {
         // hand-off state of the fused decode kernel: kNRep replicas of the
-        // tagged logits, K x kSub padded tile counters, one launch counter per
+        // tagged logits, kNRep replicas of K padded slot counters, one launch counter per
         // workgroup
         m1moe::FusedArgs fa{};
         fa.h = g.h;
@@ -364,7 +364,7 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         const int grid = m1moe::decode_grid(fa);
         c->sync_gu_cnt = (uint64_t)m1moe::kNRep * m1moe::kRepStride * 8;
         c->sync_seen =
-            c->sync_gu_cnt + (uint64_t)g.K * m1moe::kSub * m1moe::kCntStride * 4;
+            c->sync_gu_cnt + (uint64_t)m1moe::kNRep * g.K * m1moe::kCntStride * 4;
         c->sync_bytes = c->sync_seen + ((uint64_t)grid * 4 + 255) / 256 * 256;
     }
     if ((rc = device_alloc((void**)&c->arena, L * E * g.expert_bytes, "expert arena")) ||
@@ -378,7 +378,9 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         (rc = device_alloc((void**)&c->sync, c->sync_bytes, "decode hand-off state")) ||
         (rc = device_alloc((void**)&c->err, 4, "error flag")))
         return cleanup(rc);
-    if (hipMemset(c->counters, 0, cap * 4) != hipSuccess ||
+    // act starts with tag bits 0, which no launch (tags start at 1) takes for current
+    if (hipMemset(c->act, 0, (uint64_t)g.K * g.I * 4) != hipSuccess ||
+        hipMemset(c->counters, 0, cap * 4) != hipSuccess ||
         hipMemset(c->err, 0, 4) != hipSuccess || hipMemset(c->biases, 0, L * E * 4) != hipSuccess ||
         hipMemset(c->sync, 0, c->sync_bytes) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
@@ -522,6 +524,7 @@ int32_t m1moe_sync(m1moe_ctx_t ctx) {
         // restart them all from zero
         HIP_TRY(hipMemset(ctx->err, 0, 4));
         HIP_TRY(hipMemset(ctx->sync, 0, ctx->sync_bytes));
+        HIP_TRY(hipMemset(ctx->act, 0, (uint64_t)ctx->g.K * ctx->g.I * 4));
         HIP_TRY(hipDeviceSynchronize());
         if (flag & 1u)
             return fail(M1MOE_ERR_DEVICE,

@@ -82,14 +82,6 @@ __device__ __forceinline__ void st_f32(float* p, float v) {
 __device__ __forceinline__ void add_u32(uint32_t* p, uint32_t v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// All of this wave's memory operations have completed (stores acknowledged
-// at their scope) before anything after it is issued.
-__device__ __forceinline__ void wait_all_mem() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // Loads 32-element chunk c of an f32 or bf16 vector as f32.  The caller
 // passes an in-range chunk index (clamped for idle lanes) so the loads are
 // unconditional; ok = false zeroes them.
@@ -122,11 +114,10 @@ __device__ __forceinline__ void load_chunk(const void* x, int x_bf16, int c, boo
 // f32 chunk written by other workgroups in this launch: eight 128-bit
 // agent-coherent loads (sc1: they bypass the non-coherent L2 copies), all in
 // flight together, then one wait (which also covers this wave's earlier
-// loads).  The chunk address must be in range; ok = false zeroes the values.
-__device__ __forceinline__ void load_chunk_coherent(const float* x, int c, bool ok,
-                                                    float (&v)[32]) {
+// loads).  The chunk address must be in range.
+__device__ __forceinline__ void load_chunk_coherent(const float* x, int c, float (&v)[32]) {
     const float* p = x + c * 32;
-    float4 q0, q1, q2, q3, q4, q5, q6, q7;
+    float4* q = reinterpret_cast<float4*>(v);
     asm volatile(
         "global_load_dwordx4 %0, %8, off sc1\n\t"
         "global_load_dwordx4 %1, %8, off offset:16 sc1\n\t"
@@ -137,18 +128,10 @@ __device__ __forceinline__ void load_chunk_coherent(const float* x, int c, bool 
         "global_load_dwordx4 %6, %8, off offset:96 sc1\n\t"
         "global_load_dwordx4 %7, %8, off offset:112 sc1\n\t"
         "s_waitcnt vmcnt(0)"
-        : "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3), "=&v"(q4), "=&v"(q5), "=&v"(q6),
-          "=&v"(q7)
+        : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]),
+          "=&v"(q[6]), "=&v"(q[7])
         : "v"(p)
         : "memory");
-    const float4 q[8] = {q0, q1, q2, q3, q4, q5, q6, q7};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        v[4 * i + 0] = ok ? q[i].x : 0.f;
-        v[4 * i + 1] = ok ? q[i].y : 0.f;
-        v[4 * i + 2] = ok ? q[i].z : 0.f;
-        v[4 * i + 3] = ok ? q[i].w : 0.f;
-    }
 }
 
 // Scale and bias of one group, loaded as the aligned dword holding the bf16
@@ -193,8 +176,8 @@ __device__ __forceinline__ float chunk_term(const uint4& w, uint32_t sw, uint32_
 // partials are added in wave order.  Published to every replica as
 // (tag << 32 | bits).  Every thread of the workgroup calls it; s_tag must be
 // visible (a barrier after it was written) before the call.
-__device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, const uint32_t* s_tag,
-                              double* s_lp) {
+__device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, uint32_t* s_tag,
+                              uint32_t tag_reg, double* s_lp) {
     if (wave < 4) {
         const uint16_t* wr = a.router + (size_t)e * a.h;
         const int C = a.h / 32;
@@ -220,6 +203,7 @@ __device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, con
         acc = wave_sum_f64_last(acc);
         if (lane == 63) s_lp[wave] = acc;
     }
+    if (threadIdx.x == 0) *s_tag = tag_reg;  // after the row loads were issued
     __syncthreads();
     if (wave == 0 && lane < kNRep) {
         double t = s_lp[0];
@@ -440,10 +424,21 @@ __device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int
     }
 }
 
+// act values carry the launch number mod 4 in their two lowest mantissa bits,
+// so a consumer can tell this launch's value from the previous one's; it
+// clears them before use (a relative change below 2^-21, the same in every
+// launch, and the consumer rounds act to f16 anyway).
+__device__ __forceinline__ float act_tagged(float v, uint32_t tag) {
+    return __uint_as_float((__float_as_uint(v) & ~3u) | (tag & 3u));
+}
+__device__ __forceinline__ bool act_is_current(float v, uint32_t tag) {
+    return (__float_as_uint(v) & 3u) == (tag & 3u);
+}
+
 template <int CPL, int UG, int GSL>
 __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, const GUGeo& m,
                                            const GUTile<CPL, UG>& t, const XChunk (&xc)[CPL],
-                                           float inv) {
+                                           float inv, uint32_t tag) {
     const uint32_t groups = (uint32_t)a.h >> (5 + GSL);
     const NibK nk = nib_consts();
 #pragma unroll
@@ -465,31 +460,31 @@ __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, 
         pg = seg_sum(pg * inv, a.seg_g);
         pu = seg_sum(pu * inv, a.seg_g);
         if (m.writer && row < a.I)
-            st_f32(a.act + (size_t)k * a.I + row, (pg / (1.0f + expf(-pg))) * pu);  // Shaders.metal:148
+            st_f32(a.act + (size_t)k * a.I + row,
+                   act_tagged((pg / (1.0f + expf(-pg))) * pu, tag));  // Shaders.metal:148
     }
 }
 
-// Number of row blocks rb in [0, n) with rb % kSub == j.
-__device__ __forceinline__ uint32_t count_mod(int n, int j) {
-    return n > j ? (uint32_t)((n - j + kSub - 1) / kSub) : 0u;
-}
-
 // gate/up workgroup (slot k, row block rb): all loads at once, then compute,
-// then one completion count on sub-counter (k, rb % kSub).
+// then one completion count on every replica of slot k's counter (a
+// consumer polls only its own replica, so no line has many pollers).  The count does
+// not wait for the act stores to be acknowledged (that wait costs µs under
+// the expert stream): the consumer checks the tag bits of what it reads and
+// reads again until they are current.
 template <int CPL, int UG, int GSL>
 __device__ void gu_role(const FusedArgs& a, const Layout& L, int k, int rb, int wave, int lane,
-                        int e, const XChunk (&xc)[CPL], float inv) {
+                        int e, const XChunk (&xc)[CPL], float inv, uint32_t tag) {
     const GUGeo m = gu_geo(lane, a.Cg, a.seg_g);
     const int row0 = rb * a.rows_tile + wave * a.rpi_g * UG + m.q;
     if (e >= 0) {
         GUTile<CPL, UG> t;
         gu_load<CPL, UG, GSL>(a, L, e, row0, m, t);
-        gu_compute<CPL, UG, GSL>(a, k, row0, m, t, xc, inv);
+        gu_compute<CPL, UG, GSL>(a, k, row0, m, t, xc, inv, tag);
     }
-    wait_all_mem();
     __syncthreads();
-    if (threadIdx.x == 0)
-        add_u32(a.gu_cnt + ((size_t)k * kSub + (rb & (kSub - 1))) * kCntStride, 1u);
+    if (threadIdx.x < (unsigned)kNRep)
+        add_u32(a.gu_cnt + ((size_t)threadIdx.x * a.K + k) * kCntStride, 1u);
+    (void)rb;
 }
 
 // ---- down + combine ----------------------------------------------------------------
@@ -542,34 +537,27 @@ __device__ __forceinline__ void dn_load(const FusedArgs& a, const Layout& L, con
     }
 }
 
-// Waits until every gate/up tile of slots [k0, k0 + n) has been counted.
+// Waits until every gate/up workgroup of slots [k0, k0 + n) has been counted
+// (n <= K <= 32), polling replica wg % kNRep of the slot counters.
 __device__ bool wait_slots(const FusedArgs& a, int k0, int n, int lane, uint32_t tag) {
-    for (int base = 0; base < n; base += 64 / kSub) {
-        const int k = k0 + base + lane / kSub, j = lane & (kSub - 1);
-        const bool mine = (base + lane / kSub) < n && k < a.K;
-        const uint32_t want = mine ? tag * count_mod(a.tiles_per_slot, j) : 0u;
-        const uint32_t* p = a.gu_cnt + ((size_t)j * kCntStride) + (size_t)(mine ? k : 0) * kSub * kCntStride;
-        for (int it = 0;; ++it) {
-            const bool done = !mine || ld_u32(p) == want;
-            if (__all(done)) break;
-            if (it >= a.spin_limit) return false;
-            __builtin_amdgcn_s_sleep(2);
-        }
+    const bool mine = lane < n;
+    const uint32_t want = tag * (uint32_t)a.tiles_per_slot;
+    const uint32_t* p = a.gu_cnt +
+        ((size_t)(blockIdx.x & (kNRep - 1)) * a.K + (size_t)(k0 + (mine ? lane : 0))) * kCntStride;
+    for (int it = 0;; ++it) {
+        const bool done = !mine || ld_u32(p) == want;
+        if (__all(done)) return true;
+        if (it >= a.spin_limit) return false;
+        __builtin_amdgcn_s_sleep(2);
     }
-    return true;
 }
 
-// Position of an item (unit, sub-tile) in a wave's sequence: items run
-// through the wave's units (wave, wave + kWaves, ...) and, within a unit,
-// through the nsub sub-tiles of kRT rows.
+// Items of a down workgroup: (unit u, sub-tile st of kRT rows), unit-major;
+// wave w takes a contiguous block of them, so consecutive items of a wave
+// mostly share a unit (and its converted act chunk).
 struct ItemPos {
     int u, st;
-    __device__ void next(int nsub) {
-        if (++st == nsub) {
-            st = 0;
-            u += kWaves;
-        }
-    }
+    __device__ ItemPos(int g, int nsub) : u(g / nsub), st(g - (g / nsub) * nsub) {}
 };
 
 template <int GSL>
@@ -578,8 +566,10 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     const bool ok_run = r.ok != 0;
     const int row_base = dblk * a.Rd;
     const int nsub = a.Rd / kRT;
-    const int my_units = (a.units - wave + kWaves - 1) / kWaves;
-    const int n_items = my_units * nsub;
+    const int total = a.units * nsub;
+    const int per = (total + kWaves - 1) / kWaves;
+    const int g0 = wave * per;
+    const int n_items = max(0, min(total, g0 + per) - g0);
     const uint32_t groups = (uint32_t)a.I >> (5 + GSL);
     auto expert_at = [&](const DNUnit& d) {
         const int e = d.ok ? r.idx[d.k] : -1;
@@ -587,13 +577,13 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     };
     // two items in flight: the first two are loaded as soon as the routing is known
     DNTile A, B;
-    ItemPos pa{wave, 0}, pb{wave, 0};
-    pb.next(nsub);
     if (n_items > 0) {
+        const ItemPos pa(g0, nsub);
         const DNUnit d = dn_unit(a, pa.u, lane);
-        dn_load<GSL>(a, L, d, expert_at(d), row_base, A);
+        dn_load<GSL>(a, L, d, expert_at(d), row_base + pa.st * kRT, A);
     }
     if (n_items > 1) {
+        const ItemPos pb(g0 + 1, nsub);
         const DNUnit d = dn_unit(a, pb.u, lane);
         dn_load<GSL>(a, L, d, expert_at(d), row_base + pb.st * kRT, B);
     }
@@ -629,8 +619,25 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
             }
             live = ready && expert_at(d) >= 0;
             float v[1][32];
-            load_chunk_coherent(a.act + (size_t)(d.k < a.K ? d.k : 0) * a.I,
-                                min(d.c, a.Cd - 1), live, v[0]);
+            const float* src = a.act + (size_t)(d.k < a.K ? d.k : 0) * a.I;
+            const int cc = min(d.c, a.Cd - 1);
+            for (int it = 0;; ++it) {
+                load_chunk_coherent(src, cc, v[0]);
+                uint32_t bad = 0;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) bad |= (__float_as_uint(v[0][i]) ^ tag) & 3u;
+                if (__all(!live || bad == 0)) break;
+                if (it >= a.spin_limit) {
+                    flag_error(a.err, 4u);
+                    live = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            // the value without its tag bits (the same in every launch), or 0
+            const uint32_t keep = live ? ~3u : 0u;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[0][i] = __uint_as_float(__float_as_uint(v[0][i]) & keep);
             inv = lane_scale_prep<1>(v, xc);
         }
         const uint32_t cc = (uint32_t)min(d.c, a.Cd - 1);
@@ -645,20 +652,18 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
         }
     };
     for (int i = 0; i < n_items; i += 2) {
-        process(pa, A);
-        pa.next(nsub);
-        pa.next(nsub);
+        process(ItemPos(g0 + i, nsub), A);
         if (i + 2 < n_items) {
-            const DNUnit dn = dn_unit(a, pa.u, lane);
-            dn_load<GSL>(a, L, dn, expert_at(dn), row_base + pa.st * kRT, A);
+            const ItemPos p(g0 + i + 2, nsub);
+            const DNUnit dn = dn_unit(a, p.u, lane);
+            dn_load<GSL>(a, L, dn, expert_at(dn), row_base + p.st * kRT, A);
         }
         if (i + 1 < n_items) {
-            process(pb, B);
-            pb.next(nsub);
-            pb.next(nsub);
+            process(ItemPos(g0 + i + 1, nsub), B);
             if (i + 3 < n_items) {
-                const DNUnit dn = dn_unit(a, pb.u, lane);
-                dn_load<GSL>(a, L, dn, expert_at(dn), row_base + pb.st * kRT, B);
+                const ItemPos p(g0 + i + 3, nsub);
+                const DNUnit dn = dn_unit(a, p.u, lane);
+                dn_load<GSL>(a, L, dn, expert_at(dn), row_base + p.st * kRT, B);
             }
         }
     }
@@ -689,12 +694,17 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const bool is_gu = wg < a.n_gu;
 
-    // this launch's number, as counted by this workgroup (all agree)
-    if (threadIdx.x == 0) s_tag = ld_u32(a.seen + wg) + 1u;
-    __syncthreads();
+    // this launch's number, as counted by this workgroup (all agree); its
+    // load overlaps the router row loads of the producers
+    const uint32_t tag_reg = threadIdx.x == 0 ? ld_u32(a.seen + wg) + 1u : 0u;
+    if (!a.given_idx && wg < a.E) {
+        for (int e = wg; e < a.E; e += gridDim.x)
+            produce_logit(a, e, wave, lane, &s_tag, tag_reg, s_lp);
+    } else {
+        if (threadIdx.x == 0) s_tag = tag_reg;
+        __syncthreads();
+    }
     const uint32_t tag = s_tag;
-    if (!a.given_idx)
-        for (int e = wg; e < a.E; e += gridDim.x) produce_logit(a, e, wave, lane, &s_tag, s_lp);
 
     // the input vector does not depend on the routing: prepare it meanwhile
     XChunk xc[CPL];
@@ -724,7 +734,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
     if (is_gu) {
         const int k = wg / a.tiles_per_slot, rb = wg - k * a.tiles_per_slot;
         const int e = ok_run ? r.idx[k] : -1;
-        gu_role<CPL, UG, GSL>(a, L, k, rb, wave, lane, e, xc, inv);
+        gu_role<CPL, UG, GSL>(a, L, k, rb, wave, lane, e, xc, inv, tag);
     } else {
         dn_role<GSL>(a, L, wg - a.n_gu, wave, lane, r, s_part, tag);
     }

@@ -50,7 +50,7 @@ struct FusedArgs {
     // agree on the launch number ("tag") without communicating.
     unsigned long long* slots;   // [kNRep][kRepStride] logits tagged with the launch number
     float* act;                  // [K][I] silu(gate) * up
-    uint32_t* gu_cnt;            // [K][kSub] monotonic tile counters, kCntStride apart
+    uint32_t* gu_cnt;            // [kNRep][K] monotonic per-slot counters, kCntStride apart
     uint32_t* seen;              // [grid] launches completed by each workgroup
     uint32_t* err;               // sticky device error flag
     int32_t h, E, K, I, gs, norm, x_bf16, spin_limit;
@@ -67,7 +67,6 @@ struct FusedArgs {
 
 constexpr int kNRep = 8;           // replicas of the published logits
 constexpr int kRepStride = 512;    // u64 words between replicas (4 KiB)
-constexpr int kSub = 8;            // completion sub-counters per slot
 constexpr int kCntStride = 32;     // u32 words between counters (128 B)
 constexpr int kDecodeWaves = 4;    // waves per decode workgroup
 

@@ -29,8 +29,8 @@
 // Hand-off.  Relaxed agent-scope atomics and 128-bit sc1 loads of act (sc1
 // accesses are coherent across the XCDs' L2s), never release/acquire fences
 // (an L2 write-back or invalidate costs microseconds).  Logits are published as (launch tag,
-// value) pairs into kNRep replicas, and a workgroup polls replica
-// wg % kNRep, so no cache line has more than a few dozen pollers.  Nothing is
+// value) pairs into kLogitRep replicas, and a workgroup polls replica
+// wg % kLogitRep; slot counters have kNRep replicas.  Nothing is
 // reset between launches: every workgroup counts its own launches (seen[wg]),
 // so all agree on the launch number `tag` and on the counters' targets
 // (graph replay needs no memset).  Every wait is bounded: on timeout the
@@ -58,6 +58,7 @@ constexpr int kMaxK = 32;
 constexpr int kMaxE = 256;
 constexpr int kRT = 4;          // down rows per sub-tile
 constexpr int kDnTarget = 256;  // down workgroups
+constexpr int kGuMax = 512;     // gate/up workgroups (persistent beyond that many tiles)
 
 static_assert(kWaves >= 4, "the router splits a logit over four waves");
 
@@ -205,7 +206,7 @@ __device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, uin
     }
     if (threadIdx.x == 0) *s_tag = tag_reg;  // after the row loads were issued
     __syncthreads();
-    if (wave == 0 && lane < kNRep) {
+    if (wave == 0 && lane < kLogitRep) {
         double t = s_lp[0];
         t += s_lp[1];
         t += s_lp[2];
@@ -248,7 +249,7 @@ __device__ void routing(const FusedArgs& a, int wg, int wave, int lane, uint32_t
         return;
     }
     if (wave == 0) {
-        const unsigned long long* rep = a.slots + (size_t)(wg & (kNRep - 1)) * kRepStride;
+        const unsigned long long* rep = a.slots + (size_t)(wg & (kLogitRep - 1)) * kRepStride;
         float v[4];
         bool have[4];
 #pragma unroll
@@ -391,19 +392,22 @@ struct GUTile {
     uint32_t gs[UG][CPL], gb[UG][CPL], us[UG][CPL], ub[UG][CPL];
 };
 
-// GSL = log2(group_size / 32): the group of chunk c is c >> GSL.
+// GSL = log2(group_size / 32): the group of chunk c is c >> GSL.  A load that
+// is not `real` (a prefetch past the last tile) reads the first 16 bytes of
+// the layer in every lane instead: one line, an L2 hit after its first use.
 template <int CPL, int UG, int GSL>
 __device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int e, int row0,
-                                        const GUGeo& m, GUTile<CPL, UG>& t) {
+                                        bool real, const GUGeo& m, GUTile<CPL, UG>& t) {
     // e is wave-uniform: keep the sub-block bases in scalar registers and
     // address with 32-bit lane offsets
-    const uint8_t* blk = a.layer_base + (uint64_t)__builtin_amdgcn_readfirstlane(e) * a.expert_bytes;
-    const uint8_t* gw_b = blk + L.gate_w;
-    const uint8_t* uw_b = blk + L.up_w;
-    const uint8_t* gs_b = blk + L.gate_s;
-    const uint8_t* gb_b = blk + L.gate_b;
-    const uint8_t* us_b = blk + L.up_s;
-    const uint8_t* ub_b = blk + L.up_b;
+    const uint8_t* blk = a.layer_base +
+        (real ? (uint64_t)__builtin_amdgcn_readfirstlane(e) * a.expert_bytes : 0);
+    const uint8_t* gw_b = blk + (real ? L.gate_w : 0);
+    const uint8_t* uw_b = blk + (real ? L.up_w : 0);
+    const uint8_t* gs_b = blk + (real ? L.gate_s : 0);
+    const uint8_t* gb_b = blk + (real ? L.gate_b : 0);
+    const uint8_t* us_b = blk + (real ? L.up_s : 0);
+    const uint8_t* ub_b = blk + (real ? L.up_b : 0);
     const uint32_t groups = (uint32_t)a.h >> (5 + GSL);
     const uint32_t row_bytes = (uint32_t)a.h / 2;
 #pragma unroll
@@ -412,8 +416,8 @@ __device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const uint32_t cc = (uint32_t)min(m.c0 + 64 * j, a.Cg - 1);
-            const uint32_t wo = rc * row_bytes + cc * 16u;
-            const uint32_t sbw = sb_word(rc * groups + (cc >> GSL));
+            const uint32_t wo = real ? rc * row_bytes + cc * 16u : 0u;
+            const uint32_t sbw = real ? sb_word(rc * groups + (cc >> GSL)) : 0u;
             t.gw[u][j] = *reinterpret_cast<const uint4*>(gw_b + wo);
             t.uw[u][j] = *reinterpret_cast<const uint4*>(uw_b + wo);
             t.gs[u][j] = *reinterpret_cast<const uint32_t*>(gs_b + sbw);
@@ -430,9 +434,6 @@ __device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int
 // launch, and the consumer rounds act to f16 anyway).
 __device__ __forceinline__ float act_tagged(float v, uint32_t tag) {
     return __uint_as_float((__float_as_uint(v) & ~3u) | (tag & 3u));
-}
-__device__ __forceinline__ bool act_is_current(float v, uint32_t tag) {
-    return (__float_as_uint(v) & 3u) == (tag & 3u);
 }
 
 template <int CPL, int UG, int GSL>
@@ -465,26 +466,69 @@ __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, 
     }
 }
 
-// gate/up workgroup (slot k, row block rb): all loads at once, then compute,
-// then one completion count on every replica of slot k's counter (a
-// consumer polls only its own replica, so no line has many pollers).  The count does
-// not wait for the act stores to be acknowledged (that wait costs µs under
-// the expert stream): the consumer checks the tag bits of what it reads and
-// reads again until they are current.
+// gate/up workgroup g: tiles T = g, g + n_gu, ... of the K * tiles_per_slot
+// (slot-major, so slot 0 completes first and its down work can start while
+// later slots stream), each tile = rows_tile rows of one slot; the next
+// tile's loads are in flight while a tile is computed.  When the workgroup
+// moves on to another slot (and at its end) it adds the number of tiles it
+// finished of the previous one to every replica of that slot's counter (a
+// consumer polls only its own replica): one add per slot, not per tile, since
+// adds to one counter serialise in the memory system and, being counted with
+// the loads, stall the next tile's wait.  Counts do not wait for the act
+// stores to be acknowledged (that wait costs µs under the expert stream): the
+// consumer checks the tag bits of what it reads and reads again until they
+// are current.
 template <int CPL, int UG, int GSL>
-__device__ void gu_role(const FusedArgs& a, const Layout& L, int k, int rb, int wave, int lane,
-                        int e, const XChunk (&xc)[CPL], float inv, uint32_t tag) {
+__device__ void gu_role(const FusedArgs& a, const Layout& L, int g, int wave, int lane,
+                        const RouteLDS& r, const XChunk (&xc)[CPL], float inv, uint32_t tag) {
     const GUGeo m = gu_geo(lane, a.Cg, a.seg_g);
-    const int row0 = rb * a.rows_tile + wave * a.rpi_g * UG + m.q;
-    if (e >= 0) {
-        GUTile<CPL, UG> t;
-        gu_load<CPL, UG, GSL>(a, L, e, row0, m, t);
-        gu_compute<CPL, UG, GSL>(a, k, row0, m, t, xc, inv, tag);
+    const int tps = a.tiles_per_slot;
+    const int total = a.K * tps;
+    const int wave_row = wave * a.rpi_g * UG + m.q;
+    auto expert_of = [&](int T) {
+        const int e = r.idx[T / tps];
+        return (r.ok && e >= 0) ? e : -1;
+    };
+    auto row_of = [&](int T) { return (T % tps) * a.rows_tile + wave_row; };
+    int cnt_k = g / tps;  // slot being counted
+    uint32_t cnt_n = 0;   // its tiles finished by this workgroup
+    auto flush = [&]() {
+        __syncthreads();
+        if (threadIdx.x < (unsigned)kNRep)
+            add_u32(a.gu_cnt + ((size_t)threadIdx.x * a.K + cnt_k) * kCntStride, cnt_n);
+    };
+    // this workgroup's tiles: i = 0 .. n_mine-1 -> T = g + i * n_gu.  Two
+    // tiles are in flight from the start; every prefetch is issued (past the
+    // last tile it reads a dummy line), so the compiler's in-order load
+    // counting stays exact and a tile's compute waits only for its own loads.
+    const int n_mine = (total - 1 - g) / a.n_gu + 1;  // g < n_gu <= total
+    auto load = [&](int i, GUTile<CPL, UG>& t) {
+        const bool real = i < n_mine;
+        const int T = g + (real ? i : 0) * a.n_gu;
+        gu_load<CPL, UG, GSL>(a, L, expert_of(T), row_of(T), real && expert_of(T) >= 0, m, t);
+    };
+    auto step = [&](int i, const GUTile<CPL, UG>& t) {
+        const int T = g + i * a.n_gu;
+        const int k = T / tps;
+        if (k != cnt_k) {
+            flush();
+            cnt_k = k;
+            cnt_n = 0;
+        }
+        if (expert_of(T) >= 0) gu_compute<CPL, UG, GSL>(a, k, row_of(T), m, t, xc, inv, tag);
+        ++cnt_n;
+    };
+    GUTile<CPL, UG> A, B;
+    load(0, A);
+    load(1, B);
+    for (int i = 0; i < n_mine; i += 2) {
+        step(i, A);
+        if (i + 1 >= n_mine) break;
+        load(i + 2, A);
+        step(i + 1, B);
+        load(i + 3, B);
     }
-    __syncthreads();
-    if (threadIdx.x < (unsigned)kNRep)
-        add_u32(a.gu_cnt + ((size_t)threadIdx.x * a.K + k) * kCntStride, 1u);
-    (void)rb;
+    flush();
 }
 
 // ---- down + combine ----------------------------------------------------------------
@@ -520,20 +564,26 @@ __device__ __forceinline__ DNUnit dn_unit(const FusedArgs& a, int u, int lane) {
     return d;
 }
 
+// A load that is not `real` (a prefetch past the wave's last item) reads the
+// first 16 bytes of the layer in every lane instead.
 template <int GSL>
 __device__ __forceinline__ void dn_load(const FusedArgs& a, const Layout& L, const DNUnit& d,
-                                        int e, int row0, DNTile& t) {
-    const uint8_t* blk = a.layer_base + (uint64_t)(e < 0 ? 0 : e) * a.expert_bytes;
+                                        int e, int row0, bool real, DNTile& t) {
+    const uint8_t* blk = a.layer_base + (real ? (uint64_t)(e < 0 ? 0 : e) * a.expert_bytes : 0);
+    const uint8_t* w_b = blk + (real ? L.down_w : 0);
+    const uint8_t* s_b = blk + (real ? L.down_s : 0);
+    const uint8_t* b_b = blk + (real ? L.down_b : 0);
     const uint32_t groups = (uint32_t)a.I >> (5 + GSL);
     const uint32_t row_bytes = (uint32_t)a.I / 2;
     const uint32_t cc = (uint32_t)min(d.c, a.Cd - 1);
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
         const uint32_t rc = (uint32_t)min(row0 + r, a.h - 1);
-        const uint32_t sbw = sb_word(rc * groups + (cc >> GSL));
-        t.w[r] = *reinterpret_cast<const uint4*>(blk + L.down_w + (uint64_t)rc * row_bytes + cc * 16u);
-        t.s[r] = *reinterpret_cast<const uint32_t*>(blk + L.down_s + sbw);
-        t.b[r] = *reinterpret_cast<const uint32_t*>(blk + L.down_b + sbw);
+        const uint32_t sbw = real ? sb_word(rc * groups + (cc >> GSL)) : 0u;
+        const uint64_t wo = real ? (uint64_t)rc * row_bytes + cc * 16u : 0u;
+        t.w[r] = *reinterpret_cast<const uint4*>(w_b + wo);
+        t.s[r] = *reinterpret_cast<const uint32_t*>(s_b + sbw);
+        t.b[r] = *reinterpret_cast<const uint32_t*>(b_b + sbw);
     }
 }
 
@@ -575,18 +625,19 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
         const int e = d.ok ? r.idx[d.k] : -1;
         return (ok_run && e >= 0) ? e : -1;
     };
-    // two items in flight: the first two are loaded as soon as the routing is known
+    // two items in flight: the first two are loaded as soon as the routing is
+    // known.  (Unlike the gate/up role, prefetches past the wave's last item
+    // are skipped: waves here end the kernel, and even an L2 hit at the end
+    // shows in its duration.)
+    auto load = [&](int i, DNTile& t) {
+        const bool real = i < n_items;
+        const ItemPos p(real ? g0 + i : 0, nsub);
+        const DNUnit d = dn_unit(a, p.u, lane);
+        dn_load<GSL>(a, L, d, expert_at(d), row_base + p.st * kRT, real, t);
+    };
     DNTile A, B;
-    if (n_items > 0) {
-        const ItemPos pa(g0, nsub);
-        const DNUnit d = dn_unit(a, pa.u, lane);
-        dn_load<GSL>(a, L, d, expert_at(d), row_base + pa.st * kRT, A);
-    }
-    if (n_items > 1) {
-        const ItemPos pb(g0 + 1, nsub);
-        const DNUnit d = dn_unit(a, pb.u, lane);
-        dn_load<GSL>(a, L, d, expert_at(d), row_base + pb.st * kRT, B);
-    }
+    if (n_items > 0) load(0, A);
+    if (n_items > 1) load(1, B);
     // keep the weight loads above the waits below (the compiler may otherwise
     // sink them to their first use)
     asm volatile("" ::: "memory");
@@ -653,19 +704,9 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     };
     for (int i = 0; i < n_items; i += 2) {
         process(ItemPos(g0 + i, nsub), A);
-        if (i + 2 < n_items) {
-            const ItemPos p(g0 + i + 2, nsub);
-            const DNUnit dn = dn_unit(a, p.u, lane);
-            dn_load<GSL>(a, L, dn, expert_at(dn), row_base + p.st * kRT, A);
-        }
-        if (i + 1 < n_items) {
-            process(ItemPos(g0 + i + 1, nsub), B);
-            if (i + 3 < n_items) {
-                const ItemPos p(g0 + i + 3, nsub);
-                const DNUnit dn = dn_unit(a, p.u, lane);
-                dn_load<GSL>(a, L, dn, expert_at(dn), row_base + p.st * kRT, B);
-            }
-        }
+        if (i + 2 < n_items) load(i + 2, A);
+        if (i + 1 < n_items) process(ItemPos(g0 + i + 1, nsub), B);
+        if (i + 3 < n_items) load(i + 3, B);
     }
     __syncthreads();
     // combine in slot order, 64-chunk blocks summed in order (Shaders.metal:371-374)
@@ -732,9 +773,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
     }
     const Layout L(a.h, a.I, a.gs);
     if (is_gu) {
-        const int k = wg / a.tiles_per_slot, rb = wg - k * a.tiles_per_slot;
-        const int e = ok_run ? r.idx[k] : -1;
-        gu_role<CPL, UG, GSL>(a, L, k, rb, wave, lane, e, xc, inv, tag);
+        gu_role<CPL, UG, GSL>(a, L, wg, wave, lane, r, xc, inv, tag);
     } else {
         dn_role<GSL>(a, L, wg - a.n_gu, wave, lane, r, s_part, tag);
     }
@@ -802,7 +841,7 @@ int decode_grid(FusedArgs& a) {
     const int cpl = (a.Cg + 63) / 64;
     a.rows_tile = kWaves * a.rpi_g * gu_rows(cpl);
     a.tiles_per_slot = (a.I + a.rows_tile - 1) / a.rows_tile;
-    a.n_gu = a.K * a.tiles_per_slot;
+    a.n_gu = min(a.K * a.tiles_per_slot, kGuMax);
     // down
     a.Cd = a.I / 32;
     if (a.Cd < 64) {

@@ -48,7 +48,7 @@ struct FusedArgs {
     // hand-off state.  It starts at zero and is never reset between launches:
     // every workgroup counts its own launches in seen[wg], so all workgroups
     // agree on the launch number ("tag") without communicating.
-    unsigned long long* slots;   // [kNRep][kRepStride] logits tagged with the launch number
+    unsigned long long* slots;   // [kLogitRep][kRepStride] logits tagged with the launch number
     float* act;                  // [K][I] silu(gate) * up
     uint32_t* gu_cnt;            // [kNRep][K] monotonic per-slot counters, kCntStride apart
     uint32_t* seen;              // [grid] launches completed by each workgroup
@@ -65,9 +65,14 @@ struct FusedArgs {
     int32_t cp_log2;             // log2(Cp) when Cp < 64
 };
 
-constexpr int kNRep = 8;           // replicas of the published logits
-constexpr int kRepStride = 512;    // u64 words between replicas (4 KiB)
-constexpr int kCntStride = 32;     // u32 words between counters (128 B)
+// Replicas of the hand-off words (published logits, slot counters), so that
+// each line has few pollers.  Counter (replica r, slot k) is word
+// (r * K + k) * kCntStride: consecutive 128-byte lines, which spreads them over
+// the L2 channels (replicas exactly 4 KiB apart would share one channel).
+constexpr int kNRep = 32;            // counter replicas
+constexpr int kLogitRep = 8;         // logit replicas
+constexpr int kRepStride = 544;      // u64 words between logit replicas (4352 B)
+constexpr int kCntStride = 32;       // u32 words between counters (128 B)
 constexpr int kDecodeWaves = 4;    // waves per decode workgroup
 
 // Fills the work decomposition of the fused decode kernel for a shape and

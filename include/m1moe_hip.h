@@ -203,7 +203,7 @@ int32_t m1moe_moe_decode_given_topk(m1moe_ctx_t ctx, int32_t layer,
                                     const float* d_residual, float* d_out);
 
 /* T tokens at once (prefill): routing per token as m1moe_router_topk, the
- * (token, slot) pairs grouped by expert, gate/up/down as MFMA bf16 grouped
+ * (token, slot) pairs grouped by expert, gate/up/down as MFMA f16 grouped
  * GEMMs with the 4-bit dequant fused, and a deterministic weighted combine.
  * Results equal T independent m1moe_moe_decode calls up to bf16 operand
  * rounding.  d_x [T x hidden], d_residual f32 [T x hidden] or NULL,

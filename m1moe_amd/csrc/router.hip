@@ -4,12 +4,15 @@
 // selectTopK, InferenceEngine.swift:490-519), which ran after a full GPU
 // sync.  Two kernels:
 //
-//   router_logits   logits[t][e] = sum_d W[e][d] * x[t][d] for a tile of
-//                   8 tokens x 16 experts per workgroup.  Every product
-//                   bf16 * x is exact in f64; each thread sums half a row in
-//                   f64 and the two halves are added in a fixed order before
-//                   one rounding to f32 (+ the optional logit bias), so the
-//                   value is independent of the summation order in practice.
+//   router_logits   logits[t][e] = sum_d W[e][d] * x[t][d]: a wave computes
+//                   4 tokens x 4 experts with its lanes across the columns
+//                   (coalesced 128-bit loads, all of a 2048-column row in
+//                   flight at once), a workgroup 4 tokens x 16 experts.
+//                   Every product bf16 * x is exact in f64; each lane sums
+//                   its columns in f64, the lanes are added by a fixed DPP
+//                   tree, then one rounding to f32 (+ the optional logit
+//                   bias), so the value is independent of the summation
+//                   order in practice.
 //   router_rank     one wave per token: experts ranked by descending logit,
 //                   ties to the lower index (softmax is monotone; this is the
 //                   order of the reference's stable sort on probabilities),
@@ -24,51 +27,94 @@
 namespace m1moe {
 namespace {
 
-constexpr int kTT = 8;       // tokens per logits workgroup
-constexpr int kTE = 16;      // experts per logits workgroup
+constexpr int kTT = 4;       // tokens per logits wave and workgroup
+constexpr int kTEw = 4;      // experts per logits wave
+constexpr int kTE = 16;      // experts per logits workgroup (four waves)
 constexpr int kMaxE = 256;   // 4 logits per lane in the ranking wave
 constexpr int kMaxK = 32;    // one selection per lane
 
-// thread -> (token tt = tid / 32, expert te = (tid / 2) % 16, half = tid % 2)
-__global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
-    __shared__ double s_half[256];
-    const int tid = threadIdx.x;
-    const int tt = tid >> 5, te = (tid >> 1) & (kTE - 1), half = tid & 1;
-    const int t = blockIdx.x * kTT + tt, e = blockIdx.y * kTE + te;
-    const int h = a.h;
-    double acc = 0.0;
-    if (t < a.T && e < a.E) {
-        const uint16_t* wr = a.router + (size_t)e * h;
-        const int d0 = half * (h / 2), d1 = d0 + h / 2;
-        if (a.x_bf16) {
-            const uint16_t* xr = static_cast<const uint16_t*>(a.x) + (size_t)t * h;
-            for (int d = d0; d < d1; d += 8) {
-                const uint4 wv = *reinterpret_cast<const uint4*>(wr + d);
-                const uint4 xv = *reinterpret_cast<const uint4*>(xr + d);
+// Lane l takes columns blk * 512 + 8 l .. + 7 of each 512-column block; DB
+// blocks have their loads in flight together.  Rows past T / E are clamped
+// (loaded, never stored); columns past h are skipped.
+template <bool XBF16, int DB>
+__device__ __forceinline__ void logits_wave(const RouterArgs& a, int t0, int e0, int lane,
+                                            double (&acc)[kTT][kTEw]) {
+    const int h = a.h, nb = (h + 511) / 512;
+    const uint16_t* wr[kTEw];
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    acc += (double)bf16x8_at(wv, i) * (double)bf16x8_at(xv, i);
+    for (int j = 0; j < kTEw; ++j) wr[j] = a.router + (size_t)min(e0 + j, a.E - 1) * h;
+    for (int b0 = 0; b0 < nb; b0 += DB) {
+        uint4 wv[DB][kTEw];
+        float4 xv[DB][kTT][2];  // f32 x, or bf16 x in xv[][][0] as raw bits
+#pragma unroll
+        for (int u = 0; u < DB; ++u) {
+            const int c = min((b0 + u) * 512 + lane * 8, h - 8);
+#pragma unroll
+            for (int j = 0; j < kTEw; ++j) wv[u][j] = *reinterpret_cast<const uint4*>(wr[j] + c);
+#pragma unroll
+            for (int i = 0; i < kTT; ++i) {
+                const size_t row = (size_t)min(t0 + i, a.T - 1) * h + c;
+                if (XBF16) {
+                    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + row);
+                    xv[u][i][0] = __builtin_bit_cast(float4, q);
+                } else {
+                    const float* xr = static_cast<const float*>(a.x) + row;
+                    xv[u][i][0] = *reinterpret_cast<const float4*>(xr);
+                    xv[u][i][1] = *reinterpret_cast<const float4*>(xr + 4);
+                }
             }
-        } else {
-            const float* xr = static_cast<const float*>(a.x) + (size_t)t * h;
-            for (int d = d0; d < d1; d += 8) {
-                const uint4 wv = *reinterpret_cast<const uint4*>(wr + d);
-                const float4 x0 = *reinterpret_cast<const float4*>(xr + d);
-                const float4 x1 = *reinterpret_cast<const float4*>(xr + d + 4);
-                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv, i) * (double)xs[i];
+        for (int u = 0; u < DB; ++u) {
+            if ((b0 + u) * 512 + lane * 8 >= h) continue;
+#pragma unroll
+            for (int i = 0; i < kTT; ++i) {
+                float x8[8];
+                if (XBF16) {
+                    const uint4 q = __builtin_bit_cast(uint4, xv[u][i][0]);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) x8[k] = bf16x8_at(q, k);
+                } else {
+                    const float4 p = xv[u][i][0], r = xv[u][i][1];
+                    x8[0] = p.x; x8[1] = p.y; x8[2] = p.z; x8[3] = p.w;
+                    x8[4] = r.x; x8[5] = r.y; x8[6] = r.z; x8[7] = r.w;
+                }
+#pragma unroll
+                for (int j = 0; j < kTEw; ++j)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        acc[i][j] = fma((double)bf16x8_at(wv[u][j], k), (double)x8[k], acc[i][j]);
             }
         }
     }
-    s_half[tid] = acc;
-    __syncthreads();
-    if (half == 0 && t < a.T && e < a.E) {
-        float l = (float)(s_half[tid] + s_half[tid + 1]);
-        if (a.bias) l = l + a.bias[e];
-        a.logits[(size_t)t * a.E + e] = l;
-        if (a.user_logits) a.user_logits[(size_t)t * a.E + e] = l;
-    }
+}
+
+__global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.x * kTT, e0 = blockIdx.y * kTE + wave * kTEw;
+    if (e0 >= a.E) return;
+    double acc[kTT][kTEw];
+#pragma unroll
+    for (int i = 0; i < kTT; ++i)
+#pragma unroll
+        for (int j = 0; j < kTEw; ++j) acc[i][j] = 0.0;
+    if (a.x_bf16)
+        logits_wave<true, 4>(a, t0, e0, lane, acc);
+    else
+        logits_wave<false, 2>(a, t0, e0, lane, acc);
+#pragma unroll
+    for (int i = 0; i < kTT; ++i)
+#pragma unroll
+        for (int j = 0; j < kTEw; ++j) {
+            const double v = wave_sum_f64_last(acc[i][j]);  // lane 63
+            const int t = t0 + i, e = e0 + j;
+            if (lane == 63 && t < a.T && e < a.E) {
+                float l = (float)v;
+                if (a.bias) l = l + a.bias[e];
+                a.logits[(size_t)t * a.E + e] = l;
+                if (a.user_logits) a.user_logits[(size_t)t * a.E + e] = l;
+            }
+        }
 }
 
 // Orders this wave's LDS accesses before / after the call (lanes exchange
@@ -79,9 +125,11 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// One wave per token (four tokens per workgroup).
+// One wave per token (four tokens per workgroup); MB = experts per lane
+// (E <= 64 * MB).
+template <int MB>
 __global__ __launch_bounds__(256) void router_rank_kernel(RouterArgs a) {
-    __shared__ __attribute__((aligned(16))) float s_v[4][kMaxE];
+    __shared__ __attribute__((aligned(16))) float s_v[4][64 * MB];
     __shared__ int s_sel[4][kMaxK];
     __shared__ float s_p[4][kMaxK];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -89,9 +137,9 @@ __global__ __launch_bounds__(256) void router_rank_kernel(RouterArgs a) {
     if (t >= a.T) return;
     const int E = a.E, K = a.K;
     const float* lg = a.logits + (size_t)t * E;
-    float v[4];
+    float v[MB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < MB; ++j) {
         const int e = lane + 64 * j;
         float x = -INFINITY;
         if (e < E) {
@@ -103,32 +151,37 @@ __global__ __launch_bounds__(256) void router_rank_kernel(RouterArgs a) {
     }
     wave_lds_sync();
     // rank of expert i = experts ahead of it (padding: -inf at a higher index)
-    int rank[4] = {0, 0, 0, 0};
-    for (int j0 = 0; j0 < E; j0 += 4) {
+    const int Ep = (E + 3) & ~3;
+    int rank[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) rank[m] = 0;
+    for (int j0 = 0; j0 < Ep; j0 += 4) {
         const float4 w4 = *reinterpret_cast<const float4*>(&s_v[wave][j0]);
         const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int j = j0 + q;
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
+            for (int m = 0; m < MB; ++m) {
                 const int i = lane + 64 * m;
                 rank[m] += (int)(wv[q] > v[m]) | ((int)(wv[q] == v[m]) & (int)(j < i));
             }
         }
     }
-    float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-    mx = wave_max(mx);
-    float ex[4], sum = 0.f;
+    float mx = v[0];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 1; m < MB; ++m) mx = fmaxf(mx, v[m]);
+    mx = wave_max(mx);
+    float ex[MB], sum = 0.f;
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
         ex[m] = (lane + 64 * m < E) ? expf(v[m] - mx) : 0.f;
         sum += ex[m];
     }
     const float inv = 1.0f / wave_sum(sum);
     // selected (expert, probability) by slot
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < MB; ++m) {
         const int i = lane + 64 * m;
         if (i < E && rank[m] < K) {
             s_sel[wave][rank[m]] = i;
@@ -154,14 +207,20 @@ __global__ __launch_bounds__(256) void router_rank_kernel(RouterArgs a) {
 }  // namespace
 
 int launch_router_topk(const RouterArgs& a, void* stream) {
-    if (a.E > kMaxE || a.K > kMaxK || a.h % 16) return (int)hipErrorInvalidValue;
+    if (a.E > kMaxE || a.K > kMaxK || a.h % 64) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(router_logits_kernel,
                        dim3((unsigned)((a.T + kTT - 1) / kTT), (unsigned)((a.E + kTE - 1) / kTE)),
                        dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(router_rank_kernel, dim3((unsigned)((a.T + 3) / 4)), dim3(256), 0, st, a);
+    const dim3 g((unsigned)((a.T + 3) / 4));
+    if (a.E <= 64)
+        hipLaunchKernelGGL(router_rank_kernel<1>, g, dim3(256), 0, st, a);
+    else if (a.E <= 128)
+        hipLaunchKernelGGL(router_rank_kernel<2>, g, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL(router_rank_kernel<4>, g, dim3(256), 0, st, a);
     return (int)hipGetLastError();
 }
 

@@ -117,8 +117,11 @@ __device__ __forceinline__ void load_chunk(const void* x, int x_bf16, int c, boo
 // flight together, then one wait (which also covers this wave's earlier
 // loads).  The chunk address must be in range.
 __device__ __forceinline__ void load_chunk_coherent(const float* x, int c, float (&v)[32]) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
     const float* p = x + c * 32;
-    float4* q = reinterpret_cast<float4*>(v);
+    // the asm writes these locals themselves (writing the array through a
+    // vector-typed view would let the compiler assume the array unchanged)
+    f4 q0, q1, q2, q3, q4, q5, q6, q7;
     asm volatile(
         "global_load_dwordx4 %0, %8, off sc1\n\t"
         "global_load_dwordx4 %1, %8, off offset:16 sc1\n\t"
@@ -129,10 +132,14 @@ __device__ __forceinline__ void load_chunk_coherent(const float* x, int c, float
         "global_load_dwordx4 %6, %8, off offset:96 sc1\n\t"
         "global_load_dwordx4 %7, %8, off offset:112 sc1\n\t"
         "s_waitcnt vmcnt(0)"
-        : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]),
-          "=&v"(q[6]), "=&v"(q[7])
+        : "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3), "=&v"(q4), "=&v"(q5), "=&v"(q6), "=&v"(q7)
         : "v"(p)
         : "memory");
+    const f4 q[8] = {q0, q1, q2, q3, q4, q5, q6, q7};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[4 * j + k] = q[j][k];
 }
 
 // Scale and bias of one group, loaded as the aligned dword holding the bf16
@@ -428,12 +435,16 @@ __device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int
     }
 }
 
-// act values carry the launch number mod 4 in their two lowest mantissa bits,
-// so a consumer can tell this launch's value from the previous one's; it
-// clears them before use (a relative change below 2^-21, the same in every
-// launch, and the consumer rounds act to f16 anyway).
+// act values carry the launch number mod 2^kActTagBits in their lowest
+// mantissa bits, so a consumer can tell this launch's value from an earlier
+// one's; it clears them before use (a relative change below 2^(bits-23), the
+// same in every launch; the consumer rounds act to f16 anyway).
+#ifndef M1MOE_ACT_TAG_BITS
+#define M1MOE_ACT_TAG_BITS 8
+#endif
+constexpr uint32_t kActTagMask = (1u << M1MOE_ACT_TAG_BITS) - 1u;
 __device__ __forceinline__ float act_tagged(float v, uint32_t tag) {
-    return __uint_as_float((__float_as_uint(v) & ~3u) | (tag & 3u));
+    return __uint_as_float((__float_as_uint(v) & ~kActTagMask) | (tag & kActTagMask));
 }
 
 template <int CPL, int UG, int GSL>
@@ -676,7 +687,7 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
                 load_chunk_coherent(src, cc, v[0]);
                 uint32_t bad = 0;
 #pragma unroll
-                for (int i = 0; i < 32; ++i) bad |= (__float_as_uint(v[0][i]) ^ tag) & 3u;
+                for (int i = 0; i < 32; ++i) bad |= (__float_as_uint(v[0][i]) ^ tag) & kActTagMask;
                 if (__all(!live || bad == 0)) break;
                 if (it >= a.spin_limit) {
                     flag_error(a.err, 4u);
@@ -686,7 +697,7 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
                 __builtin_amdgcn_s_sleep(1);
             }
             // the value without its tag bits (the same in every launch), or 0
-            const uint32_t keep = live ? ~3u : 0u;
+            const uint32_t keep = live ? ~kActTagMask : 0u;
 #pragma unroll
             for (int i = 0; i < 32; ++i) v[0][i] = __uint_as_float(__float_as_uint(v[0][i]) & keep);
             inv = lane_scale_prep<1>(v, xc);

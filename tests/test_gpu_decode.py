@@ -254,6 +254,38 @@ def test_decode_is_deterministic(cfg0):
     assert all(np.array_equal(runs[0].view(np.uint32), r.view(np.uint32)) for r in runs[1:])
 
 
+@pytest.mark.parametrize("given", [False, True])
+def test_repeated_launches_are_bitwise_identical(cfg0, given):
+    """Many launches cycling over two layers and two inputs: each (layer, x)
+    must give the same bits every time.  The gate/up -> down hand-off lets
+    the down role read act before the stores are acknowledged and rely on the
+    launch tag in each value; if the tag check were skipped, a few percent of
+    launches would combine act of the previous launch."""
+    blk = MoEBlock(cfg0.ctx)
+    h, K, E = cfg0.shape.hidden, cfg0.shape.top_k, cfg0.shape.num_experts
+    xs = cfg0.x_bf16(2, stream=61)
+    dx = [cfg0.ctx.to_device(xs[i]) for i in range(2)]
+    didx = [cfg0.ctx.to_device(np.array([(7 * i + 8 * k) % E for k in range(K)], np.int32))
+            for i in range(2)]
+    dw = cfg0.ctx.to_device(np.full(K, 1.0 / K, np.float32))
+    out = cfg0.ctx.alloc(h * 4)
+    say(f"160 launches, {'given' if given else 'routed'} top-K")
+    first, bad = {}, []
+    for it in range(160):
+        layer, xi = it % 2, (it // 2) % 2
+        if given:
+            blk.forward_given_topk(layer, dx[xi], "bf16", didx[xi], dw, None, out)
+        else:
+            blk.forward(layer, dx[xi], "bf16", None, out)
+        cfg0.ctx.sync()
+        y = out.download(np.float32).view(np.uint32).copy()
+        if (layer, xi) not in first:
+            first[(layer, xi)] = y
+        elif not np.array_equal(y, first[(layer, xi)]):
+            bad.append(it)
+    assert not bad, f"launches {bad[:10]} differ from the first launch of the same input"
+
+
 def test_bad_expert_index_is_reported_not_read(cfg0):
     blk = MoEBlock(cfg0.ctx)
     K, h, E = cfg0.shape.top_k, cfg0.shape.hidden, cfg0.shape.num_experts

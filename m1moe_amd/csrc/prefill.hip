@@ -290,19 +290,30 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles
             s2[m] = f16x2{s16, s16};
             b2[m] = f16x2{b16, b16};
         }
+        // two k-steps at a time: their B fragments are read from LDS and their
+        // A fragments unpacked before the 2 * 4 * NMAT MFMAs that use them
+        constexpr int SP = W >= 2 ? 2 : 1;
 #pragma unroll
-        for (int s = 0; s < W; ++s) {
-            f16x8 af[NMAT];
+        for (int s0 = 0; s0 < W; s0 += SP) {
+            f16x8 bf[SP][kTN / 16];
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) af[m] = dequant_word(st.aw[m][s], s2[m], b2[m]);
+            for (int t = 0; t < SP; ++t)
 #pragma unroll
-            for (int j = 0; j < kTN / 16; ++j) {
-                const f16x8 bf = *reinterpret_cast<const f16x8*>(
-                    &s_b[buf][(j * 16 + r) * kRow + (kq * W + s) * 16]);
+                for (int j = 0; j < kTN / 16; ++j)
+                    bf[t][j] = *reinterpret_cast<const f16x8*>(
+                        &s_b[buf][(j * 16 + r) * kRow + (kq * W + s0 + t) * 16]);
+            f16x8 af[SP][NMAT];
 #pragma unroll
-                for (int m = 0; m < NMAT; ++m)
-                    acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[m], bf, acc[m][j], 0, 0, 0);
-            }
+            for (int t = 0; t < SP; ++t)
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) af[t][m] = dequant_word(st.aw[m][s0 + t], s2[m], b2[m]);
+#pragma unroll
+            for (int t = 0; t < SP; ++t)
+#pragma unroll
+                for (int j = 0; j < kTN / 16; ++j)
+#pragma unroll
+                    for (int m = 0; m < NMAT; ++m)
+                        acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][m], bf[t][j], acc[m][j], 0, 0, 0);
         }
     };
 

@@ -46,6 +46,8 @@
 // scaled back exactly before the cross-lane reduction.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "device.hpp"
 #include "internal.hpp"
 
@@ -151,8 +153,8 @@ __device__ __forceinline__ uint32_t sb_sel(uint32_t elem) { return (elem & 1u) ?
 // Scales each of a lane's chunks by one power of two (its largest element
 // into [2^13, 2^14)) and converts them to the f16 pairs of the nibble dot
 // product.  Returns the inverse scale.
-template <int N>
-__device__ __forceinline__ float lane_scale_prep(float (&v)[N][32], XChunk (&xc)[N]) {
+template <int N, class XC>
+__device__ __forceinline__ float lane_scale_prep(float (&v)[N][32], XC (&xc)[N]) {
     float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < N; ++j)
@@ -171,9 +173,18 @@ __device__ __forceinline__ float lane_scale_prep(float (&v)[N][32], XChunk (&xc)
 
 // One 32-column chunk of one row: s * sum(n x) + b * sum(x), in the lane's
 // scaled units.
+// (LO: the split chunk's lo half takes part; without it the split chunk's
+// hi half alone, exact for bf16 inputs.)
+template <bool LO = false>
 __device__ __forceinline__ float chunk_term(const uint4& w, uint32_t sw, uint32_t bw,
                                             uint32_t sel, const XChunk& xc, const NibK& nk) {
     const float d = nib_dot32(w, xc, nk) - xc.off;
+    return fmaf(bf16_pick(sw, sel), d, bf16_pick(bw, sel) * xc.xs);
+}
+template <bool LO>
+__device__ __forceinline__ float chunk_term(const uint4& w, uint32_t sw, uint32_t bw,
+                                            uint32_t sel, const XChunk2& xc, const NibK& nk) {
+    const float d = nib_dot32<LO>(w, xc, nk) - xc.off;
     return fmaf(bf16_pick(sw, sel), d, bf16_pick(bw, sel) * xc.xs);
 }
 
@@ -447,9 +458,15 @@ __device__ __forceinline__ float act_tagged(float v, uint32_t tag) {
     return __uint_as_float((__float_as_uint(v) & ~kActTagMask) | (tag & kActTagMask));
 }
 
-template <int CPL, int UG, int GSL>
+// The gate/up input chunk: split hi + lo where the registers allow it
+// (one chunk per lane); two chunks per lane keep single f16 to stay within
+// the 168 VGPRs of three waves per SIMD.
+template <int CPL>
+using GUChunk = typename std::conditional<CPL == 1, XChunk2, XChunk>::type;
+
+template <int CPL, int UG, int GSL, bool LO>
 __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, const GUGeo& m,
-                                           const GUTile<CPL, UG>& t, const XChunk (&xc)[CPL],
+                                           const GUTile<CPL, UG>& t, const GUChunk<CPL> (&xc)[CPL],
                                            float inv, uint32_t tag) {
     const uint32_t groups = (uint32_t)a.h >> (5 + GSL);
     const NibK nk = nib_consts();
@@ -463,8 +480,8 @@ __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, 
             const int c = m.c0 + 64 * j;
             const uint32_t cc = (uint32_t)min(c, a.Cg - 1);
             const uint32_t sel = sb_sel(rc * groups + (cc >> GSL));
-            const float tg = chunk_term(t.gw[u][j], t.gs[u][j], t.gb[u][j], sel, xc[j], nk);
-            const float tu = chunk_term(t.uw[u][j], t.us[u][j], t.ub[u][j], sel, xc[j], nk);
+            const float tg = chunk_term<LO>(t.gw[u][j], t.gs[u][j], t.gb[u][j], sel, xc[j], nk);
+            const float tu = chunk_term<LO>(t.uw[u][j], t.us[u][j], t.ub[u][j], sel, xc[j], nk);
             const bool ok = m.ok && c < a.Cg;
             pg += ok ? tg : 0.f;
             pu += ok ? tu : 0.f;
@@ -491,7 +508,8 @@ __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, 
 // are current.
 template <int CPL, int UG, int GSL>
 __device__ void gu_role(const FusedArgs& a, const Layout& L, int g, int wave, int lane,
-                        const RouteLDS& r, const XChunk (&xc)[CPL], float inv, uint32_t tag) {
+                        const RouteLDS& r, const GUChunk<CPL> (&xc)[CPL], float inv,
+                        uint32_t tag) {
     const GUGeo m = gu_geo(lane, a.Cg, a.seg_g);
     const int tps = a.tiles_per_slot;
     const int total = a.K * tps;
@@ -526,7 +544,13 @@ __device__ void gu_role(const FusedArgs& a, const Layout& L, int g, int wave, in
             cnt_k = k;
             cnt_n = 0;
         }
-        if (expert_of(T) >= 0) gu_compute<CPL, UG, GSL>(a, k, row_of(T), m, t, xc, inv, tag);
+        if (expert_of(T) >= 0) {
+            // bf16 inputs are exact in f16: the lo half of a split chunk is 0
+            if (std::is_same<GUChunk<CPL>, XChunk2>::value && !a.x_bf16)
+                gu_compute<CPL, UG, GSL, true>(a, k, row_of(T), m, t, xc, inv, tag);
+            else
+                gu_compute<CPL, UG, GSL, false>(a, k, row_of(T), m, t, xc, inv, tag);
+        }
         ++cnt_n;
     };
     GUTile<CPL, UG> A, B;
@@ -759,7 +783,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
     const uint32_t tag = s_tag;
 
     // the input vector does not depend on the routing: prepare it meanwhile
-    XChunk xc[CPL];
+    GUChunk<CPL> xc[CPL];
     float inv = 1.f;
     if (is_gu) {
         const GUGeo m = gu_geo(lane, a.Cg, a.seg_g);

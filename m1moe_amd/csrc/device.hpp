@@ -63,6 +63,58 @@ __device__ __forceinline__ void prep_chunk(const float* v, XChunk& c) {
     c.xs = xs;
 }
 
+// The same chunk with each input split as hi + lo, hi = f16(x), lo =
+// f16(x - hi): 22 significant bits instead of 11.  Both halves go through the
+// same nibble dot products (twice the v_dot2, 16 more VGPRs per chunk); off
+// and xs are those of hi + lo.  Used for the gate/up input, whose rounding
+// the SwiGLU and the down projection can amplify when their sums cancel.
+struct XChunk2 {
+    half2_t X[16];  // hi pairs, ordered as XChunk::X
+    half2_t L[16];  // lo pairs
+    float off;
+    float xs;
+};
+
+__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);  // x - hi is exact in f32
+}
+
+__device__ __forceinline__ void prep_chunk(const float* v, XChunk2& c) {
+    float off = 0.f, xs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float* b = v + 8 * i;
+        _Float16 h[8], l[8];
+        split_f16(b[0], h[0], l[0]);
+        split_f16(b[4], h[4], l[4]);
+        split_f16(b[2], h[2], l[2]);
+        split_f16(b[6], h[6], l[6]);
+        split_f16(b[1] * 0.0625f, h[1], l[1]);
+        split_f16(b[5] * 0.0625f, h[5], l[5]);
+        split_f16(b[3] * 0.0625f, h[3], l[3]);
+        split_f16(b[7] * 0.0625f, h[7], l[7]);
+        c.X[4 * i + 0] = half2_t{h[0], h[4]};
+        c.X[4 * i + 1] = half2_t{h[1], h[5]};
+        c.X[4 * i + 2] = half2_t{h[2], h[6]};
+        c.X[4 * i + 3] = half2_t{h[3], h[7]};
+        c.L[4 * i + 0] = half2_t{l[0], l[4]};
+        c.L[4 * i + 1] = half2_t{l[1], l[5]};
+        c.L[4 * i + 2] = half2_t{l[2], l[6]};
+        c.L[4 * i + 3] = half2_t{l[3], l[7]};
+        float se = 0.f, so = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            se += (float)h[e] + (float)l[e];
+            so += (float)h[e + 1] + (float)l[e + 1];
+        }
+        off += se + so;
+        xs += se + 16.f * so;
+    }
+    c.off = 1024.f * off;
+    c.xs = xs;
+}
+
 // Masks and the f16 magic of the nibble expansion, held in registers so that
 // each expansion is one v_and_or_b32 (masks in SGPRs, magic in a VGPR; with
 // literal operands the compiler emits a separate AND and OR).
@@ -90,6 +142,29 @@ __device__ __forceinline__ float nib_dot32(const uint4& w, const XChunk& c, cons
         a1 = dot2_f16((v8 & k.hi) | k.mg, c.X[4 * i + 3], a1);
     }
     return a0 + a1;
+}
+
+// The same over a split chunk: hi and lo pairs against the same expansions
+// (LO = false: hi only, for inputs that are exact in f16, whose lo is 0).
+template <bool LO>
+__device__ __forceinline__ float nib_dot32(const uint4& w, const XChunk2& c, const NibK& k) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t v = ws[i], v8 = v >> 8;
+        const uint32_t n0 = (v & k.lo) | k.mg, n1 = (v & k.hi) | k.mg;
+        const uint32_t n2 = (v8 & k.lo) | k.mg, n3 = (v8 & k.hi) | k.mg;
+        a0 = dot2_f16(n0, c.X[4 * i + 0], a0);
+        a1 = dot2_f16(n1, c.X[4 * i + 1], a1);
+        if (LO) a2 = dot2_f16(n0, c.L[4 * i + 0], a2);
+        if (LO) a3 = dot2_f16(n1, c.L[4 * i + 1], a3);
+        a0 = dot2_f16(n2, c.X[4 * i + 2], a0);
+        a1 = dot2_f16(n3, c.X[4 * i + 3], a1);
+        if (LO) a2 = dot2_f16(n2, c.L[4 * i + 2], a2);
+        if (LO) a3 = dot2_f16(n3, c.L[4 * i + 3], a3);
+    }
+    return LO ? (a0 + a1) + (a2 + a3) : a0 + a1;
 }
 
 // v_perm_b32 selectors that move the low / high bf16 of a dword into the

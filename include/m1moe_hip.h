@@ -221,6 +221,112 @@ int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T,
 int32_t m1moe_dequant_debug(m1moe_ctx_t ctx, int32_t layer, int32_t expert,
                             int32_t proj, float* d_out);
 
+/* ---- dense decoder step around the MoE block ---------------------------- */
+
+/* Building blocks (each asynchronous on the context stream; all vectors f32
+ * unless stated, weights bf16 row-major). */
+
+/* out[i] = x[i] * rsqrt(sum(x^2)/n + eps) * w[i]   (rmsNormSum + rmsNormApply,
+ * Shaders.metal:96-134; InferenceEngine.swift:298-320).  n <= 65536. */
+int32_t m1moe_rmsnorm(m1moe_ctx_t ctx, const float* d_x, const uint16_t* d_w,
+                      float* d_out, int32_t n, float eps);
+
+/* y[r] = sum_c W[r][c] * x[c] (+ residual[r] when d_residual is non-null)
+ * (matvecBF16, Shaders.metal:328-358; residualAdd :152-162).
+ * cols % 8 == 0, cols <= 65536. */
+int32_t m1moe_matvec_bf16(m1moe_ctx_t ctx, const uint16_t* d_w,
+                          const float* d_x, const float* d_residual,
+                          float* d_y, int32_t rows, int32_t cols);
+
+/* Decode attention of one query position over seq_len cached positions
+ * (attnScores + attnSoftmax + attnValues, Shaders.metal:209-326, dispatched as
+ * InferenceEngine.swift:349-399): per head h,
+ * s_p = (q_h . k_p[h / hpkv]) / sqrt(head_dim), p_s = softmax(s), out_h =
+ * sum_p p_p v_p[h / hpkv].  q f32 [num_heads x head_dim]; caches f32
+ * [>= seq_len x num_kv_heads*head_dim]; out f32 [num_heads x head_dim].
+ * head_dim is 64, 128 or 256; num_heads % num_kv_heads == 0;
+ * 1 <= seq_len <= 65536. */
+int32_t m1moe_attention_decode(m1moe_ctx_t ctx, const float* d_q,
+                               const float* d_kcache, const float* d_vcache,
+                               float* d_out, int32_t num_heads,
+                               int32_t num_kv_heads, int32_t head_dim,
+                               int32_t seq_len);
+
+/* Index of the largest of n values, ties to the lower index, written to
+ * d_idx (greedy sampling, InferenceEngine.swift:550-555: a scan from x[0]
+ * with a strict >, so NaN never wins except at index 0). */
+int32_t m1moe_argmax(m1moe_ctx_t ctx, const float* d_x, int32_t n,
+                     int32_t* d_idx);
+
+/* The whole decode step (InferenceEngine.forward and runLayer,
+ * InferenceEngine.swift:125-266, which ran norms/projections/attention on
+ * Metal and q/k norms, RoPE, the KV store, router and top-K on the CPU with
+ * three syncs per layer): token embedding; per layer input RMSNorm, q/k/v
+ * matvecs, per-head q/k RMSNorm (when the model has it), RoPE, f32 KV cache
+ * store, attention, o_proj + residual, post-attention RMSNorm, the MoE block
+ * of the context; final RMSNorm, lm_head, greedy argmax — all on the GPU with
+ * no host sync.  The token and the position live in device memory, so each
+ * step reads the previous step's argmax and a greedy loop can be captured in
+ * a graph and replayed. */
+typedef struct m1moe_dec* m1moe_dec_t;
+
+/* Attention and vocabulary of a model (ModelSpec.swift AttentionSpec and
+ * vocabSize).  hidden and num_layers come from the MoE context.
+ * head_dim is 64, 128 or 256 (even); num_heads % num_kv_heads == 0;
+ * 1 <= max_seq <= 65536; vocab >= 1. */
+typedef struct {
+    int32_t vocab;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t max_seq;   /* KV cache positions */
+    int32_t qk_norm;   /* per-head q/k RMSNorm before RoPE (OLMoE) */
+    float rope_theta;
+    float rms_eps;
+} m1moe_dec_shape;
+
+/* dense tensors of a model (bf16, row-major) */
+enum {
+    M1MOE_W_EMBED = 0,      /* [vocab x hidden]                 model.embed_tokens */
+    M1MOE_W_LM_HEAD = 1,    /* [vocab x hidden]                 lm_head */
+    M1MOE_W_FINAL_NORM = 2, /* [hidden]                         model.norm */
+    M1MOE_W_IN_NORM = 3,    /* [hidden]       per layer         input_layernorm */
+    M1MOE_W_POST_NORM = 4,  /* [hidden]       per layer         post_attention_layernorm */
+    M1MOE_W_Q = 5,          /* [heads*hd x hidden]   per layer  self_attn.q_proj */
+    M1MOE_W_K = 6,          /* [kv_heads*hd x hidden]           self_attn.k_proj */
+    M1MOE_W_V = 7,          /* [kv_heads*hd x hidden]           self_attn.v_proj */
+    M1MOE_W_O = 8,          /* [hidden x heads*hd]              self_attn.o_proj */
+    M1MOE_W_Q_NORM = 9,     /* [head_dim]     per layer         self_attn.q_norm (first head_dim
+                               values, applied to every head: applyHeadRMSNorm, InferenceEngine.swift:538-548) */
+    M1MOE_W_K_NORM = 10     /* [head_dim]     per layer         self_attn.k_norm */
+};
+
+/* The decoder uses the MoE context's layers, stream and error flag; destroy
+ * it before the context. */
+int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* shape,
+                         m1moe_dec_t* out);
+void m1moe_dec_destroy(m1moe_dec_t dec);
+/* count must be the tensor's element count (above); layer is ignored for
+ * the model-level tensors. */
+int32_t m1moe_dec_upload(m1moe_dec_t dec, int32_t which, int32_t layer,
+                         const uint16_t* host_bf16, uint64_t count);
+/* Position 0 and an empty KV cache (InferenceEngine.reset, :159-163; the
+ * positions past the new one are never read, so only the position is
+ * rewritten).  Enqueued on the context stream. */
+int32_t m1moe_dec_reset(m1moe_dec_t dec);
+/* One step at the current device-side position: reads the token from
+ * d_token_in (int32 device), writes the greedy next token to d_token_out
+ * (may be the same address) and advances the position.  d_logits (nullable)
+ * receives f32 [vocab].  A prompt is fed as steps with d_token_in =
+ * &prompt[i]; a greedy loop passes out = in, or &toks[i+1] to keep them.  A token outside
+ * [0, vocab) is embedded as token 0, and with the cache full (position ==
+ * max_seq) nothing is stored and the position stays; either sets the device
+ * error flag, reported by the next m1moe_sync. */
+int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in,
+                       int32_t* d_token_out, float* d_logits);
+/* The current position (waits for the context stream). */
+int32_t m1moe_dec_position(m1moe_dec_t dec, int32_t* pos);
+
 /* ---- seeded synthetic inputs (host-only; bench and test data) ----------
  * Counter-based: value i of tensor `tensor_id` under `seed` is a function of
  * (seed, tensor_id, i) only, so any slice can be generated independently.

@@ -39,6 +39,28 @@ class MoEShape(ctypes.Structure):
     ]
 
 
+class DecShape(ctypes.Structure):
+    """m1moe_dec_shape: ModelSpec.vocabSize/rmsNormEps + AttentionSpec (ModelSpec.swift:19-22,
+    62-75); qk_norm = the OLMoE per-head q/k RMSNorm (InferenceEngine.swift:55)."""
+
+    _fields_ = [
+        ("vocab", c_int32),
+        ("num_heads", c_int32),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("max_seq", c_int32),
+        ("qk_norm", c_int32),
+        ("rope_theta", c_float),
+        ("rms_eps", c_float),
+    ]
+
+
+# dense tensor ids of m1moe_dec_upload
+(W_EMBED, W_LM_HEAD, W_FINAL_NORM, W_IN_NORM, W_POST_NORM, W_Q, W_K, W_V, W_O, W_Q_NORM,
+ W_K_NORM) = range(11)
+W_PER_LAYER = (W_IN_NORM, W_POST_NORM, W_Q, W_K, W_V, W_O, W_Q_NORM, W_K_NORM)
+
+
 class M1MoEError(RuntimeError):
     """A non-zero status from the C ABI, with m1moe_last_error()'s message."""
 
@@ -87,6 +109,18 @@ _PROTOTYPES = [
     ("m1moe_moe_prefill", c_int32,
      [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("m1moe_dequant_debug", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p]),
+    ("m1moe_rmsnorm", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_float]),
+    ("m1moe_matvec_bf16", c_int32,
+     [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32]),
+    ("m1moe_attention_decode", c_int32,
+     [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32]),
+    ("m1moe_argmax", c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    ("m1moe_dec_create", c_int32, [c_void_p, POINTER(DecShape), POINTER(c_void_p)]),
+    ("m1moe_dec_destroy", None, [c_void_p]),
+    ("m1moe_dec_upload", c_int32, [c_void_p, c_int32, c_int32, POINTER(c_uint16), c_uint64]),
+    ("m1moe_dec_reset", c_int32, [c_void_p]),
+    ("m1moe_dec_step", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("m1moe_dec_position", c_int32, [c_void_p, POINTER(c_int32)]),
     ("m1moe_synth_normal_bf16", c_int32,
      [c_uint64, c_uint64, c_uint64, c_float, c_int32, c_void_p]),
     ("m1moe_synth_normal_f32", c_int32, [c_uint64, c_uint64, c_uint64, c_float, c_void_p]),

@@ -17,6 +17,7 @@
 #include <string>
 #include <vector>
 
+#include "ctx.hpp"
 #include "internal.hpp"
 #include "m1moe_hip.h"
 
@@ -62,110 +63,8 @@ Geom make_geom(const m1moe_moe_shape& s) {
 
 }  // namespace m1moe
 
-using m1moe::fail;
-
-struct m1moe_event {
-    hipEvent_t ev;
-};
-
-struct m1moe_graph {
-    hipGraph_t graph;
-    hipGraphExec_t exec;
-};
-
-struct m1moe_ctx {
-    int32_t device = 0;
-    m1moe_moe_shape shape{};
-    m1moe::Geom g{};
-    hipStream_t own_stream = nullptr;
-    hipStream_t stream = nullptr;
-    uint8_t* arena = nullptr;        // [L][E] expert blocks
-    uint16_t* routers = nullptr;     // [L][E][h] bf16
-    float* biases = nullptr;         // [L][E]
-    std::vector<bool> has_bias;
-    std::vector<bool> layer_loaded;
-    std::vector<bool> router_loaded;
-    // scratch
-    float* logits = nullptr;         // [cap][E]
-    int32_t* topk_idx = nullptr;     // [cap][K]
-    float* topk_w = nullptr;         // [cap][K]
-    uint32_t* counters = nullptr;    // [cap]
-    float* act = nullptr;            // [K][I]
-    uint8_t* sync = nullptr;         // decode hand-off state: slots | gu_cnt | seen
-    uint64_t sync_bytes = 0, sync_gu_cnt = 0, sync_seen = 0;
-    uint32_t* err = nullptr;         // sticky device error flag
-    // prefill scratch, grown on demand to the largest T seen (pf_cap tokens)
-    int32_t pf_cap = 0;
-    _Float16* pf_xq = nullptr;       // [cap][h]
-    float* pf_xinv = nullptr;        // [cap]
-    int32_t* pf_pos = nullptr;       // [cap*K]
-    int32_t* pf_sorted = nullptr;    // [cap*K]
-    int32_t* pf_eoff = nullptr;      // [E+1]
-    int32_t* pf_toff = nullptr;      // [E+1]
-    int32_t* pf_texp = nullptr;      // [cap*K/kPfTN + E + 1]
-    _Float16* pf_act = nullptr;      // [cap*K][I]
-    float* pf_y = nullptr;           // [cap*K][h]
-    std::set<void*> allocs;
-};
-
 namespace {
-
-#define HIP_TRY(expr)                                                                        \
-    do {                                                                                     \
-        hipError_t e_ = (expr);                                                              \
-        if (e_ != hipSuccess)                                                                \
-            return fail(M1MOE_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));      \
-    } while (0)
-
-int32_t device_alloc(void** p, uint64_t bytes, const char* what) {
-    hipError_t e = hipMalloc(p, bytes ? bytes : 1);
-    if (e != hipSuccess) {
-        *p = nullptr;
-        return fail(M1MOE_ERR_OOM, "hipMalloc(%s, %llu bytes) failed: %s", what,
-                    (unsigned long long)bytes, hipGetErrorString(e));
-    }
-    return M1MOE_OK;
-}
-
-int32_t check_ctx(m1moe_ctx_t ctx) {
-    if (!ctx) return fail(M1MOE_ERR_INVALID, "null context");
-    return M1MOE_OK;
-}
-
-int32_t set_device(m1moe_ctx_t ctx) {
-    HIP_TRY(hipSetDevice(ctx->device));
-    return M1MOE_OK;
-}
-
-int32_t check_layer(m1moe_ctx_t ctx, int32_t layer) {
-    if (layer < 0 || layer >= ctx->shape.num_layers)
-        return fail(M1MOE_ERR_INVALID, "layer %d out of range [0, %d)", layer,
-                    ctx->shape.num_layers);
-    return M1MOE_OK;
-}
-
-int32_t check_dev_ptr(const void* p, const char* what, bool nullable) {
-    if (!p) {
-        if (nullable) return M1MOE_OK;
-        return fail(M1MOE_ERR_INVALID, "%s is null", what);
-    }
-    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
-        return fail(M1MOE_ERR_INVALID, "%s must be 16-byte aligned", what);
-    return M1MOE_OK;
-}
-
-int32_t check_dtype(int32_t dt) {
-    if (dt != M1MOE_F32 && dt != M1MOE_BF16)
-        return fail(M1MOE_ERR_INVALID, "x_dtype %d is not M1MOE_F32 or M1MOE_BF16", dt);
-    return M1MOE_OK;
-}
-
-int32_t launched(int rc, const char* what) {
-    if (rc != (int)hipSuccess)
-        return fail(M1MOE_ERR_HIP, "launch of %s failed: %s", what,
-                    hipGetErrorString((hipError_t)rc));
-    return M1MOE_OK;
-}
+using namespace m1moe;
 
 constexpr int32_t kSpinLimit = 1 << 20;  // bounded waits in the decode kernel (~1 s)
 
@@ -317,7 +216,7 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     void* owned[] = {ctx->arena,   ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
                      ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
-                     ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y};
+                     ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part};
     for (void* p : owned)
         if (p) (void)hipFree(p);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -534,6 +433,14 @@ int32_t m1moe_sync(m1moe_ctx_t ctx) {
             return fail(M1MOE_ERR_DEVICE,
                         "prefill met a group scale with |s| >= 0.25, outside its f16 "
                         "dequantisation range (device flag 0x%x)", flag);
+        if (flag & 16u)
+            return fail(M1MOE_ERR_DEVICE,
+                        "a decoder step read a token id outside the vocabulary; token 0 was "
+                        "embedded (device flag 0x%x)", flag);
+        if (flag & 32u)
+            return fail(M1MOE_ERR_DEVICE,
+                        "a decoder step ran with the KV cache full (position == max_seq); "
+                        "nothing was stored (device flag 0x%x)", flag);
         return fail(M1MOE_ERR_DEVICE,
                     "a decode hand-off wait timed out (device flag 0x%x); state was reset", flag);
     }

@@ -128,4 +128,57 @@ int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_dequant(const uint8_t* expert_base, const ProjView& p, int32_t gs, float* out,
                    void* stream);
 
+// ---- dense decoder step (dense.hip) ----
+
+// One weight segment of a bf16 matvec: y[r] = W[r] . x (+ res[r]).
+struct MvSeg {
+    const uint16_t* w;           // [rows][cols]
+    float* y;                    // [rows]
+    const float* res;            // [rows] or null
+    int32_t rows;
+};
+// Up to three segments sharing the input x (rows concatenated).
+struct MvArgs {
+    MvSeg seg[3];
+    const float* x;              // [cols]
+    int32_t rows, cols;          // total rows of the segments, shared columns
+};
+
+struct AttnArgs {
+    const float* q;              // [num_heads][head_dim]
+    const float* kcache;         // [>= seq][num_kv_heads * head_dim]
+    const float* vcache;
+    float* out;                  // [num_heads][head_dim]
+    float* partial;              // [num_heads][chunks][head_dim + 2] scratch
+    const int32_t* seq_ptr;      // position of the current token (seq = pos + 1), or null
+    int32_t seq_len;             // used when seq_ptr is null
+    int32_t max_seq;
+    int32_t num_heads, num_kv_heads, hpkv, head_dim;
+    float scale;                 // 1 / sqrt(head_dim)
+};
+
+struct DenseStepArgs {
+    const int32_t* token;        // device: the step's input token
+    int32_t* pos;                // device: the current position
+    const uint16_t* embed;       // [vocab][h]
+    float* x_out;                // embedding output [h]
+    float *q, *k, *v;            // projections of the current layer
+    const uint16_t* q_norm;      // [layers][head_dim] or null
+    const uint16_t* k_norm;
+    float* kcache;               // [layers][max_seq][num_kv_heads * head_dim]
+    float* vcache;
+    uint32_t* err;               // sticky device error flag
+    int32_t vocab, h, num_heads, num_kv_heads, head_dim, max_seq, qk_norm;
+    float rope_theta, eps;
+};
+
+int launch_set_i32(int32_t* p, int32_t v, void* stream);
+int launch_rmsnorm(const float* x, const uint16_t* w, float* out, int n, float eps, void* stream);
+int launch_matvec_bf16(const MvArgs& a, void* stream);
+int launch_attention(const AttnArgs& a, int max_positions, void* stream);
+int attention_partial_floats(int num_heads, int head_dim, int max_positions);
+int launch_argmax(const float* x, int n, int32_t* out, int32_t* pos, int max_seq, void* stream);
+int launch_embed(const DenseStepArgs& a, void* stream);
+int launch_qk_rope_kv(const DenseStepArgs& a, int layer, void* stream);
+
 }  // namespace m1moe

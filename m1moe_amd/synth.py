@@ -68,6 +68,54 @@ CONFIGS = {
 }
 
 
+@dataclass(frozen=True)
+class DecoderWorkload:
+    """A full decoder: the MoE layers of `moe` stacked num_layers deep, dense
+    weights random-init, `prompt` random token ids then `gen` greedy steps."""
+    name: str
+    moe: Workload
+    num_layers: int
+    vocab: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    rope_theta: float
+    qk_norm: bool
+    prompt: int
+    gen: int
+    rms_eps: float = 1e-5
+    description: str = ""
+
+    def shape(self) -> MoEShape:
+        return self.moe.shape(self.num_layers)
+
+    def dec_shape(self, max_seq: Optional[int] = None):
+        from ._lib import DecShape
+        return DecShape(self.vocab, self.num_heads, self.num_kv_heads, self.head_dim,
+                        int(max_seq or (self.prompt + self.gen)), 1 if self.qk_norm else 0,
+                        self.rope_theta, self.rms_eps)
+
+
+_OLMOE_MOE = Workload("olmoe", dict(hidden=2048, num_experts=64, top_k=8, intermediate=1024,
+                                    group_size=64, norm_topk_prob=False))
+_MIXTRAL_MOE = Workload("mixtral", dict(hidden=4096, num_experts=8, top_k=2, intermediate=14336,
+                                        group_size=64, norm_topk_prob=False))
+
+# BASELINE.json configs 1 and 4 (architecture values of configs/olmoe-1b-7b.json and
+# configs/mixtral-8x7b.json; Mixtral's norm_topk_prob is that file's false)
+DECODERS = {
+    "cfg1": DecoderWorkload("cfg1", _OLMOE_MOE, 16, 50304, 16, 16, 128, 10000.0, True, 128, 128,
+                            description="OLMoE-1B-7B-shaped decoder, 16 layers, 128-token "
+                                        "prompt then 128 greedy steps, batch 1"),
+    "cfg4": DecoderWorkload("cfg4", _MIXTRAL_MOE, 32, 32000, 32, 8, 128, 1e6, False, 2048, 64,
+                            description="Mixtral-8x7B-shaped decoder, 32 layers, 2048-token "
+                                        "context then 64 greedy steps, batch 1"),
+    # small decoders for tests: GQA 2:1, KV cache over two attention chunks
+    "tiny_dec": DecoderWorkload("tiny_dec", CONFIGS["tiny"], 2, 300, 2, 1, 64, 10000.0, True,
+                                8, 8),
+}
+
+
 def _threads() -> int:
     return max(1, min(16, os.cpu_count() or 1))
 
@@ -124,6 +172,35 @@ def zipf_logit_bias(num_experts: int, s: float) -> Optional[np.ndarray]:
         return None
     ranks = np.arange(1, num_experts + 1, dtype=np.float64)
     return (-s * np.log(ranks)).astype(np.float32)
+
+
+_TID_DENSE = 5 << 56
+NORM_SIGMA = 0.1       # norm weights bf16 1 + N(0, 0.1)
+
+
+def dense_weight(wl: DecoderWorkload, seed: int, which: int, layer: int) -> np.ndarray:
+    """Dense tensor `which` (m1moe_amd._lib.W_*) of `layer` as bf16 bits, shaped
+    [rows, cols] for matrices.  Embedding N(0, 1); projections and lm_head
+    N(0, 1/sqrt(cols)), so every projection keeps unit-RMS inputs at unit
+    scale; norm weights 1 + N(0, 0.1)."""
+    from . import _lib as L
+    h = wl.moe.shape_kwargs["hidden"]
+    qd, kvd, hd = wl.num_heads * wl.head_dim, wl.num_kv_heads * wl.head_dim, wl.head_dim
+    dims = {L.W_EMBED: (wl.vocab, h), L.W_LM_HEAD: (wl.vocab, h), L.W_FINAL_NORM: (h,),
+            L.W_IN_NORM: (h,), L.W_POST_NORM: (h,), L.W_Q: (qd, h), L.W_K: (kvd, h),
+            L.W_V: (kvd, h), L.W_O: (h, qd), L.W_Q_NORM: (hd,), L.W_K_NORM: (hd,)}[which]
+    n = int(np.prod(dims))
+    tid = _TID_DENSE | (which << 32) | (layer if which in L.W_PER_LAYER else 0)
+    if len(dims) == 1:
+        return f32_to_bf16(normal_f32(seed, tid, n, NORM_SIGMA) + np.float32(1.0))
+    sigma = 1.0 if which == L.W_EMBED else 1.0 / float(np.sqrt(dims[1]))
+    return normal_bf16(seed, tid, n, sigma).reshape(dims)
+
+
+def prompt_tokens(wl: DecoderWorkload, seed: int, n: Optional[int] = None) -> np.ndarray:
+    """n (default wl.prompt) token ids uniform in [0, vocab), int32."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return rng.integers(0, wl.vocab, size=int(n or wl.prompt), dtype=np.int64).astype(np.int32)
 
 
 def bf16_to_f32(a: np.ndarray) -> np.ndarray:

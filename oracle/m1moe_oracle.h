@@ -126,6 +126,47 @@ int32_t orc_moe_prefill(const orc_shape* s, const uint8_t* layer_image,
                         const float* residual, float* out, int32_t* idx,
                         float* w, int32_t nthreads);
 
+
+/* ---- dense decoder step (dense_oracle.c) ---------------------------------- */
+
+/* embedToken, InferenceEngine.swift:482-488: row `token` of the bf16 table. */
+void orc_embed(const uint16_t* embed_bf16, int32_t token, int32_t hidden,
+               float* out);
+
+/* rmsNormSum + rmsNormApply, Shaders.metal:96-134:
+ * out = x * rsqrt(sum(x^2)/n + eps) * w. */
+void orc_rmsnorm(const float* x, const uint16_t* w_bf16, float* out, int32_t n,
+                 float eps);
+
+/* matvecBF16, Shaders.metal:328-358, then residualAdd (:152-162) when
+ * residual is not NULL: y = W x (+ residual), W bf16 [rows x cols]. */
+void orc_matvec_bf16(const uint16_t* w_bf16, const float* x,
+                     const float* residual, float* y, int32_t rows,
+                     int32_t cols);
+
+/* applyHeadRMSNorm, InferenceEngine.swift:538-548 (in place; w has head_dim
+ * entries shared by all heads). */
+void orc_head_rmsnorm(float* buf, int32_t num_heads, int32_t head_dim,
+                      const uint16_t* w_bf16, float eps);
+
+/* applyRoPE, InferenceEngine.swift:521-536 (in place; pairs (p, p+hd/2)). */
+void orc_rope(float* buf, int32_t num_heads, int32_t head_dim, float theta,
+              int32_t pos);
+
+/* attnScores + attnSoftmax + attnValues, Shaders.metal:209-326 with the
+ * dispatch of InferenceEngine.swift:349-399: caches [seq_len x kv_dim] f32,
+ * GQA head h reads kv head h / (num_heads / num_kv_heads), scale
+ * 1/sqrt(head_dim).  scratch: seq_len doubles.  Returns 0, or -1 on bad
+ * dimensions. */
+int32_t orc_attention(const float* q, const float* kcache, const float* vcache,
+                      float* out, int32_t num_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t seq_len, double* scratch);
+
+/* sampleToken at temperature 0, InferenceEngine.swift:550-555: scan from
+ * x[0] with a strict >, so ties go to the lower index and NaN never replaces
+ * (nor is replaced at index 0). */
+int32_t orc_argmax(const float* x, int32_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,13 @@ def load() -> ctypes.CDLL:
         "orc_moe_decode_given_topk": (c_int32, [POINTER(OrcShape), P, P, P, P, P, P]),
         "orc_moe_prefill": (c_int32, [POINTER(OrcShape), P, P, P, c_int32, P, P, P, P, P,
                                       c_int32]),
+        "orc_embed": (None, [P, c_int32, c_int32, P]),
+        "orc_rmsnorm": (None, [P, P, P, c_int32, c_float]),
+        "orc_matvec_bf16": (None, [P, P, P, P, c_int32, c_int32]),
+        "orc_head_rmsnorm": (None, [P, c_int32, c_int32, P, c_float]),
+        "orc_rope": (None, [P, c_int32, c_int32, c_float, c_int32]),
+        "orc_attention": (c_int32, [P, P, P, P, c_int32, c_int32, c_int32, c_int32, P]),
+        "orc_argmax": (c_int32, [P, c_int32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -229,3 +236,134 @@ def proj_arrays(s: OrcShape, block: np.ndarray, proj: int):
     sc = block[base[1]:base[1] + rows * g * 2].view(np.uint16).reshape(rows, g)
     bi = block[base[2]:base[2] + rows * g * 2].view(np.uint16).reshape(rows, g)
     return w, sc, bi
+
+
+# ---- dense decoder step (dense_oracle.c) -------------------------------------------------
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def _u16(a):
+    return np.ascontiguousarray(a, np.uint16)
+
+
+def embed(table_bf16, token: int) -> np.ndarray:
+    t = _u16(table_bf16)
+    h = t.shape[-1]
+    out = np.empty(h, dtype=np.float32)
+    load().orc_embed(_p(t), int(token), h, _p(out))
+    return out
+
+
+def rmsnorm(x, w_bf16, eps: float) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    load().orc_rmsnorm(_p(x), _p(_u16(w_bf16)), _p(out), x.size, float(eps))
+    return out
+
+
+def matvec_bf16(w_bf16, x, residual=None) -> np.ndarray:
+    w = _u16(w_bf16)
+    rows, cols = w.shape
+    y = np.empty(rows, dtype=np.float32)
+    res = None if residual is None else _f32(residual)
+    load().orc_matvec_bf16(_p(w), _p(_f32(x)), _p(res), _p(y), rows, cols)
+    return y
+
+
+def head_rmsnorm(x, num_heads: int, head_dim: int, w_bf16, eps: float) -> np.ndarray:
+    out = _f32(x).copy()
+    load().orc_head_rmsnorm(_p(out), num_heads, head_dim, _p(_u16(w_bf16)), float(eps))
+    return out
+
+
+def rope(x, num_heads: int, head_dim: int, theta: float, pos: int) -> np.ndarray:
+    out = _f32(x).copy()
+    load().orc_rope(_p(out), num_heads, head_dim, float(theta), int(pos))
+    return out
+
+
+def attention(q, kcache, vcache, num_heads: int, num_kv_heads: int, head_dim: int,
+              seq_len: int) -> np.ndarray:
+    """kcache/vcache [>= seq_len x num_kv_heads*head_dim] f32."""
+    out = np.empty(num_heads * head_dim, dtype=np.float32)
+    scratch = np.empty(max(1, seq_len), dtype=np.float64)
+    rc = load().orc_attention(_p(_f32(q)), _p(_f32(kcache)), _p(_f32(vcache)), _p(out),
+                              num_heads, num_kv_heads, head_dim, int(seq_len), _p(scratch))
+    if rc:
+        raise ValueError(f"orc_attention returned {rc}")
+    return out
+
+
+def argmax(x) -> int:
+    x = _f32(x)
+    return int(load().orc_argmax(_p(x), x.size))
+
+
+class DecoderOracle:
+    """InferenceEngine.forward at temperature 0 (InferenceEngine.swift:125-266)
+    composed from the oracle's functions, with an f32 KV cache of max_seq
+    positions per layer.
+
+    tensors[name] for name in embed, lm_head, final_norm (model level) and
+    tensors[name][layer] for in_norm, post_norm, q, k, v, o, q_norm, k_norm:
+    bf16 (uint16) arrays, matrices as [rows x cols].  images[layer] and
+    routers[layer]: the MoE block's expert image and bf16 router."""
+
+    def __init__(self, moe: OrcShape, num_layers: int, vocab: int, num_heads: int,
+                 num_kv_heads: int, head_dim: int, max_seq: int, qk_norm: bool,
+                 rope_theta: float, eps: float, tensors: dict, images, routers):
+        self.moe, self.L = moe, num_layers
+        self.vocab, self.nh, self.nkv, self.hd = vocab, num_heads, num_kv_heads, head_dim
+        self.max_seq, self.qk_norm = max_seq, bool(qk_norm)
+        self.theta, self.eps = float(rope_theta), float(eps)
+        self.t, self.images, self.routers = tensors, images, routers
+        kvd = num_kv_heads * head_dim
+        self.kc = np.zeros((num_layers, max_seq, kvd), dtype=np.float32)
+        self.vc = np.zeros((num_layers, max_seq, kvd), dtype=np.float32)
+        self.pos = 0
+        # smallest gap, over the layers of the last step, between the K-th and
+        # (K+1)-th router logit: where it is tiny the selected set (and so the
+        # step's output) changes under arbitrarily small input perturbations
+        self.route_margin = np.inf
+
+    def reset(self) -> None:
+        """InferenceEngine.reset (:159-163)."""
+        self.pos = 0
+        self.kc[:] = 0
+        self.vc[:] = 0
+
+    def step(self, token: int):
+        """One forward step; returns (greedy next token, logits f32 [vocab])."""
+        if self.pos >= self.max_seq:
+            raise ValueError("KV cache full")
+        t, pos = self.t, self.pos
+        nh, nkv, hd = self.nh, self.nkv, self.hd
+        res = embed(t["embed"], token)                                          # :129-131
+        self.route_margin = np.inf
+        for layer in range(self.L):
+            xn = rmsnorm(res, t["in_norm"][layer], self.eps)                    # :181-184
+            q = matvec_bf16(t["q"][layer], xn)                                  # :185-190
+            k = matvec_bf16(t["k"][layer], xn)
+            v = matvec_bf16(t["v"][layer], xn)
+            if self.qk_norm:                                                    # :199-208
+                q = head_rmsnorm(q, nh, hd, t["q_norm"][layer], self.eps)
+                k = head_rmsnorm(k, nkv, hd, t["k_norm"][layer], self.eps)
+            q = rope(q, nh, hd, self.theta, pos)                                # :210-213
+            k = rope(k, nkv, hd, self.theta, pos)
+            self.kc[layer, pos] = k                                             # :215-220
+            self.vc[layer, pos] = v
+            a = attention(q, self.kc[layer], self.vc[layer], nh, nkv, hd, pos + 1)  # :226
+            res2 = matvec_bf16(t["o"][layer], a, residual=res)                  # :227-233
+            hmid = rmsnorm(res2, t["post_norm"][layer], self.eps)               # :234-236
+            res, _, _, lg = moe_decode(self.moe, self.images[layer], self.routers[layer],
+                                       hmid, residual=res2)                     # :240-266
+            if self.moe.top_k < self.moe.num_experts:
+                srt = np.sort(lg)[::-1]
+                k = self.moe.top_k
+                self.route_margin = min(self.route_margin, float(srt[k - 1] - srt[k]))
+        self.pos += 1                                                           # :138
+        xn = rmsnorm(res, t["final_norm"], self.eps)                            # :142-144
+        logits = matvec_bf16(t["lm_head"], xn)                                  # :145-147
+        return argmax(logits), logits                                           # :151-155

@@ -1,0 +1,343 @@
+"""GPU parity of the dense decoder step and the whole decoder against the CPU
+oracle (oracle/dense_oracle.c, oracle.DecoderOracle), through the C ABI.
+
+Tolerances: every sum on the GPU is f32 in its own order against the
+oracle's f64, so the building blocks are held to relative L2 1e-5 (argmax
+bit-exact).  The MoE block rounds its input and the SwiGLU activations to
+f16 for the nibble dot products (its own parity bar is relative L2 1e-2), so
+decoder logits are held to the north-star bar of relative L2 1e-2, and greedy
+tokens must agree wherever the oracle's top-2 logit margin exceeds the logit
+error bound.
+"""
+import numpy as np
+import pytest
+
+import m1moe_amd as m
+from m1moe_amd import _lib, synth
+from m1moe_amd.decoder import Decoder, DenseOps
+from oracle import oracle as orc
+
+from cases import rel_l2, say
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(77)
+NAMES = {_lib.W_EMBED: "embed", _lib.W_LM_HEAD: "lm_head", _lib.W_FINAL_NORM: "final_norm",
+         _lib.W_IN_NORM: "in_norm", _lib.W_POST_NORM: "post_norm", _lib.W_Q: "q", _lib.W_K: "k",
+         _lib.W_V: "v", _lib.W_O: "o", _lib.W_Q_NORM: "q_norm", _lib.W_K_NORM: "k_norm"}
+LOGIT_TOL = 1e-2
+
+
+def bf16(a):
+    return synth.f32_to_bf16(np.asarray(a, np.float32))
+
+
+@pytest.fixture(scope="module")
+def ops_ctx():
+    say("dense ops context")
+    ctx = m.HIPContext(m.make_shape(128, 8, 2, 64, 64))
+    yield ctx, DenseOps(ctx)
+    ctx.close()
+
+
+# ---- building blocks --------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 100, 2048, 4096, 5000])
+def test_rmsnorm(ops_ctx, n):
+    ctx, ops = ops_ctx
+    x = RNG.normal(0, 3, n).astype(np.float32)
+    w = bf16(RNG.normal(1, 0.1, n))
+    dx, dw, dout = ctx.to_device(x), ctx.to_device(w), ctx.alloc(4 * n)
+    say(f"rmsnorm n={n}")
+    ops.rmsnorm(dx, dw, dout, n, 1e-5)
+    ctx.sync()
+    assert rel_l2(dout.download(np.float32), orc.rmsnorm(x, w, 1e-5)) < 1e-6
+
+
+@pytest.mark.parametrize("rows,cols,with_res", [(1, 8, False), (37, 200, True), (2048, 2048, True),
+                                                (6144, 2048, False), (2048, 4096, True),
+                                                (50304, 2048, False), (3, 65536, False)])
+def test_matvec_bf16(ops_ctx, rows, cols, with_res):
+    ctx, ops = ops_ctx
+    w = bf16(RNG.normal(0, 1 / np.sqrt(cols), (rows, cols)))
+    x = RNG.normal(0, 1, cols).astype(np.float32)
+    r = RNG.normal(0, 1, rows).astype(np.float32) if with_res else None
+    dw, dx, dy = ctx.to_device(w), ctx.to_device(x), ctx.alloc(4 * rows)
+    dr = ctx.to_device(r) if with_res else None
+    say(f"matvec_bf16 {rows}x{cols} residual={with_res}")
+    ops.matvec_bf16(dw, dx, dr, dy, rows, cols)
+    ctx.sync()
+    got = dy.download(np.float32)
+    want = orc.matvec_bf16(w, x, residual=r)
+    assert rel_l2(got, want) < 1e-5
+
+
+@pytest.mark.parametrize("nh,nkv,hd,sl", [(16, 16, 128, 1), (4, 2, 64, 255), (4, 2, 64, 256),
+                                           (4, 2, 64, 257), (32, 8, 128, 1000), (2, 1, 256, 700),
+                                           (16, 16, 128, 4096)])
+def test_attention_decode(ops_ctx, nh, nkv, hd, sl):
+    ctx, ops = ops_ctx
+    kvd = nkv * hd
+    q = RNG.normal(0, 1, nh * hd).astype(np.float32)
+    kc = RNG.normal(0, 1, (sl, kvd)).astype(np.float32)
+    vc = RNG.normal(0, 1, (sl, kvd)).astype(np.float32)
+    dq, dk, dv, dout = ctx.to_device(q), ctx.to_device(kc), ctx.to_device(vc), ctx.alloc(4 * nh * hd)
+    say(f"attention nh={nh} nkv={nkv} hd={hd} seq={sl}")
+    ops.attention_decode(dq, dk, dv, dout, nh, nkv, hd, sl)
+    ctx.sync()
+    want = orc.attention(q, kc, vc, nh, nkv, hd, sl)
+    assert rel_l2(dout.download(np.float32), want) < 1e-5
+
+
+@pytest.mark.parametrize("case", ["random", "ties", "nan0", "nan_mid", "neg_inf", "one"])
+def test_argmax(ops_ctx, case):
+    ctx, ops = ops_ctx
+    n = 50304
+    x = RNG.normal(0, 1, n).astype(np.float32)
+    if case == "ties":
+        x[[7, 3000, 50000]] = 9.0
+    elif case == "nan0":
+        x[0] = np.nan
+    elif case == "nan_mid":
+        x[[5, 60, 40000]] = np.nan
+    elif case == "neg_inf":
+        x[:] = -np.inf
+    elif case == "one":
+        x = x[:1]
+        n = 1
+    dx, di = ctx.to_device(x), ctx.alloc(16)
+    say(f"argmax {case}")
+    ops.argmax(dx, n, di)
+    ctx.sync()
+    assert int(di.download(np.int32, 1)[0]) == orc.argmax(x)
+
+
+# ---- the decoder -------------------------------------------------------------------------
+
+class Pair:
+    """The same seeded model on the GPU (Decoder) and in the oracle."""
+
+    def __init__(self, wl, seed, max_seq, num_layers=None):
+        self.wl = wl
+        L = num_layers or wl.num_layers
+        shape = wl.moe.shape(L)
+        say(f"decoder {wl.name} layers={L} max_seq={max_seq} seed={seed}")
+        self.ctx = m.HIPContext(shape)
+        ds = wl.dec_shape(max_seq)
+        self.dec = Decoder(self.ctx, ds)
+        tensors = {}
+        for which, name in NAMES.items():
+            if which in _lib.W_PER_LAYER:
+                tensors[name] = [synth.dense_weight(wl, seed, which, l) for l in range(L)]
+            else:
+                tensors[name] = synth.dense_weight(wl, seed, which, 0)
+        self.dec.upload_all(lambda which, l: tensors[NAMES[which]][l]
+                            if which in _lib.W_PER_LAYER else tensors[NAMES[which]])
+        images, routers = [], []
+        for l in range(L):
+            img = synth.layer_image(shape, seed, l)
+            r = synth.router(shape, seed, l)
+            self.ctx.upload_layer_experts(l, img)
+            self.ctx.upload_router(l, r)
+            images.append(img)
+            routers.append(r)
+        self.orc = orc.DecoderOracle(orc.from_moe_shape(shape), L, wl.vocab, wl.num_heads,
+                                     wl.num_kv_heads, wl.head_dim, max_seq, wl.qk_norm,
+                                     wl.rope_theta, wl.rms_eps, tensors, images, routers)
+
+    def close(self):
+        self.dec.close()
+        self.ctx.close()
+
+
+def check_step(got_tok, got_logits, want_tok, want_logits, where):
+    rel = rel_l2(got_logits, want_logits)
+    assert rel < LOGIT_TOL, f"{where}: logits rel L2 {rel:.2e}"
+    if got_tok != want_tok:
+        top2 = np.sort(want_logits.astype(np.float64))[-2:]
+        bound = 4 * LOGIT_TOL * np.linalg.norm(want_logits) / np.sqrt(want_logits.size)
+        assert top2[1] - top2[0] < bound, f"{where}: token {got_tok} != {want_tok}"
+    return rel
+
+
+def test_decoder_tiny_teacher_forced_over_two_attention_chunks():
+    """280 forced tokens: the cache crosses the 256-position attention chunk."""
+    p = Pair(synth.DECODERS["tiny_dec"], seed=11, max_seq=300)
+    try:
+        toks = synth.prompt_tokens(p.wl, 5, 280)
+        rels = []
+        for i, t in enumerate(toks):
+            g_tok, g_lg = p.dec.forward(int(t), return_logits=True)
+            w_tok, w_lg = p.orc.step(int(t))
+            rels.append(check_step(g_tok, g_lg, w_tok, w_lg, f"step {i}"))
+        assert p.dec.position() == 280
+        rels = np.array(rels)
+        say(f"tiny decoder logits rel L2: median {np.median(rels):.2e}, worst before "
+            f"position 256 {rels[:256].max():.2e}, from 256 on {rels[256:].max():.2e}")
+    finally:
+        p.close()
+
+
+def test_decoder_reset_restarts_the_sequence():
+    p = Pair(synth.DECODERS["tiny_dec"], seed=12, max_seq=32)
+    try:
+        toks = synth.prompt_tokens(p.wl, 6, 6)
+        first = [p.dec.forward(int(t), return_logits=True)[1] for t in toks]
+        p.dec.reset()
+        assert p.dec.position() == 0
+        again = [p.dec.forward(int(t), return_logits=True)[1] for t in toks]
+        for a, b in zip(first, again):
+            np.testing.assert_array_equal(a, b)
+    finally:
+        p.close()
+
+
+def test_decoder_greedy_loop_in_a_graph():
+    """Prompt steps read &prompt[i]; greedy steps chain toks[i] -> toks[i+1];
+    the captured loop is replayed three times against the eager run."""
+    p = Pair(synth.DECODERS["tiny_dec"], seed=13, max_seq=64)
+    try:
+        ctx, dec = p.ctx, p.dec
+        prompt = synth.prompt_tokens(p.wl, 7, 8)
+        n_gen = 24
+        # eager reference run through forward() (one host round trip per step)
+        eager = []
+        tok = None
+        for t in prompt:
+            tok = dec.forward(int(t))
+        for _ in range(n_gen):
+            eager.append(tok)
+            tok = dec.forward(tok)
+        eager.append(tok)
+        P = len(prompt)
+        dprompt = ctx.to_device(prompt)
+        dpred = ctx.alloc(4 * P)
+        dtoks = ctx.alloc(4 * (n_gen + 1))  # toks[i+1] = greedy(toks[i]); toks[0] unused
+        ctx.graph_begin()
+        dec.reset()
+        for i in range(P):
+            dec.step_device(dprompt.addr + 4 * i, dpred.addr + 4 * i)
+        for i in range(n_gen):
+            src = dpred.addr + 4 * (P - 1) if i == 0 else dtoks.addr + 4 * i
+            dec.step_device(src, dtoks.addr + 4 * (i + 1))
+        graph = ctx.graph_end()
+        for rep in range(3):
+            say(f"graph replay {rep}")
+            graph.launch()
+            ctx.sync()
+            assert int(dpred.download(np.int32)[P - 1]) == eager[0], f"replay {rep}"
+            assert dtoks.download(np.int32).tolist()[1:] == eager[1:], f"replay {rep}"
+            assert dec.position() == P + n_gen
+            dtoks.upload(np.zeros(n_gen + 1, np.int32))  # eager work between replays
+        # the oracle, fed the same tokens, picks the same ones wherever its
+        # top-2 margin is clear of the logit error
+        p.orc.reset()
+        for t in prompt:
+            w, lg = p.orc.step(int(t))
+        for i in range(n_gen + 1):
+            top2 = np.sort(lg.astype(np.float64))[-2:]
+            assert w == eager[i] or top2[1] - top2[0] < 1e-2, f"greedy step {i}"
+            if i < n_gen:
+                w, lg = p.orc.step(eager[i])
+    finally:
+        p.close()
+
+
+def test_decoder_dense_only_is_tight():
+    """With the MoE block's expert weights all zero (scales and biases 0) the
+    block adds only the residual, so the step is the dense kernels alone:
+    logits to relative L2 1e-5 over positions on both sides of 256."""
+    wl = synth.DECODERS["tiny_dec"]
+    p = Pair(wl, seed=15, max_seq=300)
+    try:
+        zero = np.zeros_like(p.orc.images[0])
+        for l in range(wl.num_layers):
+            p.ctx.upload_layer_experts(l, zero)
+            p.orc.images[l] = zero
+        worst = 0.0
+        for i, t in enumerate(synth.prompt_tokens(wl, 8, 270)):
+            g_tok, g_lg = p.dec.forward(int(t), return_logits=True)
+            w_tok, w_lg = p.orc.step(int(t))
+            rel = rel_l2(g_lg, w_lg)
+            assert rel < 1e-5, f"step {i}: rel L2 {rel:.2e}"
+            worst = max(worst, rel)
+            if g_tok != w_tok:
+                top2 = np.sort(w_lg.astype(np.float64))[-2:]
+                assert top2[1] - top2[0] < 1e-4, f"step {i}: token {g_tok} != {w_tok}"
+        say(f"dense-only decoder worst logits rel L2 {worst:.2e}")
+    finally:
+        p.close()
+
+
+def test_decoder_olmoe_dims_two_layers():
+    """Full OLMoE widths (h 2048, 16x128 heads, vocab 50304, 64 experts top-8),
+    two layers, four prompt tokens and four greedy steps."""
+    p = Pair(synth.DECODERS["cfg1"], seed=2026, max_seq=16, num_layers=2)
+    try:
+        toks = synth.prompt_tokens(p.wl, 2026, 4)
+        tok = None
+        for i, t in enumerate(toks):
+            g_tok, g_lg = p.dec.forward(int(t), return_logits=True)
+            w_tok, w_lg = p.orc.step(int(t))
+            check_step(g_tok, g_lg, w_tok, w_lg, f"prompt {i}")
+            tok = w_tok
+        for i in range(4):
+            g_tok, g_lg = p.dec.forward(tok, return_logits=True)
+            w_tok, w_lg = p.orc.step(tok)
+            check_step(g_tok, g_lg, w_tok, w_lg, f"greedy {i}")
+            tok = w_tok
+    finally:
+        p.close()
+
+
+def test_decoder_mixtral_gqa_dims_one_layer():
+    """Mixtral widths (h 4096, 32 q / 8 kv heads, vocab 32000, 8 experts
+    top-2, intermediate 14336), one layer, three steps."""
+    p = Pair(synth.DECODERS["cfg4"], seed=5, max_seq=8, num_layers=1)
+    try:
+        for i, t in enumerate(synth.prompt_tokens(p.wl, 5, 3)):
+            g_tok, g_lg = p.dec.forward(int(t), return_logits=True)
+            w_tok, w_lg = p.orc.step(int(t))
+            check_step(g_tok, g_lg, w_tok, w_lg, f"step {i}")
+    finally:
+        p.close()
+
+
+def test_decoder_reports_bad_token_and_full_cache():
+    p = Pair(synth.DECODERS["tiny_dec"], seed=14, max_seq=3)
+    try:
+        say("bad token")
+        with pytest.raises(m.M1MoEError, match="vocabulary"):
+            p.dec.forward(p.wl.vocab + 5)
+        p.dec.reset()
+        for t in (1, 2, 3):
+            p.dec.forward(t)
+        assert p.dec.position() == 3
+        say("full cache")
+        with pytest.raises(m.M1MoEError, match="KV cache full"):
+            p.dec.forward(4)
+        assert p.dec.position() == 3
+        p.dec.reset()
+        p.dec.forward(1)  # usable again after the error
+        assert p.dec.position() == 1
+    finally:
+        p.close()
+
+
+def test_decoder_rejects_missing_weights_and_bad_shapes():
+    ctx = m.HIPContext(m.make_shape(128, 8, 2, 64, 64))
+    try:
+        wl = synth.DECODERS["tiny_dec"]
+        dec = Decoder(ctx, wl.dec_shape(8))
+        tok = ctx.to_device(np.zeros(4, np.int32))
+        with pytest.raises(m.M1MoEError, match="not uploaded"):
+            dec.step_device(tok, tok)
+        bad = wl.dec_shape(8)
+        bad.head_dim = 96
+        with pytest.raises(m.M1MoEError, match="head_dim"):
+            Decoder(ctx, bad)
+        with pytest.raises(m.M1MoEError, match="count"):
+            dec.upload(_lib.W_Q, 0, np.zeros(5, np.uint16))
+        dec.close()
+    finally:
+        ctx.close()

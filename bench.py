@@ -76,19 +76,31 @@ def copy_calibration(m, nbytes: int, reps: int) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="cfg0", choices=["cfg0", "cfg2", "cfg3"],
-                    help="cfg0/cfg2: batch-1 decode; cfg3: 512-token prefill")
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 200; cfg1: 5 jobs, cfg4: 1 job)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps (default 20; cfg1/cfg4: 1 job)")
+    ap.add_argument("--config", default="cfg0", choices=["cfg0", "cfg1", "cfg2", "cfg3", "cfg4"],
+                    help="cfg0/cfg2: MoE-layer batch-1 decode; cfg3: 512-token MoE prefill; "
+                         "cfg1/cfg4: whole decoder, prompt then greedy steps (a step is one "
+                         "such job)")
     ap.add_argument("--replicas", type=int, default=0,
                     help="distinct layer replicas (default: >= 1 GiB of selected experts per pass)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU-baseline sample (0 disables it)")
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--eager", action="store_true",
+                    help="cfg1/cfg4: launch every step's kernels from the host instead of "
+                         "replaying the captured one-step graph (for kernel traces)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES bytes (to scale HBM "
                          "byte counters against a plain copy of known size), then exit")
     args = ap.parse_args()
+    job_defaults = {"cfg1": (5, 1), "cfg4": (1, 1)}.get(args.config, (200, 20))
+    if args.steps is None:
+        args.steps = job_defaults[0]
+    if args.warmup is None:
+        args.warmup = job_defaults[1]
 
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -105,6 +117,8 @@ def main() -> int:
 
     if args.config == "cfg3":
         return bench_prefill(args, m, synth)
+    if args.config in ("cfg1", "cfg4"):
+        return bench_decoder(args, m, synth)
 
     wl = synth.CONFIGS[args.config]
     one = wl.shape(1)
@@ -225,6 +239,174 @@ def main() -> int:
         "parity": {"topk_exact": idx_ok, "rel_l2": rel},
     }
     print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+DECODER_METRIC = "decoder greedy decode tok/s at batch 1 (prompt then greedy steps)"
+
+
+def decoder_step_bytes(wl, eb: int, pos: int) -> int:
+    """HBM bytes one decode step at position pos must move: every dense
+    weight once (lm_head, q/k/v/o, norms, one embedding row), each layer's
+    MoE block (K expert blocks, bf16 router, f32 input/residual/output), and
+    the K/V cache rows 0..pos of every layer (read) plus row pos (written)."""
+    s = wl.shape()
+    h, L, V = s.hidden, s.num_layers, wl.vocab
+    qd, kvd = wl.num_heads * wl.head_dim, wl.num_kv_heads * wl.head_dim
+    dense = 2 * (V * h + h + L * (2 * h + 2 * qd * h + 2 * kvd * h)
+                 + (2 * L * wl.head_dim if wl.qk_norm else 0)) + 2 * h
+    moe = L * (s.top_k * eb + s.num_experts * h * 2 + 3 * h * 4)
+    kv = L * 2 * kvd * 4 * (pos + 2)
+    return dense + moe + kv
+
+
+def bench_decoder(args, m, synth) -> int:
+    """cfg1 / cfg4: the whole decoder (Decoder, m1moe_dec_*), seeded random
+    weights, a random prompt forwarded token by token then greedy steps
+    (Sources/bench/main.swift:136-163).  One HIP graph holds one
+    sequence-mode step; a job replays it prompt + gen times after a reset."""
+    from m1moe_amd import _lib
+    from m1moe_amd.decoder import Decoder
+    from oracle import oracle as orc
+
+    wl = synth.DECODERS[args.config]
+    shape = wl.shape()
+    L, P, G = shape.num_layers, wl.prompt, wl.gen
+    eb = m.expert_bytes(shape)
+    log(f"{wl.description}: {L} layers, {L * shape.num_experts * eb / 2**30:.1f} GiB of experts")
+    t0 = time.time()
+    ctx = m.HIPContext(shape, device=0)
+    dec = Decoder(ctx, wl.dec_shape(P + G))
+    keep = args.cpu_seconds > 0
+    tensors = {}
+    names = {_lib.W_EMBED: "embed", _lib.W_LM_HEAD: "lm_head", _lib.W_FINAL_NORM: "final_norm",
+             _lib.W_IN_NORM: "in_norm", _lib.W_POST_NORM: "post_norm", _lib.W_Q: "q",
+             _lib.W_K: "k", _lib.W_V: "v", _lib.W_O: "o", _lib.W_Q_NORM: "q_norm",
+             _lib.W_K_NORM: "k_norm"}
+    for which, name in names.items():
+        if which in (_lib.W_Q_NORM, _lib.W_K_NORM) and not wl.qk_norm:
+            continue
+        layers = range(L) if which in _lib.W_PER_LAYER else [0]
+        arrs = []
+        for layer in layers:
+            w = synth.dense_weight(wl, args.seed, which, layer)
+            dec.upload(which, layer, w)
+            arrs.append(w if keep else None)
+        tensors[name] = arrs if which in _lib.W_PER_LAYER else arrs[0]
+    images, routers = [], []
+    for layer in range(L):
+        img = synth.layer_image(shape, args.seed, layer)
+        r = synth.router(shape, args.seed, layer)
+        ctx.upload_layer_experts(layer, img)
+        ctx.upload_router(layer, r)
+        images.append(img if keep else None)
+        routers.append(r)
+        del img
+    log(f"weights synthesised and uploaded in {time.time() - t0:.1f}s")
+    prompt = synth.prompt_tokens(wl, args.seed)
+
+    # parity (and the CPU baseline): the first prompt tokens through the GPU
+    # decoder eagerly and through the scalar oracle on one thread
+    cpu = None
+    parity = None
+    if keep:
+        oracle = orc.DecoderOracle(orc.from_moe_shape(shape), L, wl.vocab, wl.num_heads,
+                                   wl.num_kv_heads, wl.head_dim, P + G, wl.qk_norm,
+                                   wl.rope_theta, wl.rms_eps, tensors, images, routers)
+        dec.reset()
+        worst, n, t_cpu, tok_ok = 0.0, 0, 0.0, True
+        while n < P and (n == 0 or t_cpu < args.cpu_seconds):
+            g_tok, g_lg = dec.forward(int(prompt[n]), return_logits=True)
+            t1 = time.perf_counter()
+            w_tok, w_lg = oracle.step(int(prompt[n]))
+            t_cpu += time.perf_counter() - t1
+            rel = float(np.linalg.norm(g_lg - w_lg) / np.linalg.norm(w_lg))
+            worst = max(worst, rel)
+            top2 = np.sort(w_lg.astype(np.float64))[-2:]
+            tok_ok &= g_tok == w_tok or bool(top2[1] - top2[0] < 1e-2)
+            n += 1
+        parity = {"steps_checked": n, "logits_rel_l2_max": worst, "greedy_tokens_agree": tok_ok}
+        log(f"parity over {n} steps: logits rel L2 max {worst:.2e}, tokens agree {tok_ok}")
+        if worst > 1e-2 or not tok_ok:
+            log("parity FAILED; not reporting throughput")
+            return 1
+        cpu = {"value": round(n / t_cpu, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"{n} decoder steps of {args.config} (positions 0..{n - 1}) through the "
+                         f"scalar oracle on 1 thread ({t_cpu:.1f}s); host CPU: {cpu_model()}"}
+        log(f"cpu baseline: {cpu['value']} tok/s")
+        del oracle, images, tensors
+
+    cap = P + G + 1
+    seq = ctx.alloc(4 * cap)
+    init = np.concatenate([prompt, np.zeros(cap - P, np.int32)])
+    # eager sequence-mode run: the reference tokens for the graph replays
+    want = dec.generate(prompt, G)
+    if args.eager:
+        class _Eager:
+            @staticmethod
+            def launch():
+                dec.step_seq(seq, P, cap)
+        graph = _Eager()
+    else:
+        ctx.graph_begin()
+        dec.step_seq(seq, P, cap)
+        graph = ctx.graph_end()
+    ev = [ctx.event() for _ in range(3)]
+    t_pre = t_gen = 0.0
+    same = True
+    for it in range(args.warmup + args.steps):
+        seq.upload(init)
+        dec.reset()
+        ctx.sync()
+        ev[0].record()
+        for _ in range(P):
+            graph.launch()
+        ev[1].record()
+        for _ in range(G):
+            graph.launch()
+        ev[2].record()
+        ctx.sync()
+        same &= seq.download(np.int32)[P:].tolist() == want.tolist()
+        if it >= args.warmup:
+            t_pre += ev[0].elapsed_ms(ev[1])
+            t_gen += ev[1].elapsed_ms(ev[2])
+    if not same:
+        log("graph replays produced other tokens than the eager run")
+        return 1
+    jobs = args.steps
+    gen_tok_s = G * jobs / (t_gen * 1e-3)
+    pre_tok_s = P * jobs / (t_pre * 1e-3)
+    us_gen = t_gen * 1e3 / (G * jobs)
+    bytes_step = sum(decoder_step_bytes(wl, eb, P + i) for i in range(G)) / G
+    gbs = bytes_step / (us_gen * 1e-6) / 1e9
+    log(f"prefill {P} tok: {t_pre / jobs:.2f} ms ({pre_tok_s:.1f} tok/s); decode {G} tok: "
+        f"{t_gen / jobs:.2f} ms ({gen_tok_s:.1f} tok/s, {us_gen:.1f} us/token, {gbs:.0f} GB/s)")
+    line = {
+        "metric": DECODER_METRIC, "value": round(gen_tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round((t_pre + t_gen) / jobs, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 dense weights, u4 experts x f16 pairs -> f32; f32 KV cache",
+        "data": "synthetic (seeded; random-init weights, random prompt ids)",
+        "config": {"workload": wl.description, "config": args.config, "layers": L,
+                   "hidden": shape.hidden, "vocab": wl.vocab, "num_heads": wl.num_heads,
+                   "num_kv_heads": wl.num_kv_heads, "head_dim": wl.head_dim,
+                   "num_experts": shape.num_experts, "top_k": shape.top_k,
+                   "intermediate": shape.intermediate, "prompt_tokens": P, "gen_tokens": G,
+                   "step": "one job = reset + prompt + greedy steps, each token one " +
+                           ("host launch of its kernels" if args.eager else
+                            "replay of a one-step HIP graph"),
+                   "prefill_tok_s": round(pre_tok_s, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "decoder step (all kernels of one greedy token)",
+                     "bytes_per_launch": int(bytes_step), "us_per_launch": round(us_gen, 3)},
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    dec.close()
     ctx.close()
     return 0
 

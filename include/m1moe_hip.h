@@ -324,6 +324,17 @@ int32_t m1moe_dec_reset(m1moe_dec_t dec);
  * error flag, reported by the next m1moe_sync. */
 int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in,
                        int32_t* d_token_out, float* d_logits);
+/* Sequence mode: d_seq int32 [seq_cap] holds the prompt in [0, n_prompt).
+ * The step at device-side position p embeds d_seq[p] and, when p + 1 >=
+ * n_prompt, stores its greedy token at d_seq[p + 1] (if p + 1 < seq_cap).
+ * After m1moe_dec_reset, n_prompt + n_gen calls (or replays of one graph
+ * captured around one call) run the reference's prefill-then-generate loop
+ * (Sources/bench/main.swift:136-163): the prompt forwarded token by token,
+ * then each generated token fed back, d_seq[n_prompt .. n_prompt + n_gen]
+ * receiving the n_gen + 1 greedy tokens.  p >= seq_cap sets the device error
+ * flag (as a token outside the vocabulary). */
+int32_t m1moe_dec_step_seq(m1moe_dec_t dec, int32_t* d_seq, int32_t n_prompt,
+                           int32_t seq_cap, float* d_logits);
 /* The current position (waits for the context stream). */
 int32_t m1moe_dec_position(m1moe_dec_t dec, int32_t* pos);
 

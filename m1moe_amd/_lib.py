@@ -120,6 +120,7 @@ _PROTOTYPES = [
     ("m1moe_dec_upload", c_int32, [c_void_p, c_int32, c_int32, POINTER(c_uint16), c_uint64]),
     ("m1moe_dec_reset", c_int32, [c_void_p]),
     ("m1moe_dec_step", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("m1moe_dec_step_seq", c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     ("m1moe_dec_position", c_int32, [c_void_p, POINTER(c_int32)]),
     ("m1moe_synth_normal_bf16", c_int32,
      [c_uint64, c_uint64, c_uint64, c_float, c_int32, c_void_p]),

@@ -216,7 +216,7 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     void* owned[] = {ctx->arena,   ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
                      ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
-                     ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part};
+                     ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part, ctx->attn_cnt};
     for (void* p : owned)
         if (p) (void)hipFree(p);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -581,6 +581,27 @@ int32_t m1moe_moe_decode(m1moe_ctx_t ctx, int32_t layer, const void* d_x, int32_
     a.user_w = d_topk_w;
     return launched(m1moe::launch_moe_decode(a, ctx->stream), "moe_decode");
 }
+
+}  // extern "C"
+
+namespace m1moe {
+int32_t moe_decode_normed(m1moe_ctx_t ctx, int32_t layer, const float* d_x, const float* d_ssq,
+                          int32_t n_ssq, const uint16_t* d_norm_w, float eps,
+                          const float* d_residual, float* d_out) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if ((rc = require_loaded(ctx, layer, true))) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    m1moe::FusedArgs a = fused_args(ctx, layer, d_x, M1MOE_F32, d_residual, d_out);
+    a.x_ssq = d_ssq;
+    a.n_ssq = n_ssq;
+    a.x_norm_w = d_norm_w;
+    a.x_eps = eps;
+    return launched(m1moe::launch_moe_decode(a, ctx->stream), "moe_decode (normed input)");
+}
+}  // namespace m1moe
+
+extern "C" {
 
 int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_x,
                           int32_t x_dtype, const float* d_residual, float* d_out,

@@ -59,6 +59,7 @@ struct m1moe_ctx {
     // attention scratch of m1moe_attention_decode, grown on demand
     float* attn_part = nullptr;
     uint64_t attn_part_floats = 0;
+    uint32_t* attn_cnt = nullptr;    // [kAttnCounters], zero between launches
     std::set<void*> allocs;
 };
 
@@ -113,6 +114,12 @@ inline int32_t check_dtype(int32_t dt) {
         return fail(M1MOE_ERR_INVALID, "x_dtype %d is not M1MOE_F32 or M1MOE_BF16", dt);
     return M1MOE_OK;
 }
+
+// The decode entry with the post-attention RMSNorm applied to the f32 input
+// in the kernel (sum of squares given as n_ssq partials); for the decoder.
+int32_t moe_decode_normed(m1moe_ctx_t ctx, int32_t layer, const float* d_x, const float* d_ssq,
+                          int32_t n_ssq, const uint16_t* d_norm_w, float eps,
+                          const float* d_residual, float* d_out);
 
 inline int32_t launched(int rc, const char* what) {
     if (rc != (int)hipSuccess)

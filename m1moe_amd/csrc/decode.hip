@@ -195,8 +195,34 @@ __device__ __forceinline__ float chunk_term(const uint4& w, uint32_t sw, uint32_
 // partials are added in wave order.  Published to every replica as
 // (tag << 32 | bits).  Every thread of the workgroup calls it; s_tag must be
 // visible (a barrier after it was written) before the call.
+// rsqrt(sum(x^2) / h + eps) of a normalised input, from its n_ssq partial
+// sums added in the same order in every wave (lane l takes partials l,
+// l + 64, ..., then the wave sum), so every wave of every role gets the same
+// value.
+__device__ __forceinline__ float input_rms(const FusedArgs& a, int lane) {
+    float s = 0.f;
+    for (int i0 = 0; i0 < a.n_ssq; i0 += 256) {
+        float t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = i0 + lane + 64 * j;
+            t[j] = i < a.n_ssq ? a.x_ssq[i] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s += t[j];
+    }
+    return rsqrtf(wave_sum(s) / (float)a.h + a.x_eps);
+}
+
+// x[d .. d+7] *= rms * w[d .. d+7] (the norm of Shaders.metal:121-134)
+__device__ __forceinline__ void norm8(const FusedArgs& a, int d, float rms, float* xv) {
+    const uint4 w = *reinterpret_cast<const uint4*>(a.x_norm_w + d);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = xv[i] * rms * bf16x8_at(w, i);
+}
+
 __device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, uint32_t* s_tag,
-                              uint32_t tag_reg, double* s_lp) {
+                              uint32_t tag_reg, double* s_lp, float rms) {
     if (wave < 4) {
         const uint16_t* wr = a.router + (size_t)e * a.h;
         const int C = a.h / 32;
@@ -215,6 +241,7 @@ __device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, uin
                 const float4 x1 = *reinterpret_cast<const float4*>(xr + 4);
                 xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
                 xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
+                if (a.x_norm_w) norm8(a, d, rms, xv);
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv, i) * (double)xv[i];
@@ -774,8 +801,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
     // load overlaps the router row loads of the producers
     const uint32_t tag_reg = threadIdx.x == 0 ? ld_u32(a.seen + wg) + 1u : 0u;
     if (!a.given_idx && wg < a.E) {
+        const float rms = a.x_norm_w ? input_rms(a, lane) : 1.f;
         for (int e = wg; e < a.E; e += gridDim.x)
-            produce_logit(a, e, wave, lane, &s_tag, tag_reg, s_lp);
+            produce_logit(a, e, wave, lane, &s_tag, tag_reg, s_lp, rms);
     } else {
         if (threadIdx.x == 0) s_tag = tag_reg;
         __syncthreads();
@@ -792,6 +820,15 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
         for (int j = 0; j < CPL; ++j) {
             const int c = m.c0 + 64 * j;
             load_chunk(a.x, a.x_bf16, min(c, a.Cg - 1), m.ok && c < a.Cg, v[j]);
+        }
+        if (a.x_norm_w) {
+            const float rms = input_rms(a, lane);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = min(m.c0 + 64 * j, a.Cg - 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) norm8(a, 32 * c + 8 * q, rms, &v[j][8 * q]);
+            }
         }
         inv = lane_scale_prep<CPL>(v, xc);
     }

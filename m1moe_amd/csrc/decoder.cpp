@@ -21,7 +21,14 @@ namespace {
 
 int32_t check_f32_vec(const void* p, const char* what) { return check_dev_ptr(p, what, false); }
 
+constexpr int kAttnCounters = 1024;  // >= num_heads (num_heads * 64 <= 65536)
+
 int32_t ensure_attn_scratch(m1moe_ctx_t ctx, uint64_t floats) {
+    if (!ctx->attn_cnt) {
+        int32_t rc = device_alloc((void**)&ctx->attn_cnt, kAttnCounters * 4, "attention counters");
+        if (rc) return rc;
+        HIP_TRY(hipMemset(ctx->attn_cnt, 0, kAttnCounters * 4));
+    }
     if (floats <= ctx->attn_part_floats) return M1MOE_OK;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     if (ctx->attn_part) HIP_TRY(hipFree(ctx->attn_part));
@@ -59,9 +66,13 @@ struct m1moe_dec {
     float *kcache = nullptr, *vcache = nullptr;  // [L][max_seq][kvd]
     int32_t* pos = nullptr;
     // step scratch
-    float *res = nullptr, *res2 = nullptr, *xn = nullptr, *hmid = nullptr;
+    float *res = nullptr, *res2 = nullptr;
     float *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float *logits = nullptr, *part = nullptr;
+    uint32_t* cnt = nullptr;   // [2 + num_heads]: (unused), lm_head, attention groups
+    float* ssq = nullptr;      // o_proj's per-workgroup sums of squares
+    float* am_val = nullptr;   // lm_head's per-workgroup best logit
+    int32_t* am_idx = nullptr;
     std::vector<void*> allocs;
 };
 
@@ -110,32 +121,6 @@ int32_t dec_alloc(m1moe_dec* d, void** p, uint64_t bytes, const char* what) {
     int32_t rc = device_alloc(p, bytes, what);
     if (rc == M1MOE_OK) d->allocs.push_back(*p);
     return rc;
-}
-
-DenseStepArgs step_args(const m1moe_dec* d, const int32_t* token) {
-    DenseStepArgs a{};
-    a.token = token;
-    a.pos = d->pos;
-    a.embed = d->embed;
-    a.x_out = d->res;
-    a.q = d->q;
-    a.k = d->k;
-    a.v = d->v;
-    a.q_norm = d->q_norm;
-    a.k_norm = d->k_norm;
-    a.kcache = d->kcache;
-    a.vcache = d->vcache;
-    a.err = d->moe->err;
-    a.vocab = d->sh.vocab;
-    a.h = d->h;
-    a.num_heads = d->sh.num_heads;
-    a.num_kv_heads = d->sh.num_kv_heads;
-    a.head_dim = d->sh.head_dim;
-    a.max_seq = d->sh.max_seq;
-    a.qk_norm = d->sh.qk_norm;
-    a.rope_theta = d->sh.rope_theta;
-    a.eps = d->sh.rms_eps;
-    return a;
 }
 
 MvArgs mv_one(const uint16_t* w, const float* x, const float* res, float* y, int32_t rows, int32_t cols) {
@@ -192,20 +177,23 @@ int32_t m1moe_attention_decode(m1moe_ctx_t ctx, const float* d_q, const float* d
     if ((rc = set_device(ctx))) return rc;
     if ((rc = ensure_attn_scratch(ctx, attention_partial_floats(num_heads, head_dim, seq_len)))) return rc;
     AttnArgs a{};
+    a.fused = 0;
     a.q = d_q;
-    a.kcache = d_kcache;
-    a.vcache = d_vcache;
+    a.kcache = const_cast<float*>(d_kcache);  // read only when fused = 0
+    a.vcache = const_cast<float*>(d_vcache);
     a.out = d_out;
     a.partial = ctx->attn_part;
-    a.seq_ptr = nullptr;
+    a.counters = ctx->attn_cnt;
+    a.err = ctx->err;
     a.seq_len = seq_len;
     a.max_seq = seq_len;
     a.num_heads = num_heads;
     a.num_kv_heads = num_kv_heads;
     a.hpkv = num_heads / num_kv_heads;
     a.head_dim = head_dim;
+    a.qh = attention_qh(a.hpkv);
     a.scale = 1.0f / sqrtf((float)head_dim);
-    return launched(launch_attention(a, seq_len, ctx->stream), "attention");
+    return launched(launch_attention(a, ctx->stream), "attention");
 }
 
 int32_t m1moe_argmax(m1moe_ctx_t ctx, const float* d_x, int32_t n, int32_t* d_idx) {
@@ -214,7 +202,7 @@ int32_t m1moe_argmax(m1moe_ctx_t ctx, const float* d_x, int32_t n, int32_t* d_id
     if (!d_idx) return fail(M1MOE_ERR_INVALID, "d_idx is null");
     if (n <= 0) return fail(M1MOE_ERR_INVALID, "n %d must be positive", n);
     if ((rc = set_device(ctx))) return rc;
-    return launched(launch_argmax(d_x, n, d_idx, nullptr, 0, ctx->stream), "argmax");
+    return launched(launch_argmax(d_x, n, d_idx, ctx->stream), "argmax");
 }
 
 // ---- the decoder ---------------------------------------------------------------------
@@ -240,6 +228,9 @@ int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* s, m1moe_dec_t*
         return fail(M1MOE_ERR_INVALID, "rope_theta must be > 0 and rms_eps >= 0");
     if (s->num_heads * s->head_dim > 65536)
         return fail(M1MOE_ERR_INVALID, "num_heads * head_dim exceeds 65536");
+    if (moe->g.h > kMvStageMax)
+        return fail(M1MOE_ERR_INVALID, "hidden %d exceeds the decoder's %d (normalised inputs are "
+                    "staged in LDS)", moe->g.h, kMvStageMax);
     if ((rc = set_device(moe))) return rc;
     m1moe_dec* d = new (std::nothrow) m1moe_dec;
     if (!d) return fail(M1MOE_ERR_OOM, "out of host memory");
@@ -270,20 +261,23 @@ int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* s, m1moe_dec_t*
         (rc = dec_alloc(d, (void**)&d->pos, 16, "position")) ||
         (rc = dec_alloc(d, (void**)&d->res, h * 4, "residual")) ||
         (rc = dec_alloc(d, (void**)&d->res2, h * 4, "residual 2")) ||
-        (rc = dec_alloc(d, (void**)&d->xn, h * 4, "normed input")) ||
-        (rc = dec_alloc(d, (void**)&d->hmid, h * 4, "MoE input")) ||
         (rc = dec_alloc(d, (void**)&d->q, qd * 4, "q")) ||
         (rc = dec_alloc(d, (void**)&d->k, kvd * 4, "k")) ||
         (rc = dec_alloc(d, (void**)&d->v, kvd * 4, "v")) ||
         (rc = dec_alloc(d, (void**)&d->attn, qd * 4, "attention output")) ||
         (rc = dec_alloc(d, (void**)&d->logits, V * 4, "logits")) ||
-        (rc = dec_alloc(d, (void**)&d->part, part * 4, "attention scratch"))) {
+        (rc = dec_alloc(d, (void**)&d->part, part * 4, "attention scratch")) ||
+        (rc = dec_alloc(d, (void**)&d->cnt, (2 + (uint64_t)s->num_heads) * 4, "counters")) ||
+        (rc = dec_alloc(d, (void**)&d->ssq, (uint64_t)matvec_workgroups(d->h) * 4, "o_proj sums")) ||
+        (rc = dec_alloc(d, (void**)&d->am_val, (uint64_t)matvec_workgroups(s->vocab) * 4, "argmax scratch")) ||
+        (rc = dec_alloc(d, (void**)&d->am_idx, (uint64_t)matvec_workgroups(s->vocab) * 4, "argmax scratch"))) {
         m1moe_dec_destroy(d);
         return rc;
     }
-    if (hipMemset(d->pos, 0, 16) != hipSuccess) {
+    if (hipMemset(d->pos, 0, 16) != hipSuccess ||
+        hipMemset(d->cnt, 0, (2 + (size_t)s->num_heads) * 4) != hipSuccess) {
         m1moe_dec_destroy(d);
-        return fail(M1MOE_ERR_HIP, "hipMemset(position) failed");
+        return fail(M1MOE_ERR_HIP, "hipMemset(position / counters) failed");
     }
     *out = d;
     return M1MOE_OK;
@@ -325,13 +319,16 @@ int32_t m1moe_dec_position(m1moe_dec_t dec, int32_t* pos) {
     return M1MOE_OK;
 }
 
-int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in, int32_t* d_token_out,
-                       float* d_logits) {
+}  // extern "C"
+
+namespace {
+
+// One step; seq_cap == 0: token from *tok_in, greedy token to *tok_out;
+// seq_cap > 0: sequence mode over tok_out[0 .. seq_cap) (tok_in == tok_out).
+int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32_t n_prompt,
+                 int32_t seq_cap, float* d_logits) {
     int32_t rc;
     if (!dec) return fail(M1MOE_ERR_INVALID, "null decoder");
-    if (!d_token_in || reinterpret_cast<uintptr_t>(d_token_in) % 4 || !d_token_out ||
-        reinterpret_cast<uintptr_t>(d_token_out) % 4)
-        return fail(M1MOE_ERR_INVALID, "d_token_in / d_token_out must be 4-byte aligned device pointers");
     if ((rc = check_dev_ptr(d_logits, "d_logits", true))) return rc;
     const bool needs_qk = dec->sh.qk_norm != 0;
     for (int w = 0; w < kNumW; ++w) {
@@ -346,60 +343,104 @@ int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in, int32_t* d_to
             return fail(M1MOE_ERR_INVALID, "MoE layer %d was not uploaded", l);
     if ((rc = set_device(ctx))) return rc;
     void* st = ctx->stream;
-    const int32_t h = dec->h, qd = dec->qd, kvd = dec->kvd, V = dec->sh.vocab;
+    const int32_t h = dec->h, qd = dec->qd, kvd = dec->kvd, V = dec->sh.vocab, hd = dec->sh.head_dim;
     const float eps = dec->sh.rms_eps;
-    const DenseStepArgs a = step_args(dec, d_token_in);
-    if ((rc = launched(launch_embed(a, st), "embed"))) return rc;
+    const bool qk = dec->sh.qk_norm != 0;
     AttnArgs at{};
+    at.fused = 1;
     at.q = dec->q;
+    at.k_new = dec->k;
+    at.v_new = dec->v;
     at.out = dec->attn;
     at.partial = dec->part;
-    at.seq_ptr = dec->pos;
+    at.counters = dec->cnt + 2;
+    at.pos = dec->pos;
+    at.err = ctx->err;
     at.max_seq = dec->sh.max_seq;
     at.num_heads = dec->sh.num_heads;
     at.num_kv_heads = dec->sh.num_kv_heads;
     at.hpkv = dec->sh.num_heads / dec->sh.num_kv_heads;
-    at.head_dim = dec->sh.head_dim;
-    at.scale = 1.0f / sqrtf((float)dec->sh.head_dim);
+    at.head_dim = hd;
+    at.qh = attention_qh(at.hpkv);
+    at.scale = 1.0f / sqrtf((float)hd);
+    at.rope_theta = dec->sh.rope_theta;
+    at.eps = eps;
     const uint64_t cache_layer = (uint64_t)dec->sh.max_seq * kvd;
     for (int l = 0; l < dec->L; ++l) {
-        // input norm, q/k/v in one launch (InferenceEngine.swift:177-192)
-        if ((rc = launched(launch_rmsnorm(dec->res, dec->in_norm + (size_t)l * h, dec->xn, h, eps, st),
-                           "input norm")))
-            return rc;
+        // input RMSNorm and q/k/v in one launch (InferenceEngine.swift:177-192); layer 0
+        // takes its input from the embedding table at the step's token (:129-131)
         MvArgs m{};
         m.seg[0] = MvSeg{dec->wq + (size_t)l * qd * h, dec->q, nullptr, qd};
         m.seg[1] = MvSeg{dec->wk + (size_t)l * kvd * h, dec->k, nullptr, kvd};
         m.seg[2] = MvSeg{dec->wv + (size_t)l * kvd * h, dec->v, nullptr, kvd};
-        m.x = dec->xn;
         m.rows = qd + 2 * kvd;
         m.cols = h;
+        m.norm_w = dec->in_norm + (size_t)l * h;
+        m.eps = eps;
+        m.err = ctx->err;
+        if (l == 0) {
+            m.embed = dec->embed;
+            m.token = tok_in;
+            m.seq_cap = seq_cap;
+            m.pos = dec->pos;
+            m.vocab = V;
+            m.x_copy = dec->res;
+        } else {
+            m.x = dec->res;
+        }
         if ((rc = launched(launch_matvec_bf16(m, st), "qkv"))) return rc;
-        // q/k norms, RoPE, KV store (:194-220), attention (:226)
-        if ((rc = launched(launch_qk_rope_kv(a, l, st), "qk norm / rope / kv store"))) return rc;
+        // q/k norms, RoPE, KV store (:194-220) and attention (:226)
+        at.q_norm = qk ? dec->q_norm + (size_t)l * hd : nullptr;
+        at.k_norm = qk ? dec->k_norm + (size_t)l * hd : nullptr;
         at.kcache = dec->kcache + l * cache_layer;
         at.vcache = dec->vcache + l * cache_layer;
-        if ((rc = launched(launch_attention(at, dec->sh.max_seq, st), "attention"))) return rc;
-        // o_proj + residual, post-attention norm (:227-236)
-        if ((rc = launched(launch_matvec_bf16(
-                               mv_one(dec->wo + (size_t)l * h * qd, dec->attn, dec->res, dec->res2, h, qd), st),
-                           "o_proj")))
-            return rc;
-        if ((rc = launched(launch_rmsnorm(dec->res2, dec->post_norm + (size_t)l * h, dec->hmid, h, eps, st),
-                           "post-attention norm")))
-            return rc;
-        // the MoE block with the residual, its output the next residual (:240-266)
-        if ((rc = m1moe_moe_decode(ctx, l, dec->hmid, M1MOE_F32, dec->res2, dec->res, nullptr, nullptr)))
+        if ((rc = launched(launch_attention(at, st), "attention"))) return rc;
+        // o_proj + residual (:227-233), with the sums of squares of its rows
+        MvArgs o = mv_one(dec->wo + (size_t)l * h * qd, dec->attn, dec->res, dec->res2, h, qd);
+        o.ssq_out = dec->ssq;
+        if ((rc = launched(launch_matvec_bf16(o, st), "o_proj"))) return rc;
+        // the post-attention RMSNorm (:234-236) applied by the MoE kernel to its
+        // input, the MoE block with the residual, its output the next residual
+        // (:240-266)
+        if ((rc = moe_decode_normed(ctx, l, dec->res2, dec->ssq, matvec_workgroups(h),
+                                    dec->post_norm + (size_t)l * h, eps, dec->res2, dec->res)))
             return rc;
     }
-    // final norm, lm_head, greedy token, next position (:138-155)
-    float* logits = d_logits ? d_logits : dec->logits;
-    if ((rc = launched(launch_rmsnorm(dec->res, dec->final_norm, dec->xn, h, eps, st), "final norm")))
-        return rc;
-    if ((rc = launched(launch_matvec_bf16(mv_one(dec->lm_head, dec->xn, nullptr, logits, V, h), st),
-                       "lm_head")))
-        return rc;
-    return launched(launch_argmax(logits, V, d_token_out, dec->pos, dec->sh.max_seq, st), "argmax");
+    // final RMSNorm, lm_head, greedy token, next position (:138-155)
+    MvArgs f = mv_one(dec->lm_head, dec->res, nullptr, d_logits ? d_logits : dec->logits, V, h);
+    f.norm_w = dec->final_norm;
+    f.eps = eps;
+    f.counter = dec->cnt + 1;
+    f.am_val = dec->am_val;
+    f.am_idx = dec->am_idx;
+    f.tok_out = tok_out;
+    f.n_prompt = n_prompt;
+    f.seq_cap = seq_cap;
+    f.pos = dec->pos;
+    f.max_seq = dec->sh.max_seq;
+    f.err = ctx->err;
+    return launched(launch_matvec_bf16(f, st), "lm_head");
+}
+
+bool aligned_i32(const void* p) { return p && reinterpret_cast<uintptr_t>(p) % 4 == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in, int32_t* d_token_out,
+                       float* d_logits) {
+    if (!aligned_i32(d_token_in) || !aligned_i32(d_token_out))
+        return fail(M1MOE_ERR_INVALID, "d_token_in / d_token_out must be 4-byte aligned device pointers");
+    return dec_step(dec, d_token_in, d_token_out, 0, 0, d_logits);
+}
+
+int32_t m1moe_dec_step_seq(m1moe_dec_t dec, int32_t* d_seq, int32_t n_prompt, int32_t seq_cap,
+                           float* d_logits) {
+    if (!aligned_i32(d_seq)) return fail(M1MOE_ERR_INVALID, "d_seq must be a 4-byte aligned device pointer");
+    if (seq_cap <= 0 || n_prompt < 1 || n_prompt > seq_cap)
+        return fail(M1MOE_ERR_INVALID, "need 1 <= n_prompt (%d) <= seq_cap (%d)", n_prompt, seq_cap);
+    return dec_step(dec, d_seq, d_seq, n_prompt, seq_cap, d_logits);
 }
 
 }  // extern "C"

@@ -2,24 +2,32 @@
 //
 // The reference runs these on Metal one threadgroup per row or per dot
 // product (Shaders.metal:96-358) and the q/k norms, RoPE and the KV store on
-// the CPU between syncs (InferenceEngine.swift:196-228, 521-548).  Here:
+// the CPU between syncs (InferenceEngine.swift:194-228, 521-548).  Here a
+// layer is four launches, the MoE block's included:
 //
-//   embed          token row of the bf16 embedding -> f32
-//                  (InferenceEngine.swift:482-488)
-//   rmsnorm        one workgroup: sum of squares, then x * rsqrt(ss/n + eps) * w
-//   matvec_bf16    y = W x (+ residual): a wave takes kMvRows rows, its lanes
-//                  128-bit loads across the columns; up to three weight
-//                  segments per launch (q, k, v share the input)
-//   qk_rope_kv     one workgroup per q or k head: optional per-head RMSNorm,
-//                  RoPE on (d, d + hd/2) pairs, k and v stored at the
-//                  device-side position
-//   attn_partial   one workgroup per (head, 256 positions): scores, their
-//   attn_combine   max and exp-sum, the weighted V sum; then the chunks are
-//                  merged per head (the softmax of the reference, computed in
-//                  pieces)
-//   argmax         one workgroup; ties to the lower index, NaN never wins
-//                  except at index 0 (InferenceEngine.swift:550-555);
-//                  advances the device-side position
+//   matvec_kernel  y = W x over up to three weight segments (q, k, v share
+//                  the input).  The input is staged in LDS once per
+//                  workgroup, RMS-normalised there (the layer's input norm,
+//                  the final norm) or taken from the embedding table at the
+//                  step's token.  o_proj also stores per-workgroup sums of
+//                  squares of its output, from which the MoE kernel applies
+//                  the post-attention RMSNorm to its input; lm_head's last
+//                  workgroup to finish takes the greedy argmax (and advances
+//                  the device-side position).
+//   attn_kernel    one workgroup per (kv head, 64 positions): the per-head
+//                  q/k RMSNorm and RoPE of the current token, its K/V row
+//                  stored, scores, a chunk softmax and the weighted V sum;
+//                  the last workgroup of each kv head merges the chunks (the
+//                  reference's softmax, computed in pieces)
+//   rmsnorm_kernel, argmax_kernel   the standalone building blocks
+//
+// Cross-workgroup results (attention partials, per-workgroup maxima) are
+// written with agent-scope (coherent) stores; every thread waits
+// for its stores to complete, then after a barrier thread 0 counts the
+// workgroup in with a relaxed agent-scope add (a release fence instead would
+// write back the whole L2 once per workgroup).  The last workgroup reads
+// the results with coherent loads, issued in batches, and puts the counter
+// back to 0, so a captured graph can replay the kernels.
 #include <hip/hip_runtime.h>
 
 #include "device.hpp"
@@ -28,11 +36,8 @@
 namespace m1moe {
 namespace {
 
-constexpr int kMvRows = 2;        // matvec rows per wave
-constexpr int kAttnChunk = 256;   // positions per attention workgroup
-
-// Sum over a workgroup of `nw` waves; every thread gets the total (waves
-// added in order).
+// Sum over a workgroup of `nw` waves; every thread gets the result (waves
+// combined in order).
 __device__ __forceinline__ float block_sum(float v, float* s_red, int nw) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     v = wave_sum(v);
@@ -43,6 +48,7 @@ __device__ __forceinline__ float block_sum(float v, float* s_red, int nw) {
     __syncthreads();
     return t;
 }
+
 __device__ __forceinline__ float block_max(float v, float* s_red, int nw) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     v = wave_max(v);
@@ -54,20 +60,44 @@ __device__ __forceinline__ float block_max(float v, float* s_red, int nw) {
     return t;
 }
 
-// ---- embedding ----------------------------------------------------------------------
-
-__global__ __launch_bounds__(256) void embed_kernel(DenseStepArgs a) {
-    int t = *a.token;
-    if (t < 0 || t >= a.vocab) {
-        if (blockIdx.x == 0 && threadIdx.x == 0) flag_error(a.err, 16u);
-        t = 0;
-    }
-    const uint16_t* row = a.embed + (size_t)t * a.h;
-    for (int d = blockIdx.x * 256 + threadIdx.x; d < a.h; d += gridDim.x * 256)
-        a.x_out[d] = bf16_to_f32(row[d]);
+__device__ __forceinline__ void st_coh(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_coh(const int32_t* p) {
+    return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---- RMSNorm ------------------------------------------------------------------------
+// True in the workgroup that finishes last of `total`.  Every thread's
+// coherent stores have completed before the barrier, so they are visible to
+// coherent loads once the counter shows the workgroup.
+__device__ __forceinline__ bool last_workgroup(uint32_t* counter, uint32_t total, int* s_flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = old == total - 1;
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}
+__device__ __forceinline__ void reset_counter(uint32_t* c) {
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// (value, index) pairs: the larger value wins, ties to the lower index; NaN
+// never wins.
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// ---- RMSNorm (standalone) ------------------------------------------------------------
 
 // Shaders.metal:96-134: the sum of squares in f32, rms = rsqrt(ss / n + eps),
 // out = x * rms * w.
@@ -84,207 +114,507 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* x, const uin
     for (int i = threadIdx.x; i < n; i += 1024) out[i] = x[i] * rms * bf16_to_f32(w[i]);
 }
 
-// ---- bf16 matvec --------------------------------------------------------------------
+// ---- bf16 matvec ----------------------------------------------------------------------
 
-// Row `row` of the concatenated segments: its weight row, output and residual.
-__device__ __forceinline__ const MvSeg& mv_seg(const MvArgs& a, int row, int& local) {
-    if (row < a.seg[0].rows) {
-        local = row;
-        return a.seg[0];
+// Row `row` of the concatenated segments: its weight row, output and
+// residual slots.  Fields are picked with constant indices (a reference into
+// the argument array with a computed index would copy it to scratch).
+struct RowRef {
+    const uint16_t* w;
+    float* y;
+    const float* res;
+};
+__device__ __forceinline__ RowRef mv_row(const MvArgs& a, int row) {
+    const int e0 = a.seg[0].rows, e1 = e0 + a.seg[1].rows;
+    RowRef r;
+    int loc;
+    if (row < e0) {
+        loc = row;
+        r.w = a.seg[0].w, r.y = a.seg[0].y, r.res = a.seg[0].res;
+    } else if (row < e1) {
+        loc = row - e0;
+        r.w = a.seg[1].w, r.y = a.seg[1].y, r.res = a.seg[1].res;
+    } else {
+        loc = row - e1;
+        r.w = a.seg[2].w, r.y = a.seg[2].y, r.res = a.seg[2].res;
     }
-    if (row < a.seg[0].rows + a.seg[1].rows) {
-        local = row - a.seg[0].rows;
-        return a.seg[1];
-    }
-    local = row - a.seg[0].rows - a.seg[1].rows;
-    return a.seg[2];
+    r.w += (size_t)loc * a.cols;
+    r.y += loc;
+    if (r.res) r.res += loc;
+    return r;
 }
 
-// Lane l takes columns 8l .. 8l+7 of each 512-column block; four blocks of
-// loads are in flight together.
-__global__ __launch_bounds__(256) void matvec_bf16_kernel(MvArgs a) {
+// Stages the input in LDS: x, or the embedding row of the step's token
+// (InferenceEngine.swift:482-488), then (norm_w) RMS-normalised
+// (Shaders.metal:96-134).  Workgroup 0 stores the un-normalised input to
+// x_copy.
+__device__ void mv_stage(const MvArgs& a, float* s_x, float* s_red) {
+    const int n4 = a.cols >> 2;
+    float ss = 0.f;
+    if (a.embed) {
+        int t;
+        if (a.seq_cap > 0) {
+            const int p = *a.pos;
+            t = p < a.seq_cap ? a.token[p] : -1;
+        } else {
+            t = *a.token;
+        }
+        if (t < 0 || t >= a.vocab) {
+            if (blockIdx.x == 0 && threadIdx.x == 0) flag_error(a.err, 16u);
+            t = 0;
+        }
+        const uint2* row = reinterpret_cast<const uint2*>(a.embed + (size_t)t * a.cols);
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            const uint2 b = row[i];
+            const float4 v = {bf16_to_f32(b.x & 0xFFFFu), bf16_to_f32(b.x >> 16),
+                              bf16_to_f32(b.y & 0xFFFFu), bf16_to_f32(b.y >> 16)};
+            reinterpret_cast<float4*>(s_x)[i] = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    } else {
+        const float4* x4 = reinterpret_cast<const float4*>(a.x);
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            const float4 v = x4[i];
+            reinterpret_cast<float4*>(s_x)[i] = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    }
+    if (a.x_copy && blockIdx.x == 0) {
+        // each thread copies the elements it staged itself
+        for (int i = threadIdx.x; i < n4; i += 256)
+            reinterpret_cast<float4*>(a.x_copy)[i] = reinterpret_cast<const float4*>(s_x)[i];
+    }
+    if (a.norm_w) {
+        const float tot = block_sum(ss, s_red, 4);
+        const float rms = rsqrtf(tot / (float)a.cols + a.eps);
+        const uint2* w = reinterpret_cast<const uint2*>(a.norm_w);
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            const uint2 b = w[i];
+            float4 v = reinterpret_cast<float4*>(s_x)[i];
+            v.x = v.x * rms * bf16_to_f32(b.x & 0xFFFFu);
+            v.y = v.y * rms * bf16_to_f32(b.x >> 16);
+            v.z = v.z * rms * bf16_to_f32(b.y & 0xFFFFu);
+            v.w = v.w * rms * bf16_to_f32(b.y >> 16);
+            reinterpret_cast<float4*>(s_x)[i] = v;
+        }
+    }
+    __syncthreads();
+}
+
+// Workgroup = 4 waves x RPW rows.  Lane l takes columns 8l .. 8l+7 of each
+// 512-column block; U blocks of every row are loaded per group, the next
+// group's loads issued before the current one is used.  The first group is
+// in flight while the input is staged.
+template <int RPW, bool STAGE>
+__global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
+    constexpr int U = 8 / RPW;
+    extern __shared__ __attribute__((aligned(16))) float s_x[];
+    __shared__ float s_red[4];
+    __shared__ float s_bv[4];
+    __shared__ int s_bi[4];
+    __shared__ int s_flag;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + wave) * kMvRows;
-    if (r0 >= a.rows) return;
-    const uint16_t* wr[kMvRows];
-    int loc[kMvRows];
+    const int r0 = (blockIdx.x * 4 + wave) * RPW;
+    const uint16_t* wr[RPW];
 #pragma unroll
-    for (int i = 0; i < kMvRows; ++i) {
-        const int row = min(r0 + i, a.rows - 1);
-        const MvSeg& sg = mv_seg(a, row, loc[i]);
-        wr[i] = sg.w + (size_t)loc[i] * a.cols;
-    }
-    float acc[kMvRows];
-#pragma unroll
-    for (int i = 0; i < kMvRows; ++i) acc[i] = 0.f;
-    constexpr int U = 4;
-    for (int c0 = 0; c0 < a.cols; c0 += 512 * U) {
-        uint4 wv[U][kMvRows];
-        float4 x0[U], x1[U];
+    for (int i = 0; i < RPW; ++i) wr[i] = mv_row(a, min(r0 + i, a.rows - 1)).w;
+    const int ngroups = (a.cols + 512 * U - 1) / (512 * U);
+    uint4 cur[U][RPW], nxt[U][RPW];
+    auto load = [&](int gi, uint4 (&dst)[U][RPW]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int c = min(c0 + 512 * u + 8 * lane, a.cols - 8);
+            const int c = min(gi * 512 * U + 512 * u + 8 * lane, a.cols - 8);
 #pragma unroll
-            for (int i = 0; i < kMvRows; ++i) wv[u][i] = *reinterpret_cast<const uint4*>(wr[i] + c);
-            x0[u] = *reinterpret_cast<const float4*>(a.x + c);
-            x1[u] = *reinterpret_cast<const float4*>(a.x + c + 4);
+            for (int i = 0; i < RPW; ++i) dst[u][i] = *reinterpret_cast<const uint4*>(wr[i] + c);
         }
+    };
+    load(0, cur);
+    if (STAGE) mv_stage(a, s_x, s_red);
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
+    for (int gi = 0; gi < ngroups; ++gi) {
+        if (gi + 1 < ngroups) load(gi + 1, nxt);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (c0 + 512 * u + 8 * lane >= a.cols) continue;
-            const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w, x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+            const int c = gi * 512 * U + 512 * u + 8 * lane;
+            if (c >= a.cols) continue;
+            float4 x0, x1;
+            if (STAGE) {
+                x0 = *reinterpret_cast<const float4*>(s_x + c);
+                x1 = *reinterpret_cast<const float4*>(s_x + c + 4);
+            } else {
+                x0 = *reinterpret_cast<const float4*>(a.x + c);
+                x1 = *reinterpret_cast<const float4*>(a.x + c + 4);
+            }
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int i = 0; i < kMvRows; ++i)
+            for (int i = 0; i < RPW; ++i)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[i] = fmaf(bf16x8_at(wv[u][i], k), xs[k], acc[i]);
+                for (int k = 0; k < 8; ++k) acc[i] = fmaf(bf16x8_at(cur[u][i], k), xs[k], acc[i]);
+        }
+        if (gi + 1 < ngroups) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int i = 0; i < RPW; ++i) cur[u][i] = nxt[u][i];
         }
     }
+    float bv = -INFINITY, ssq = 0.f;
+    int bi = 0x7fffffff;
 #pragma unroll
-    for (int i = 0; i < kMvRows; ++i) {
+    for (int i = 0; i < RPW; ++i) {
         const float v = wave_sum(acc[i]);
         const int row = r0 + i;
-        if (lane == 0 && row < a.rows) {
-            int l;
-            const MvSeg& sg = mv_seg(a, row, l);
-            sg.y[l] = sg.res ? sg.res[l] + v : v;
+        if (row < a.rows) {
+            const RowRef rr = mv_row(a, row);
+            const float y = rr.res ? *rr.res + v : v;
+            if (lane == 0) {
+                if (a.counter)
+                    st_coh(rr.y, y);  // the last workgroup reads it
+                else
+                    *rr.y = y;
+            }
+            ssq = fmaf(y, y, ssq);
+            if (am_better(y, row, bv, bi)) {
+                bv = y;
+                bi = row;
+            }
         }
     }
-}
-
-// ---- q/k norm, RoPE, KV store --------------------------------------------------------
-
-// Workgroup b < num_heads: q head b; else k head (and v head) b - num_heads.
-// Thread d < head_dim holds element d.
-__global__ __launch_bounds__(256) void qk_rope_kv_kernel(DenseStepArgs a, int layer) {
-    __shared__ float s_x[256];
-    __shared__ float s_red[4];
-    const int pos = *a.pos;
-    if (pos >= a.max_seq) {
-        if (blockIdx.x == 0 && threadIdx.x == 0) flag_error(a.err, 32u);
-        return;
+    if (a.ssq_out) {
+        if (lane == 0) s_red[wave] = ssq;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            a.ssq_out[blockIdx.x] = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
     }
-    const int hd = a.head_dim, half = hd / 2;
-    const bool is_q = (int)blockIdx.x < a.num_heads;
-    const int head = is_q ? blockIdx.x : blockIdx.x - a.num_heads;
-    float* vec = (is_q ? a.q : a.k) + (size_t)head * hd;
-    const int d = threadIdx.x;
-    float x = d < hd ? vec[d] : 0.f;
-    if (a.qk_norm) {
-        // InferenceEngine.swift:538-548: x *= rms * w[d], w of length head_dim
-        const float ss = block_sum(x * x, s_red, 4);
-        const float rms = 1.0f / sqrtf(ss / (float)hd + a.eps);
-        const uint16_t* w = (is_q ? a.q_norm : a.k_norm) + (size_t)layer * hd;
-        if (d < hd) x *= rms * bf16_to_f32(w[d]);
-    }
-    if (d < hd) s_x[d] = x;
-    __syncthreads();
-    // RoPE (InferenceEngine.swift:521-536): pairs (p, p + hd/2)
-    const size_t kvd = (size_t)a.num_kv_heads * hd;
-    if (d < half) {
-        const float freq = 1.0f / powf(a.rope_theta, (float)(2 * d) / (float)hd);
-        const float angle = (float)pos * freq;
-        const float c = cosf(angle), s = sinf(angle);
-        const float x0 = s_x[d], x1 = s_x[d + half];
-        const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
-        if (is_q) {
-            vec[d] = y0;
-            vec[d + half] = y1;
-        } else {
-            float* kc = a.kcache + (size_t)layer * a.max_seq * kvd + (size_t)pos * kvd + (size_t)head * hd;
-            kc[d] = y0;
-            kc[d + half] = y1;
+    if (!a.counter) return;
+
+    {
+        // this workgroup's best row, then the last workgroup's reduction
+        if (lane == 0) {
+            s_bv[wave] = bv;
+            s_bi[wave] = bi;
         }
-    }
-    if (!is_q && d < hd) {
-        float* vc = a.vcache + (size_t)layer * a.max_seq * kvd + (size_t)pos * kvd + (size_t)head * hd;
-        vc[d] = a.v[(size_t)head * hd + d];
-    }
-}
-
-// ---- attention ----------------------------------------------------------------------
-
-// Workgroup (head, chunk): positions chunk*256 .. +255 of the first seq.
-// Thread t scores position p0 + t; thread d < head_dim sums V column d.
-// Writes (max, exp-sum, acc[head_dim]) of the chunk, or max = -inf if empty.
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) float s_q[256];
-    __shared__ float s_e[kAttnChunk];
-    __shared__ float s_red[4];
-    const int head = blockIdx.x, chunk = blockIdx.y;
-    const int seq = a.seq_ptr ? min(*a.seq_ptr + 1, a.max_seq) : a.seq_len;
-    const int hd = a.head_dim;
-    const int p0 = chunk * kAttnChunk;
-    float* part = a.partial + ((size_t)head * gridDim.y + chunk) * (hd + 2);
-    if (p0 >= seq) {
+        __syncthreads();
         if (threadIdx.x == 0) {
-            part[0] = -INFINITY;
-            part[1] = 0.f;
+            for (int w = 1; w < 4; ++w)
+                if (am_better(s_bv[w], s_bi[w], bv, bi)) {
+                    bv = s_bv[w];
+                    bi = s_bi[w];
+                }
+            st_coh(a.am_val + blockIdx.x, bv);
+            st_coh(a.am_idx + blockIdx.x, bi);
+        }
+        if (!last_workgroup(a.counter, gridDim.x, &s_flag)) return;
+        bv = -INFINITY;
+        bi = 0x7fffffff;
+        const int nwg = (int)gridDim.x;
+        for (int w0 = 0; w0 < nwg; w0 += 256 * 16) {
+            float vv[16];
+            int ii[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int w = w0 + threadIdx.x + 256 * j;
+                vv[j] = w < nwg ? ld_coh(a.am_val + w) : -INFINITY;
+                ii[j] = w < nwg ? ld_coh(a.am_idx + w) : 0x7fffffff;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (am_better(vv[j], ii[j], bv, bi)) {
+                    bv = vv[j];
+                    bi = ii[j];
+                }
+        }
+        wave_argmax(bv, bi);
+        if (lane == 0) {
+            s_bv[wave] = bv;
+            s_bi[wave] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w = 1; w < 4; ++w)
+                if (am_better(s_bv[w], s_bi[w], bv, bi)) {
+                    bv = s_bv[w];
+                    bi = s_bi[w];
+                }
+            // the reference's scan starts from y[0] with a strict > (its
+            // sampleToken, InferenceEngine.swift:550-555): a NaN there is
+            // never replaced; all NaN also gives 0
+            const int n = a.seg[0].rows;
+            const int best = (bi < n && !__builtin_isnan(ld_coh(a.seg[0].y))) ? bi : 0;
+            const int p = *a.pos;
+            if (a.seq_cap > 0) {
+                if (p + 1 >= a.n_prompt && p + 1 < a.seq_cap) a.tok_out[p + 1] = best;
+            } else {
+                *a.tok_out = best;
+            }
+            if (p < a.max_seq) *a.pos = p + 1;
+            reset_counter(a.counter);
         }
         return;
     }
-    const int kvh = head / a.hpkv;
-    const size_t kvd = (size_t)a.num_kv_heads * hd;
-    if ((int)threadIdx.x < hd) s_q[threadIdx.x] = a.q[(size_t)head * hd + threadIdx.x];
-    __syncthreads();
-    const int p = p0 + threadIdx.x;
-    float s = -INFINITY;
-    if (p < seq) {
-        const float4* kp = reinterpret_cast<const float4*>(a.kcache + (size_t)p * kvd + (size_t)kvh * hd);
-        const float4* qp = reinterpret_cast<const float4*>(s_q);
-        float acc = 0.f;
-        for (int i = 0; i < hd / 4; ++i) {
-            const float4 k4 = kp[i], q4 = qp[i];
-            acc = fmaf(q4.x, k4.x, acc);
-            acc = fmaf(q4.y, k4.y, acc);
-            acc = fmaf(q4.z, k4.z, acc);
-            acc = fmaf(q4.w, k4.w, acc);
+}
+
+// ---- attention --------------------------------------------------------------------------
+
+// Workgroup (g, c): q heads g*QH .. g*QH+QH-1 (one kv head), positions
+// 64c .. 64c+63.  Lanes take 8 dims of one position each (HD/8 lanes per
+// position), so every K or V row is one coalesced read shared by the QH
+// heads.
+template <int HD, int QH>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+    constexpr int LP = HD / 8;                 // lanes per position
+    constexpr int PPI = 64 / LP;               // positions per wave and iteration
+    constexpr int PW = kAttnChunk / 4;         // positions per wave
+    constexpr int IT = PW / PPI;               // iterations
+    constexpr int HALF = HD / 2;
+    __shared__ __attribute__((aligned(16))) float s_q[QH][HD];
+    __shared__ __attribute__((aligned(16))) float s_kv[2][HD];
+    __shared__ float s_p[QH][kAttnChunk];
+    __shared__ __attribute__((aligned(16))) float s_acc[4][QH][HD];
+    __shared__ float s_m[QH], s_l[QH];
+    __shared__ float s_cf[kAttnMaxChunks];  // merge: chunk maxima, then weights
+    __shared__ int s_flag;
+
+    const int g = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h0 = g * QH, kvh = h0 / a.hpkv;
+    const size_t kvd = (size_t)a.num_kv_heads * HD;
+    int p = -1, seq;
+    if (a.fused) {
+        p = *a.pos;
+        if (p >= a.max_seq) {
+            if (g == 0 && c == 0 && tid == 0) flag_error(a.err, 32u);
+            seq = a.max_seq;
+        } else {
+            seq = p + 1;
         }
-        s = acc * a.scale;
+    } else {
+        seq = a.seq_len;
     }
-    const float m = block_max(s, s_red, 4);
-    const float e = p < seq ? expf(s - m) : 0.f;
-    s_e[threadIdx.x] = e;
-    const float l = block_sum(e, s_red, 4);  // (its barriers also publish s_e)
-    if ((int)threadIdx.x < hd) {
-        const int np = min(kAttnChunk, seq - p0);
-        const float* vp = a.vcache + (size_t)p0 * kvd + (size_t)kvh * hd + threadIdx.x;
-        float acc = 0.f;
-        for (int t = 0; t < np; ++t) acc = fmaf(s_e[t], vp[(size_t)t * kvd], acc);
-        part[2 + threadIdx.x] = acc;
+    const bool has_new = a.fused && p < a.max_seq;  // row p comes from k_new / v_new
+    const int p0 = c * kAttnChunk;
+    float* part = a.partial + ((size_t)g * nch + c) * QH * (HD + 2);
+
+    const int nact = min(nch, (seq + kAttnChunk - 1) / kAttnChunk);  // chunks with positions
+    if (p0 < seq) {
+        // this lane's K and V rows: 8 dims of position p0 + wave*PW + it*PPI + pg;
+        // the cache rows are loaded first, row p (the current token's, not yet
+        // in the cache) is taken from LDS once it is prepared
+        const int lp = lane % LP, pg = lane / LP;
+        float kr[IT][8], vr[IT][8];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int pp = p0 + wave * PW + it * PPI + pg;
+            float4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, v0 = k0, v1 = k0;
+            if (pp < seq && !(has_new && pp == p)) {
+                const size_t off = (size_t)pp * kvd + (size_t)kvh * HD + 8 * lp;
+                k0 = *reinterpret_cast<const float4*>(a.kcache + off);
+                k1 = *reinterpret_cast<const float4*>(a.kcache + off + 4);
+                v0 = *reinterpret_cast<const float4*>(a.vcache + off);
+                v1 = *reinterpret_cast<const float4*>(a.vcache + off + 4);
+            }
+            kr[it][0] = k0.x, kr[it][1] = k0.y, kr[it][2] = k0.z, kr[it][3] = k0.w;
+            kr[it][4] = k1.x, kr[it][5] = k1.y, kr[it][6] = k1.z, kr[it][7] = k1.w;
+            vr[it][0] = v0.x, vr[it][1] = v0.y, vr[it][2] = v0.z, vr[it][3] = v0.w;
+            vr[it][4] = v1.x, vr[it][5] = v1.y, vr[it][6] = v1.z, vr[it][7] = v1.w;
+        }
+        // q heads (and the new k when this chunk holds row p): per-head
+        // RMSNorm (InferenceEngine.swift:538-548), then RoPE (:521-536)
+        const bool mine_new = has_new && p >= p0 && p < p0 + kAttnChunk;
+        const int items = QH + (mine_new ? 1 : 0);
+        for (int it = wave; it < items; it += 4) {
+            const bool is_k = it == QH;
+            const float* src = is_k ? a.k_new + (size_t)kvh * HD : a.q + (size_t)(h0 + it) * HD;
+            float* dst = is_k ? s_kv[0] : s_q[it];
+            const uint16_t* nw = is_k ? a.k_norm : a.q_norm;
+            float v[HD / 64];
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < HD / 64; ++j) {
+                v[j] = src[lane + 64 * j];
+                ss = fmaf(v[j], v[j], ss);
+            }
+            if (a.fused && nw) {
+                const float rms = 1.0f / sqrtf(wave_sum(ss) / (float)HD + a.eps);
+#pragma unroll
+                for (int j = 0; j < HD / 64; ++j) v[j] *= rms * bf16_to_f32(nw[lane + 64 * j]);
+            }
+#pragma unroll
+            for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = v[j];
+        }
+        if (mine_new)
+            for (int d = tid; d < HD; d += 256) s_kv[1][d] = a.v_new[(size_t)kvh * HD + d];
+        __syncthreads();
+        if (a.fused) {
+            for (int t = tid; t < items * HALF; t += 256) {
+                const int it = t / HALF, d = t - it * HALF;
+                float* vec = it == QH ? s_kv[0] : s_q[it];
+                const float freq = 1.0f / powf(a.rope_theta, (float)(2 * d) / (float)HD);
+                const float ang = (float)p * freq;
+                const float cs = cosf(ang), sn = sinf(ang);
+                const float x0 = vec[d], x1 = vec[d + HALF];
+                vec[d] = x0 * cs - x1 * sn;
+                vec[d + HALF] = x0 * sn + x1 * cs;
+            }
+            __syncthreads();
+            // the new row into the caches, by the first group of its kv head
+            if (mine_new && h0 % a.hpkv == 0) {
+                for (int d = tid; d < HD; d += 256) {
+                    a.kcache[(size_t)p * kvd + (size_t)kvh * HD + d] = s_kv[0][d];
+                    a.vcache[(size_t)p * kvd + (size_t)kvh * HD + d] = s_kv[1][d];
+                }
+            }
+        }
+
+        if (mine_new) {
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                if (p0 + wave * PW + it * PPI + pg != p) continue;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    kr[it][e] = s_kv[0][8 * lp + e];
+                    vr[it][e] = s_kv[1][8 * lp + e];
+                }
+            }
+        }
+        // scores (attnScores, Shaders.metal:209-243)
+        float qv[QH][8];
+#pragma unroll
+        for (int i = 0; i < QH; ++i) {
+            const float4 q0 = *reinterpret_cast<const float4*>(&s_q[i][8 * lp]);
+            const float4 q1 = *reinterpret_cast<const float4*>(&s_q[i][8 * lp + 4]);
+            qv[i][0] = q0.x, qv[i][1] = q0.y, qv[i][2] = q0.z, qv[i][3] = q0.w;
+            qv[i][4] = q1.x, qv[i][5] = q1.y, qv[i][6] = q1.z, qv[i][7] = q1.w;
+        }
+        {
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const int pl = wave * PW + it * PPI + pg;
+#pragma unroll
+                for (int i = 0; i < QH; ++i) {
+                    float d = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d = fmaf(qv[i][e], kr[it][e], d);
+#pragma unroll
+                    for (int o = 1; o < LP; o <<= 1) d += __shfl_xor(d, o);
+                    if (lp == 0) s_p[i][pl] = p0 + pl < seq ? d * a.scale : -INFINITY;
+                }
+            }
+        }
+        __syncthreads();
+        // the chunk's softmax numerators (attnSoftmax, :245-289), lane = position
+        for (int i = wave; i < QH; i += 4) {
+            const float s = s_p[i][lane];
+            const float m = wave_max(s);
+            const float e = s == -INFINITY ? 0.f : expf(s - m);
+            const float l = wave_sum(e);
+            s_p[i][lane] = e;
+            if (lane == 0) {
+                s_m[i] = m;
+                s_l[i] = l;
+            }
+        }
+        __syncthreads();
+        // weighted V sum (attnValues, :291-326)
+        float acc[QH][8];
+#pragma unroll
+        for (int i = 0; i < QH; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+        {
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const int pl = wave * PW + it * PPI + pg;
+#pragma unroll
+                for (int i = 0; i < QH; ++i) {
+                    const float w = s_p[i][pl];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[i][e] = fmaf(w, vr[it][e], acc[i][e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int o = LP; o < 64; o <<= 1)
+#pragma unroll
+            for (int i = 0; i < QH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[i][e] += __shfl_xor(acc[i][e], o);
+        if (pg == 0) {
+#pragma unroll
+            for (int i = 0; i < QH; ++i) {
+                *reinterpret_cast<float4*>(&s_acc[wave][i][8 * lp]) =
+                    float4{acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+                *reinterpret_cast<float4*>(&s_acc[wave][i][8 * lp + 4]) =
+                    float4{acc[i][4], acc[i][5], acc[i][6], acc[i][7]};
+            }
+        }
+        __syncthreads();
+        if (nact == 1) {
+            // the only chunk with positions: no merge
+            for (int t = tid; t < QH * HD; t += 256) {
+                const int i = t / HD, d = t - i * HD;
+                a.out[(size_t)(h0 + i) * HD + d] =
+                    (((s_acc[0][i][d] + s_acc[1][i][d]) + s_acc[2][i][d]) + s_acc[3][i][d]) / s_l[i];
+            }
+            return;
+        }
+        for (int t = tid; t < QH * HD; t += 256) {
+            const int i = t / HD, d = t - i * HD;
+            st_coh(part + i * (HD + 2) + 2 + d,
+                   ((s_acc[0][i][d] + s_acc[1][i][d]) + s_acc[2][i][d]) + s_acc[3][i][d]);
+        }
+        if (tid < QH) {
+            st_coh(part + tid * (HD + 2), s_m[tid]);
+            st_coh(part + tid * (HD + 2) + 1, s_l[tid]);
+        }
     }
-    if (threadIdx.x == 0) {
-        part[0] = m;
-        part[1] = l;
+    if (nact == 1) return;  // (chunks past the sequence are not read by the merge)
+
+    // the last workgroup of the group merges the chunks:
+    // out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M)
+    if (!last_workgroup(a.counters + g, nch, &s_flag)) return;
+    const size_t cstride = (size_t)QH * (HD + 2);
+    const float* base = a.partial + (size_t)g * nch * cstride;
+    float* s_red = &s_acc[0][0][0];  // free now
+    for (int i = 0; i < QH; ++i) {
+        const float* pb = base + i * (HD + 2);
+        float mloc = -INFINITY;
+        for (int cc = tid; cc < nact; cc += 256) {
+            const float m = ld_coh(pb + cc * cstride);
+            s_cf[cc] = m;
+            mloc = fmaxf(mloc, m);
+        }
+        const float M = block_max(mloc, s_red, 4);
+        float lloc = 0.f;
+        for (int cc = tid; cc < nact; cc += 256) {
+            const float f = expf(s_cf[cc] - M);
+            lloc = fmaf(ld_coh(pb + cc * cstride + 1), f, lloc);
+            s_cf[cc] = f;
+        }
+        const float inv = 1.0f / block_sum(lloc, s_red, 4);  // (its barriers publish s_cf)
+        for (int d = tid; d < HD; d += 256) {
+            float acc = 0.f;
+            for (int c0 = 0; c0 < nact; c0 += 8) {
+                float t[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    t[j] = c0 + j < nact ? ld_coh(pb + (size_t)(c0 + j) * cstride + 2 + d) : 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (c0 + j < nact) acc = fmaf(s_cf[c0 + j], t[j], acc);
+            }
+            a.out[(size_t)(h0 + i) * HD + d] = acc * inv;
+        }
+        __syncthreads();  // s_cf is rewritten for the next head
     }
+    if (tid == 0) reset_counter(a.counters + g);
 }
 
-// Workgroup per head, thread d < head_dim: out = sum_c acc_c e^(m_c - M) / L.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int nchunks) {
-    const int head = blockIdx.x, d = threadIdx.x, hd = a.head_dim;
-    if (d >= hd) return;
-    const float* part = a.partial + (size_t)head * nchunks * (hd + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, part[(size_t)c * (hd + 2)]);
-    float L = 0.f, acc = 0.f;
-    for (int c = 0; c < nchunks; ++c) {
-        const float* pc = part + (size_t)c * (hd + 2);
-        if (pc[0] == -INFINITY) continue;
-        const float f = expf(pc[0] - M);
-        L = fmaf(pc[1], f, L);
-        acc = fmaf(pc[2 + d], f, acc);
-    }
-    a.out[(size_t)head * hd + d] = acc / L;
-}
+// ---- argmax (standalone) -------------------------------------------------------------
 
-// ---- argmax -------------------------------------------------------------------------
-
-// (value, index) pairs: larger value wins, ties to the lower index.
-__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
-    return v > bv || (v == bv && i < bi);
-}
-
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* x, int n, int32_t* out,
-                                                      int32_t* pos, int max_seq) {
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* x, int n, int32_t* out) {
     __shared__ float s_v[16];
     __shared__ int s_i[16];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -297,15 +627,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* x, int n, int
             bi = i;
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (am_better(ov, oi, bv, bi)) {
-            bv = ov;
-            bi = oi;
-        }
-    }
+    wave_argmax(bv, bi);
     if (lane == 0) {
         s_v[wave] = bv;
         s_i[wave] = bi;
@@ -317,14 +639,36 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* x, int n, int
                 bv = s_v[w];
                 bi = s_i[w];
             }
-        // the reference's scan starts from x[0] with a strict >, so a NaN
-        // there is never replaced; all NaN also gives 0
+        // InferenceEngine.swift:550-555 scans from x[0] with a strict >
         *out = (bi < n && !__builtin_isnan(x[0])) ? bi : 0;
-        if (pos && *pos < max_seq) *pos += 1;
     }
 }
 
 __global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
+
+int mv_rpw(int rows) { return rows >= 8192 ? 4 : rows >= 2048 ? 2 : 1; }
+
+template <int RPW>
+int launch_mv(const MvArgs& a, hipStream_t st) {
+    const unsigned grid = (unsigned)((a.rows + 4 * RPW - 1) / (4 * RPW));
+    if (a.cols <= kMvStageMax)
+        hipLaunchKernelGGL((matvec_kernel<RPW, true>), dim3(grid), dim3(256), (size_t)a.cols * 4, st, a);
+    else
+        hipLaunchKernelGGL((matvec_kernel<RPW, false>), dim3(grid), dim3(256), 0, st, a);
+    return (int)hipGetLastError();
+}
+
+template <int HD>
+int launch_attn_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
+    switch (a.qh) {
+        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, st, a); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
 
 }  // namespace
 
@@ -339,44 +683,48 @@ int launch_rmsnorm(const float* x, const uint16_t* w, float* out, int n, float e
     return (int)hipGetLastError();
 }
 
-int launch_matvec_bf16(const MvArgs& a, void* stream) {
-    if (a.cols % 8 || a.rows <= 0) return (int)hipErrorInvalidValue;
-    const int per_wg = 4 * kMvRows;
-    hipLaunchKernelGGL(matvec_bf16_kernel, dim3((unsigned)((a.rows + per_wg - 1) / per_wg)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
-    return (int)hipGetLastError();
+int matvec_workgroups(int rows) {
+    const int per = 4 * mv_rpw(rows);
+    return (rows + per - 1) / per;
 }
 
-int launch_attention(const AttnArgs& a, int max_positions, void* stream) {
+int launch_matvec_bf16(const MvArgs& a, void* stream) {
+    if (a.cols % 8 || a.rows <= 0 || a.cols <= 0) return (int)hipErrorInvalidValue;
+    if ((a.embed || a.norm_w) && a.cols > kMvStageMax) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int nchunks = (max_positions + kAttnChunk - 1) / kAttnChunk;
-    hipLaunchKernelGGL(attn_partial_kernel, dim3((unsigned)a.num_heads, (unsigned)nchunks), dim3(256), 0,
-                       st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.num_heads), dim3(256), 0, st, a, nchunks);
-    return (int)hipGetLastError();
+    switch (mv_rpw(a.rows)) {
+        case 4: return launch_mv<4>(a, st);
+        case 2: return launch_mv<2>(a, st);
+        default: return launch_mv<1>(a, st);
+    }
+}
+
+int attention_qh(int hpkv) {
+    for (int q = kAttnMaxQH; q > 1; q >>= 1)
+        if (hpkv % q == 0) return q;
+    return 1;
 }
 
 int attention_partial_floats(int num_heads, int head_dim, int max_positions) {
     return num_heads * ((max_positions + kAttnChunk - 1) / kAttnChunk) * (head_dim + 2);
 }
 
-int launch_argmax(const float* x, int n, int32_t* out, int32_t* pos, int max_seq, void* stream) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), x, n, out,
-                       pos, max_seq);
-    return (int)hipGetLastError();
+int launch_attention(const AttnArgs& a, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (a.qh <= 0 || a.num_heads % a.qh || a.hpkv % a.qh) return (int)hipErrorInvalidValue;
+    const dim3 grid((unsigned)(a.num_heads / a.qh),
+                    (unsigned)((a.max_seq + kAttnChunk - 1) / kAttnChunk));
+    switch (a.head_dim) {
+        case 64: return launch_attn_hd<64>(a, grid, st);
+        case 128: return launch_attn_hd<128>(a, grid, st);
+        case 256: return launch_attn_hd<256>(a, grid, st);
+        default: return (int)hipErrorInvalidValue;
+    }
 }
 
-int launch_embed(const DenseStepArgs& a, void* stream) {
-    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((a.h + 255) / 256)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
-    return (int)hipGetLastError();
-}
-
-int launch_qk_rope_kv(const DenseStepArgs& a, int layer, void* stream) {
-    hipLaunchKernelGGL(qk_rope_kv_kernel, dim3((unsigned)(a.num_heads + a.num_kv_heads)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a, layer);
+int launch_argmax(const float* x, int n, int32_t* out, void* stream) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), x, n,
+                       out);
     return (int)hipGetLastError();
 }
 

@@ -45,6 +45,14 @@ struct FusedArgs {
     const float* given_w;        // [K]
     int32_t* user_idx;           // optional copies of the routing
     float* user_w;
+    // optional RMSNorm of an f32 input (the decoder's post-attention norm):
+    // x <- x * rsqrt(sum(x^2) / h + x_eps) * x_norm_w, sum(x^2) given as
+    // n_ssq partial sums (added in a fixed order, so every wave gets the same
+    // value)
+    const float* x_ssq;
+    const uint16_t* x_norm_w;
+    int32_t n_ssq;
+    float x_eps;
     // hand-off state.  It starts at zero and is never reset between launches:
     // every workgroup counts its own launches in seen[wg], so all workgroups
     // agree on the launch number ("tag") without communicating.
@@ -132,53 +140,90 @@ int launch_dequant(const uint8_t* expert_base, const ProjView& p, int32_t gs, fl
 
 // One weight segment of a bf16 matvec: y[r] = W[r] . x (+ res[r]).
 struct MvSeg {
-    const uint16_t* w;           // [rows][cols]
-    float* y;                    // [rows]
-    const float* res;            // [rows] or null
+    const uint16_t* w;   // [rows][cols] bf16
+    float* y;            // [rows]
+    const float* res;    // [rows] or null
     int32_t rows;
 };
-// Up to three segments sharing the input x (rows concatenated).
+
+// y = W x over up to three segments sharing the input x.
+//   input:    x (f32), or row *token (or token[*pos] with seq_cap > 0) of the
+//             bf16 table `embed` (a token outside [0, vocab) embeds row 0
+//             and sets error flag 16); x_copy: workgroup 0 stores the f32
+//             input there; norm_w: the input is RMS-normalised first,
+//             x * rsqrt(mean(x^2) + eps) * w (the input is staged in LDS)
+//   outputs:  ssq_out non-null: each workgroup stores the sum of squares of
+//             its output rows (after the residual) at ssq_out[workgroup];
+//             counter non-null (argmax): the last workgroup to finish reduces
+//             the per-workgroup best (am_val, am_idx) to the greedy token of
+//             segment 0's output and advances *pos; the counter is back at 0
+//             when the kernel ends.
 struct MvArgs {
     MvSeg seg[3];
-    const float* x;              // [cols]
-    int32_t rows, cols;          // total rows of the segments, shared columns
-};
-
-struct AttnArgs {
-    const float* q;              // [num_heads][head_dim]
-    const float* kcache;         // [>= seq][num_kv_heads * head_dim]
-    const float* vcache;
-    float* out;                  // [num_heads][head_dim]
-    float* partial;              // [num_heads][chunks][head_dim + 2] scratch
-    const int32_t* seq_ptr;      // position of the current token (seq = pos + 1), or null
-    int32_t seq_len;             // used when seq_ptr is null
+    const float* x;
+    int32_t rows, cols;
+    const uint16_t* embed;
+    const int32_t* token;
+    int32_t seq_cap;
+    int32_t vocab;
+    float* x_copy;
+    const uint16_t* norm_w;
+    float eps;
+    float* ssq_out;              // [workgroups]
+    uint32_t* counter;
+    float* am_val;               // [workgroups]
+    int32_t* am_idx;             // [workgroups]
+    int32_t* tok_out;            // single mode: *tok_out; sequence mode: tok_out[p + 1]
+    int32_t n_prompt;
+    int32_t* pos;                // device position (read for the embedding, advanced by argmax)
     int32_t max_seq;
-    int32_t num_heads, num_kv_heads, hpkv, head_dim;
-    float scale;                 // 1 / sqrt(head_dim)
+    uint32_t* err;
 };
 
-struct DenseStepArgs {
-    const int32_t* token;        // device: the step's input token
-    int32_t* pos;                // device: the current position
-    const uint16_t* embed;       // [vocab][h]
-    float* x_out;                // embedding output [h]
-    float *q, *k, *v;            // projections of the current layer
-    const uint16_t* q_norm;      // [layers][head_dim] or null
+// Decode attention of one query position.  Workgroup (g, c): q heads
+// g*qh .. g*qh+qh-1 (one kv head) over positions 64c .. 64c+63.
+//   fused = 1: q, k_new, v_new are the raw projections of the current token;
+//     q and k get the per-head RMSNorm (q_norm/k_norm non-null) and RoPE at
+//     p = *pos, the new k/v row is stored at cache row p (flag 32 and no
+//     store when p >= max_seq), positions 0..p attended;
+//   fused = 0: q final, positions 0..seq_len-1 all from the caches.
+// The last workgroup of each group merges the chunks into out; counters
+// ([groups]) are back at 0 when the kernel ends.
+struct AttnArgs {
+    int32_t fused;
+    const float* q;              // [num_heads][head_dim]
+    const float* k_new;          // [num_kv_heads][head_dim] (fused)
+    const float* v_new;
+    const uint16_t* q_norm;      // [head_dim] or null
     const uint16_t* k_norm;
-    float* kcache;               // [layers][max_seq][num_kv_heads * head_dim]
+    float* kcache;               // [max_seq][num_kv_heads * head_dim]
     float* vcache;
-    uint32_t* err;               // sticky device error flag
-    int32_t vocab, h, num_heads, num_kv_heads, head_dim, max_seq, qk_norm;
-    float rope_theta, eps;
+    float* out;                  // [num_heads][head_dim]
+    float* partial;              // [groups][chunks][qh][head_dim + 2]
+    uint32_t* counters;          // [groups]
+    const int32_t* pos;
+    uint32_t* err;
+    int32_t seq_len;             // fused = 0
+    int32_t max_seq;             // cache rows (fused) / seq_len
+    int32_t num_heads, num_kv_heads, hpkv, head_dim, qh;
+    float scale, rope_theta, eps;
 };
+
+constexpr int kAttnChunk = 64;   // positions per attention workgroup
+constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
+constexpr int kAttnMaxChunks = 1024;  // 65536 positions
+constexpr int kMvStageMax = 8192;   // largest staged (normalised / embedded) input, floats
 
 int launch_set_i32(int32_t* p, int32_t v, void* stream);
 int launch_rmsnorm(const float* x, const uint16_t* w, float* out, int n, float eps, void* stream);
+// Workgroups of a matvec launch (the size of am_val / am_idx).
+int matvec_workgroups(int rows);
 int launch_matvec_bf16(const MvArgs& a, void* stream);
-int launch_attention(const AttnArgs& a, int max_positions, void* stream);
+// q heads per attention workgroup (0: unsupported hpkv).
+int attention_qh(int hpkv);
 int attention_partial_floats(int num_heads, int head_dim, int max_positions);
-int launch_argmax(const float* x, int n, int32_t* out, int32_t* pos, int max_seq, void* stream);
-int launch_embed(const DenseStepArgs& a, void* stream);
-int launch_qk_rope_kv(const DenseStepArgs& a, int layer, void* stream);
+int launch_attention(const AttnArgs& a, void* stream);
+// Greedy token of x[0..n) to *out (ties to the lower index; x[0] NaN gives 0).
+int launch_argmax(const float* x, int n, int32_t* out, void* stream);
 
 }  // namespace m1moe

@@ -52,6 +52,25 @@ void fill_bf16(uint64_t key, uint64_t n, float sigma, bool absval, uint16_t* out
     }
 }
 
+// Runs body(i0, i1) over [0, n) on up to 16 threads (values depend only on
+// the index, so the split does not change them).
+template <class F>
+void parallel_range(uint64_t n, F body) {
+    constexpr uint64_t kMinPerThread = 1u << 20;
+    unsigned hw = std::thread::hardware_concurrency();
+    uint64_t nt = hw ? hw : 1;
+    if (nt > 16) nt = 16;
+    if (nt > n / kMinPerThread) nt = n / kMinPerThread;
+    if (nt <= 1) {
+        body((uint64_t)0, n);
+        return;
+    }
+    std::vector<std::thread> pool;
+    for (uint64_t t = 1; t < nt; ++t) pool.emplace_back(body, n * t / nt, n * (t + 1) / nt);
+    body((uint64_t)0, n / nt);
+    for (auto& th : pool) th.join();
+}
+
 void fill_words(uint64_t key, uint64_t n, uint32_t* out) {
     // every nibble of a uniform 32-bit word is uniform in 0..15
     for (uint64_t i = 0; i < n; ++i) out[i] = (uint32_t)(draw(key, i) >> 32);
@@ -69,7 +88,14 @@ inline uint64_t expert_tensor_id(int32_t layer, int32_t expert, int proj, int ki
 extern "C" int32_t m1moe_synth_normal_bf16(uint64_t seed, uint64_t tensor_id, uint64_t n,
                                            float sigma, int32_t absval, uint16_t* out) {
     if (!out && n) return m1moe::fail(M1MOE_ERR_INVALID, "synth_normal_bf16: null output");
-    fill_bf16(stream_key(seed, tensor_id), n, sigma, absval != 0, out);
+    const uint64_t key = stream_key(seed, tensor_id);
+    parallel_range(n, [&](uint64_t i0, uint64_t i1) {
+        for (uint64_t i = i0; i < i1; ++i) {
+            float v = normal_at(key, i, sigma);
+            if (absval) v = std::fabs(v);
+            out[i] = f32_to_bf16_rne(v);
+        }
+    });
     return M1MOE_OK;
 }
 
@@ -77,7 +103,9 @@ extern "C" int32_t m1moe_synth_normal_f32(uint64_t seed, uint64_t tensor_id, uin
                                           float sigma, float* out) {
     if (!out && n) return m1moe::fail(M1MOE_ERR_INVALID, "synth_normal_f32: null output");
     const uint64_t key = stream_key(seed, tensor_id);
-    for (uint64_t i = 0; i < n; ++i) out[i] = normal_at(key, i, sigma);
+    parallel_range(n, [&](uint64_t i0, uint64_t i1) {
+        for (uint64_t i = i0; i < i1; ++i) out[i] = normal_at(key, i, sigma);
+    });
     return M1MOE_OK;
 }
 

@@ -198,6 +198,29 @@ class Decoder:
         check(self.lib.m1moe_dec_step(self.handle, _ptr(token_in), _ptr(token_out),
                                       _ptr(logits)), "m1moe_dec_step")
 
+    def step_seq(self, seq, n_prompt: int, seq_cap: int, logits=None) -> None:
+        """Sequence-mode step (asynchronous): embeds seq[pos]; past the prompt
+        stores the greedy token at seq[pos + 1].  n_prompt + n_gen calls after
+        reset() run prompt-then-generate with no host round trip."""
+        check(self.lib.m1moe_dec_step_seq(self.handle, _ptr(seq), int(n_prompt), int(seq_cap),
+                                          _ptr(logits)), "m1moe_dec_step_seq")
+
+    def generate(self, prompt, n_gen: int):
+        """Sources/bench/main.swift:136-163 at temperature 0: the prompt
+        forwarded token by token, then n_gen greedy steps; returns the
+        n_gen + 1 greedy tokens (the prompt's own prediction first)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        P, cap = prompt.size, prompt.size + n_gen + 1
+        seq = self.ctx.alloc(4 * cap)
+        seq.upload(np.concatenate([prompt, np.zeros(cap - P, np.int32)]))
+        self.reset()
+        for _ in range(P + n_gen):
+            self.step_seq(seq, P, cap)
+        self.ctx.sync()
+        out = seq.download(np.int32)[P:]
+        seq.free()
+        return out
+
     def forward(self, token: int, return_logits: bool = False):
         """InferenceEngine.forward(token:) at temperature 0: the greedy next
         token (and the f32 logits when asked)."""

@@ -243,6 +243,44 @@ def test_decoder_greedy_loop_in_a_graph():
         p.close()
 
 
+def test_decoder_sequence_mode_and_one_step_graph():
+    """m1moe_dec_step_seq: eager calls, and one captured step replayed P + G
+    times, give the tokens of the forward() loop (prompt then greedy)."""
+    p = Pair(synth.DECODERS["tiny_dec"], seed=16, max_seq=40)
+    try:
+        ctx, dec = p.ctx, p.dec
+        prompt = synth.prompt_tokens(p.wl, 9, 7)
+        P, G = len(prompt), 20
+        want = []
+        tok = None
+        for t in prompt:
+            tok = dec.forward(int(t))
+        for _ in range(G):
+            want.append(tok)
+            tok = dec.forward(tok)
+        want.append(tok)
+        assert dec.generate(prompt, G).tolist() == want
+        cap = P + G + 1
+        seq = ctx.alloc(4 * cap)
+        init = np.concatenate([prompt, np.full(cap - P, -7, np.int32)])
+        ctx.graph_begin()
+        dec.step_seq(seq, P, cap)
+        graph = ctx.graph_end()
+        for rep in range(3):
+            seq.upload(init)
+            dec.reset()
+            say(f"one-step graph, {P + G} replays, round {rep}")
+            for _ in range(P + G):
+                graph.launch()
+            ctx.sync()
+            got = seq.download(np.int32)
+            assert got[:P].tolist() == prompt.tolist()  # the prompt is never overwritten
+            assert got[P:].tolist() == want, f"round {rep}"
+            assert dec.position() == P + G
+    finally:
+        p.close()
+
+
 def test_decoder_dense_only_is_tight():
     """With the MoE block's expert weights all zero (scales and biases 0) the
     block adds only the residual, so the step is the dense kernels alone:
@@ -338,6 +376,8 @@ def test_decoder_rejects_missing_weights_and_bad_shapes():
             Decoder(ctx, bad)
         with pytest.raises(m.M1MoEError, match="count"):
             dec.upload(_lib.W_Q, 0, np.zeros(5, np.uint16))
+        with pytest.raises(m.M1MoEError, match="n_prompt"):
+            dec.step_seq(tok, 5, 4)
         dec.close()
     finally:
         ctx.close()

@@ -221,14 +221,19 @@ __device__ __forceinline__ void norm8(const FusedArgs& a, int d, float rms, floa
     for (int i = 0; i < 8; ++i) xv[i] = xv[i] * rms * bf16x8_at(w, i);
 }
 
+// rms / need_rms: a normalised input's scale, computed at the first call
+// (after this call's row loads are issued, so the two latencies overlap).
 __device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, uint32_t* s_tag,
-                              uint32_t tag_reg, double* s_lp, float rms) {
+                              uint32_t tag_reg, double* s_lp, float& rms, bool& need_rms) {
     if (wave < 4) {
         const uint16_t* wr = a.router + (size_t)e * a.h;
         const int C = a.h / 32;
+        const int niter = (C + 63) / 64;
         double acc = 0.0;
-        for (int c = lane; c < C; c += 64) {
-            const int d = c * 32 + wave * 8;
+        for (int it = 0; it < niter; ++it) {
+            const int c = lane + 64 * it;
+            const bool ok = c < C;
+            const int d = (ok ? c : 0) * 32 + wave * 8;
             const uint4 wv = *reinterpret_cast<const uint4*>(wr + d);
             float xv[8];
             if (a.x_bf16) {
@@ -241,10 +246,18 @@ __device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, uin
                 const float4 x1 = *reinterpret_cast<const float4*>(xr + 4);
                 xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
                 xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
-                if (a.x_norm_w) norm8(a, d, rms, xv);
+                if (a.x_norm_w) {
+                    if (need_rms) {  // uniform: every lane of the wave is here
+                        rms = input_rms(a, lane);
+                        need_rms = false;
+                    }
+                    norm8(a, d, rms, xv);
+                }
             }
+            if (ok) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv, i) * (double)xv[i];
+                for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv, i) * (double)xv[i];
+            }
         }
         acc = wave_sum_f64_last(acc);
         if (lane == 63) s_lp[wave] = acc;
@@ -801,9 +814,10 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
     // load overlaps the router row loads of the producers
     const uint32_t tag_reg = threadIdx.x == 0 ? ld_u32(a.seen + wg) + 1u : 0u;
     if (!a.given_idx && wg < a.E) {
-        const float rms = a.x_norm_w ? input_rms(a, lane) : 1.f;
+        float rms = 1.f;
+        bool need_rms = a.x_norm_w != nullptr;
         for (int e = wg; e < a.E; e += gridDim.x)
-            produce_logit(a, e, wave, lane, &s_tag, tag_reg, s_lp, rms);
+            produce_logit(a, e, wave, lane, &s_tag, tag_reg, s_lp, rms, need_rms);
     } else {
         if (threadIdx.x == 0) s_tag = tag_reg;
         __syncthreads();

@@ -338,6 +338,37 @@ int32_t m1moe_dec_step_seq(m1moe_dec_t dec, int32_t* d_seq, int32_t n_prompt,
 /* The current position (waits for the context stream). */
 int32_t m1moe_dec_position(m1moe_dec_t dec, int32_t* pos);
 
+/* ---- the converted model directory on disk (host-side) -----------------
+ * scripts/extract_olmoe.py writes model_weights.bin (non-expert tensors,
+ * 4-byte aligned) + model_weights.json ({name: {offset, shape, dtype}}) and
+ * packed_experts/layer_NN.bin (E expert blocks per layer). */
+typedef struct m1moe_store* m1moe_store_t;
+enum { M1MOE_DT_BF16 = 0, M1MOE_DT_F32 = 1, M1MOE_DT_U32 = 2 };
+
+/* WeightStore.init (WeightStore.swift:47-76): maps the .bin read-only and
+ * reads the manifest; every tensor must lie inside the file.  Host only. */
+int32_t m1moe_store_open(const char* bin_path, const char* json_path,
+                         m1moe_store_t* out);
+void m1moe_store_close(m1moe_store_t store);
+int32_t m1moe_store_count(m1moe_store_t store, int32_t* n);
+/* WeightStore.info / pointer (:86-100): the tensor's bytes inside the
+ * mapping, dtype (M1MOE_DT_*), shape (4 entries, unused ones 0) and rank.
+ * Each output is nullable. */
+int32_t m1moe_store_tensor(m1moe_store_t store, const char* name,
+                           const void** data, int32_t* dtype, int64_t* shape,
+                           int32_t* ndim);
+
+/* Uploads a converted model directory: every layer_NN.bin of the context's
+ * layers (m1moe_upload_layer_experts; the size must be E x expert_bytes),
+ * each layer's router (mlp.gate.weight, or block_sparse_moe.gate.weight,
+ * InferenceEngine.swift:593-598) and, when dec is non-null, the dense
+ * tensors under the reference's weight keys (:580-599; f32 tensors are
+ * rounded to bf16; q/k norms: the first head_dim values).  Shapes are
+ * checked against the context and decoder.  threads: parallel reads per
+ * layer file. */
+int32_t m1moe_load_model(m1moe_ctx_t ctx, m1moe_dec_t dec, const char* model_dir,
+                         int32_t threads);
+
 /* ---- seeded synthetic inputs (host-only; bench and test data) ----------
  * Counter-based: value i of tensor `tensor_id` under `seed` is a function of
  * (seed, tensor_id, i) only, so any slice can be generated independently.

@@ -55,6 +55,9 @@ class DecShape(ctypes.Structure):
     ]
 
 
+# dtypes of the on-disk manifest (m1moe_store_tensor)
+DT_BF16, DT_F32, DT_U32 = 0, 1, 2
+
 # dense tensor ids of m1moe_dec_upload
 (W_EMBED, W_LM_HEAD, W_FINAL_NORM, W_IN_NORM, W_POST_NORM, W_Q, W_K, W_V, W_O, W_Q_NORM,
  W_K_NORM) = range(11)
@@ -122,6 +125,13 @@ _PROTOTYPES = [
     ("m1moe_dec_step", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
     ("m1moe_dec_step_seq", c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     ("m1moe_dec_position", c_int32, [c_void_p, POINTER(c_int32)]),
+    ("m1moe_store_open", c_int32, [c_char_p, c_char_p, POINTER(c_void_p)]),
+    ("m1moe_store_close", None, [c_void_p]),
+    ("m1moe_store_count", c_int32, [c_void_p, POINTER(c_int32)]),
+    ("m1moe_store_tensor", c_int32,
+     [c_void_p, c_char_p, POINTER(c_void_p), POINTER(c_int32), POINTER(ctypes.c_int64),
+      POINTER(c_int32)]),
+    ("m1moe_load_model", c_int32, [c_void_p, c_void_p, c_char_p, c_int32]),
     ("m1moe_synth_normal_bf16", c_int32,
      [c_uint64, c_uint64, c_uint64, c_float, c_int32, c_void_p]),
     ("m1moe_synth_normal_f32", c_int32, [c_uint64, c_uint64, c_uint64, c_float, c_void_p]),

@@ -121,6 +121,10 @@ int32_t moe_decode_normed(m1moe_ctx_t ctx, int32_t layer, const float* d_x, cons
                           int32_t n_ssq, const uint16_t* d_norm_w, float eps,
                           const float* d_residual, float* d_out);
 
+// A decoder's vocabulary and attention dimensions (for the loader).
+int32_t dec_dims(m1moe_dec_t dec, int32_t* vocab, int32_t* num_heads, int32_t* num_kv_heads,
+                 int32_t* head_dim, int32_t* qk_norm);
+
 inline int32_t launched(int rc, const char* what) {
     if (rc != (int)hipSuccess)
         return fail(M1MOE_ERR_HIP, "launch of %s failed: %s", what,

@@ -426,6 +426,17 @@ bool aligned_i32(const void* p) { return p && reinterpret_cast<uintptr_t>(p) % 4
 
 }  // namespace
 
+int32_t m1moe::dec_dims(m1moe_dec_t dec, int32_t* vocab, int32_t* num_heads, int32_t* num_kv_heads,
+                        int32_t* head_dim, int32_t* qk_norm) {
+    if (!dec) return fail(M1MOE_ERR_INVALID, "null decoder");
+    *vocab = dec->sh.vocab;
+    *num_heads = dec->sh.num_heads;
+    *num_kv_heads = dec->sh.num_kv_heads;
+    *head_dim = dec->sh.head_dim;
+    *qk_norm = dec->sh.qk_norm;
+    return M1MOE_OK;
+}
+
 extern "C" {
 
 int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in, int32_t* d_token_out,

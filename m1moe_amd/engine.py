@@ -204,6 +204,14 @@ class HIPContext:
             self.handle, int(layer), b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
             int(b.size)), "m1moe_set_logit_bias")
 
+    def load_model(self, model_dir: str, decoder=None, threads: int = 8) -> None:
+        """Uploads a converted model directory (model_weights.bin/.json and
+        packed_experts/layer_NN.bin, as scripts/extract_olmoe.py writes them):
+        every layer's experts and router, and the dense tensors into `decoder`
+        (a m1moe_amd.decoder.Decoder) when given."""
+        check(self.lib.m1moe_load_model(self.handle, decoder.handle if decoder is not None else None,
+                                        model_dir.encode(), int(threads)), "m1moe_load_model")
+
     # ---- memory ----------------------------------------------------------
     def alloc(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)

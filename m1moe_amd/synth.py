@@ -203,6 +203,69 @@ def prompt_tokens(wl: DecoderWorkload, seed: int, n: Optional[int] = None) -> np
     return rng.integers(0, wl.vocab, size=int(n or wl.prompt), dtype=np.int64).astype(np.int32)
 
 
+def write_model_dir(wl: DecoderWorkload, seed: int, path: str, num_layers: Optional[int] = None,
+                    architecture: str = "olmoe") -> dict:
+    """Writes a converted model directory of the seeded synthetic model in the
+    format scripts/extract_olmoe.py produces (:216-266, :268-345):
+    model_weights.bin (tensors in sorted-name order, each 4-byte aligned) +
+    model_weights.json ({name: {offset, shape, dtype}}) and
+    packed_experts/layer_NN.bin.  Norm vectors are written as f32 (the
+    converter keeps f32 sources as f32), the q/k norms at their Hugging Face
+    length (q_dim / kv_dim) with the first head_dim values the decoder uses,
+    the router under the reference's key for `architecture`.  Returns the
+    manifest."""
+    import json
+
+    from . import _lib as L
+    L_ = int(num_layers or wl.num_layers)
+    shape = wl.moe.shape(L_)
+    os.makedirs(os.path.join(path, "packed_experts"), exist_ok=True)
+    for layer in range(L_):
+        layer_image(shape, seed, layer).tofile(
+            os.path.join(path, "packed_experts", f"layer_{layer:02d}.bin"))
+    qd, kvd, hd = wl.num_heads * wl.head_dim, wl.num_kv_heads * wl.head_dim, wl.head_dim
+    tensors = {}
+
+    def as_f32(bits):
+        return bf16_to_f32(bits)
+
+    tensors["model.embed_tokens.weight"] = dense_weight(wl, seed, L.W_EMBED, 0)
+    tensors["lm_head.weight"] = dense_weight(wl, seed, L.W_LM_HEAD, 0)
+    tensors["model.norm.weight"] = as_f32(dense_weight(wl, seed, L.W_FINAL_NORM, 0))
+    gate = "block_sparse_moe.gate" if architecture == "mixtral" else "mlp.gate"
+    for layer in range(L_):
+        pre = f"model.layers.{layer}."
+        tensors[pre + "input_layernorm.weight"] = as_f32(dense_weight(wl, seed, L.W_IN_NORM, layer))
+        tensors[pre + "post_attention_layernorm.weight"] = as_f32(
+            dense_weight(wl, seed, L.W_POST_NORM, layer))
+        tensors[pre + "self_attn.q_proj.weight"] = dense_weight(wl, seed, L.W_Q, layer)
+        tensors[pre + "self_attn.k_proj.weight"] = dense_weight(wl, seed, L.W_K, layer)
+        tensors[pre + "self_attn.v_proj.weight"] = dense_weight(wl, seed, L.W_V, layer)
+        tensors[pre + "self_attn.o_proj.weight"] = dense_weight(wl, seed, L.W_O, layer)
+        if wl.qk_norm:
+            for which, n, name in ((L.W_Q_NORM, qd, "q_norm"), (L.W_K_NORM, kvd, "k_norm")):
+                full = np.concatenate([dense_weight(wl, seed, which, layer),
+                                       f32_to_bf16(normal_f32(seed, _TID_DENSE | (which << 32) |
+                                                              (1 << 31) | layer, n - hd, 0.1) + 1)])
+                tensors[pre + "self_attn." + name + ".weight"] = as_f32(full)
+        tensors[pre + gate + ".weight"] = router(shape, seed, layer)
+    manifest, offset = {}, 0
+    with open(os.path.join(path, "model_weights.bin"), "wb") as f:
+        for name in sorted(tensors):
+            arr = tensors[name]
+            dtype = "bf16" if arr.dtype == np.uint16 else "f32"
+            if offset % 4:
+                f.write(b"\x00" * (4 - offset % 4))
+                offset += 4 - offset % 4
+            manifest[name] = {"offset": offset, "shape": list(arr.shape), "dtype": dtype}
+            raw = np.ascontiguousarray(arr).tobytes()
+            f.write(raw)
+            offset += len(raw)
+    with open(os.path.join(path, "model_weights.json"), "w") as f:
+        json.dump(manifest, f, indent=2)
+    return manifest
+
+
 def bf16_to_f32(a: np.ndarray) -> np.ndarray:
     """Exact bf16 (uint16 bits) -> f32."""
     return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)

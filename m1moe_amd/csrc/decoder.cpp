@@ -192,6 +192,7 @@ int32_t m1moe_attention_decode(m1moe_ctx_t ctx, const float* d_q, const float* d
     a.hpkv = num_heads / num_kv_heads;
     a.head_dim = head_dim;
     a.qh = attention_qh(a.hpkv);
+    a.chunk = attention_chunk(seq_len);
     a.scale = 1.0f / sqrtf((float)head_dim);
     return launched(launch_attention(a, ctx->stream), "attention");
 }
@@ -362,6 +363,7 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
     at.hpkv = dec->sh.num_heads / dec->sh.num_kv_heads;
     at.head_dim = hd;
     at.qh = attention_qh(at.hpkv);
+    at.chunk = attention_chunk(dec->sh.max_seq);
     at.scale = 1.0f / sqrtf((float)hd);
     at.rope_theta = dec->sh.rope_theta;
     at.eps = eps;

@@ -359,26 +359,28 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
 // ---- attention --------------------------------------------------------------------------
 
 // Workgroup (g, c): q heads g*QH .. g*QH+QH-1 (one kv head), positions
-// 64c .. 64c+63.  Lanes take 8 dims of one position each (HD/8 lanes per
-// position), so every K or V row is one coalesced read shared by the QH
-// heads.
+// c*a.chunk .. (c+1)*a.chunk - 1, walked 64 at a time with a running max
+// and sum (the softmax of attnSoftmax, Shaders.metal:245-289, in pieces).
+// Lanes take 8 dims of one position each (HD/8 lanes per position), so every
+// K or V row is one coalesced read shared by the QH heads.
 template <int HD, int QH>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int LP = HD / 8;                 // lanes per position
     constexpr int PPI = 64 / LP;               // positions per wave and iteration
-    constexpr int PW = kAttnChunk / 4;         // positions per wave
+    constexpr int PW = kAttnChunk / 4;         // positions per wave per sub-chunk
     constexpr int IT = PW / PPI;               // iterations
     constexpr int HALF = HD / 2;
     __shared__ __attribute__((aligned(16))) float s_q[QH][HD];
     __shared__ __attribute__((aligned(16))) float s_kv[2][HD];
     __shared__ float s_p[QH][kAttnChunk];
     __shared__ __attribute__((aligned(16))) float s_acc[4][QH][HD];
-    __shared__ float s_m[QH], s_l[QH];
-    __shared__ float s_cf[kAttnMaxChunks];  // merge: chunk maxima, then weights
+    __shared__ float s_m[QH], s_l[QH], s_f[QH];
+    __shared__ float s_st[2][QH][kAttnMaxChunks];  // merge: chunk max and sum
     __shared__ int s_flag;
 
     const int g = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lp = lane % LP, pg = lane / LP;
     const int h0 = g * QH, kvh = h0 / a.hpkv;
     const size_t kvd = (size_t)a.num_kv_heads * HD;
     int p = -1, seq;
@@ -394,35 +396,37 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         seq = a.seq_len;
     }
     const bool has_new = a.fused && p < a.max_seq;  // row p comes from k_new / v_new
-    const int p0 = c * kAttnChunk;
+    const int c0 = c * a.chunk, c1 = min(c0 + a.chunk, seq);
+    const int nact = min(nch, (seq + a.chunk - 1) / a.chunk);  // workgroups with positions
     float* part = a.partial + ((size_t)g * nch + c) * QH * (HD + 2);
 
-    const int nact = min(nch, (seq + kAttnChunk - 1) / kAttnChunk);  // chunks with positions
-    if (p0 < seq) {
-        // this lane's K and V rows: 8 dims of position p0 + wave*PW + it*PPI + pg;
-        // the cache rows are loaded first, row p (the current token's, not yet
-        // in the cache) is taken from LDS once it is prepared
-        const int lp = lane % LP, pg = lane / LP;
+    if (c0 < seq) {
+        // this lane's K and V rows of a 64-position sub-chunk (row p, not yet
+        // in the cache, comes from LDS once it is prepared)
         float kr[IT][8], vr[IT][8];
+        auto load_rows = [&](int p0) {
 #pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const int pp = p0 + wave * PW + it * PPI + pg;
-            float4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, v0 = k0, v1 = k0;
-            if (pp < seq && !(has_new && pp == p)) {
-                const size_t off = (size_t)pp * kvd + (size_t)kvh * HD + 8 * lp;
-                k0 = *reinterpret_cast<const float4*>(a.kcache + off);
-                k1 = *reinterpret_cast<const float4*>(a.kcache + off + 4);
-                v0 = *reinterpret_cast<const float4*>(a.vcache + off);
-                v1 = *reinterpret_cast<const float4*>(a.vcache + off + 4);
+            for (int it = 0; it < IT; ++it) {
+                const int pp = p0 + wave * PW + it * PPI + pg;
+                float4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, v0 = k0, v1 = k0;
+                if (pp < c1 && !(has_new && pp == p)) {
+                    const size_t off = (size_t)pp * kvd + (size_t)kvh * HD + 8 * lp;
+                    k0 = *reinterpret_cast<const float4*>(a.kcache + off);
+                    k1 = *reinterpret_cast<const float4*>(a.kcache + off + 4);
+                    v0 = *reinterpret_cast<const float4*>(a.vcache + off);
+                    v1 = *reinterpret_cast<const float4*>(a.vcache + off + 4);
+                }
+                kr[it][0] = k0.x, kr[it][1] = k0.y, kr[it][2] = k0.z, kr[it][3] = k0.w;
+                kr[it][4] = k1.x, kr[it][5] = k1.y, kr[it][6] = k1.z, kr[it][7] = k1.w;
+                vr[it][0] = v0.x, vr[it][1] = v0.y, vr[it][2] = v0.z, vr[it][3] = v0.w;
+                vr[it][4] = v1.x, vr[it][5] = v1.y, vr[it][6] = v1.z, vr[it][7] = v1.w;
             }
-            kr[it][0] = k0.x, kr[it][1] = k0.y, kr[it][2] = k0.z, kr[it][3] = k0.w;
-            kr[it][4] = k1.x, kr[it][5] = k1.y, kr[it][6] = k1.z, kr[it][7] = k1.w;
-            vr[it][0] = v0.x, vr[it][1] = v0.y, vr[it][2] = v0.z, vr[it][3] = v0.w;
-            vr[it][4] = v1.x, vr[it][5] = v1.y, vr[it][6] = v1.z, vr[it][7] = v1.w;
-        }
-        // q heads (and the new k when this chunk holds row p): per-head
+        };
+        load_rows(c0);
+
+        // q heads (and the new k when this workgroup holds row p): per-head
         // RMSNorm (InferenceEngine.swift:538-548), then RoPE (:521-536)
-        const bool mine_new = has_new && p >= p0 && p < p0 + kAttnChunk;
+        const bool mine_new = has_new && p >= c0 && p < c1;
         const int items = QH + (mine_new ? 1 : 0);
         for (int it = wave; it < items; it += 4) {
             const bool is_k = it == QH;
@@ -467,19 +471,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 }
             }
         }
-
-        if (mine_new) {
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                if (p0 + wave * PW + it * PPI + pg != p) continue;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    kr[it][e] = s_kv[0][8 * lp + e];
-                    vr[it][e] = s_kv[1][8 * lp + e];
-                }
-            }
-        }
-        // scores (attnScores, Shaders.metal:209-243)
         float qv[QH][8];
 #pragma unroll
         for (int i = 0; i < QH; ++i) {
@@ -488,7 +479,29 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             qv[i][0] = q0.x, qv[i][1] = q0.y, qv[i][2] = q0.z, qv[i][3] = q0.w;
             qv[i][4] = q1.x, qv[i][5] = q1.y, qv[i][6] = q1.z, qv[i][7] = q1.w;
         }
-        {
+        float acc[QH][8];
+#pragma unroll
+        for (int i = 0; i < QH; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+        if (tid < QH) {
+            s_m[tid] = -INFINITY;
+            s_l[tid] = 0.f;
+        }
+
+        for (int p0 = c0; p0 < c1; p0 += kAttnChunk) {
+            if (mine_new && p >= p0 && p < p0 + kAttnChunk) {
+#pragma unroll
+                for (int it = 0; it < IT; ++it) {
+                    if (p0 + wave * PW + it * PPI + pg != p) continue;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        kr[it][e] = s_kv[0][8 * lp + e];
+                        vr[it][e] = s_kv[1][8 * lp + e];
+                    }
+                }
+            }
+            // scores (attnScores, Shaders.metal:209-243)
 #pragma unroll
             for (int it = 0; it < IT; ++it) {
                 const int pl = wave * PW + it * PPI + pg;
@@ -499,31 +512,33 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     for (int e = 0; e < 8; ++e) d = fmaf(qv[i][e], kr[it][e], d);
 #pragma unroll
                     for (int o = 1; o < LP; o <<= 1) d += __shfl_xor(d, o);
-                    if (lp == 0) s_p[i][pl] = p0 + pl < seq ? d * a.scale : -INFINITY;
+                    if (lp == 0) s_p[i][pl] = p0 + pl < c1 ? d * a.scale : -INFINITY;
                 }
             }
-        }
-        __syncthreads();
-        // the chunk's softmax numerators (attnSoftmax, :245-289), lane = position
-        for (int i = wave; i < QH; i += 4) {
-            const float s = s_p[i][lane];
-            const float m = wave_max(s);
-            const float e = s == -INFINITY ? 0.f : expf(s - m);
-            const float l = wave_sum(e);
-            s_p[i][lane] = e;
-            if (lane == 0) {
-                s_m[i] = m;
-                s_l[i] = l;
+            __syncthreads();
+            // running max and sum per head; lane = position of the sub-chunk
+            for (int i = wave; i < QH; i += 4) {
+                const float sc = s_p[i][lane];
+                const float m_old = s_m[i];
+                const float m = fmaxf(m_old, wave_max(sc));
+                const float e = sc == -INFINITY ? 0.f : expf(sc - m);
+                const float f = m_old == -INFINITY ? 0.f : expf(m_old - m);
+                const float l = wave_sum(e);
+                s_p[i][lane] = e;
+                if (lane == 0) {
+                    s_m[i] = m;
+                    s_l[i] = fmaf(s_l[i], f, l);
+                    s_f[i] = f;
+                }
             }
-        }
-        __syncthreads();
-        // weighted V sum (attnValues, :291-326)
-        float acc[QH][8];
+            __syncthreads();
+            // weighted V sum (attnValues, :291-326), earlier sub-chunks rescaled
 #pragma unroll
-        for (int i = 0; i < QH; ++i)
+            for (int i = 0; i < QH; ++i) {
+                const float f = s_f[i];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
-        {
+                for (int e = 0; e < 8; ++e) acc[i][e] *= f;
+            }
 #pragma unroll
             for (int it = 0; it < IT; ++it) {
                 const int pl = wave * PW + it * PPI + pg;
@@ -533,6 +548,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[i][e] = fmaf(w, vr[it][e], acc[i][e]);
                 }
+            }
+            if (p0 + kAttnChunk < c1) {
+                __syncthreads();  // s_p is rewritten by the next sub-chunk
+                load_rows(p0 + kAttnChunk);
             }
         }
 #pragma unroll
@@ -552,7 +571,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
         __syncthreads();
         if (nact == 1) {
-            // the only chunk with positions: no merge
+            // the only workgroup with positions: no merge
             for (int t = tid; t < QH * HD; t += 256) {
                 const int i = t / HD, d = t - i * HD;
                 a.out[(size_t)(h0 + i) * HD + d] =
@@ -570,44 +589,36 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             st_coh(part + tid * (HD + 2) + 1, s_l[tid]);
         }
     }
-    if (nact == 1) return;  // (chunks past the sequence are not read by the merge)
+    if (nact == 1) return;  // (workgroups past the sequence are not read by the merge)
 
-    // the last workgroup of the group merges the chunks:
+    // the last workgroup of the group merges the nact partials:
     // out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M)
     if (!last_workgroup(a.counters + g, nch, &s_flag)) return;
     const size_t cstride = (size_t)QH * (HD + 2);
     const float* base = a.partial + (size_t)g * nch * cstride;
-    float* s_red = &s_acc[0][0][0];  // free now
-    for (int i = 0; i < QH; ++i) {
-        const float* pb = base + i * (HD + 2);
-        float mloc = -INFINITY;
-        for (int cc = tid; cc < nact; cc += 256) {
-            const float m = ld_coh(pb + cc * cstride);
-            s_cf[cc] = m;
-            mloc = fmaxf(mloc, m);
-        }
-        const float M = block_max(mloc, s_red, 4);
-        float lloc = 0.f;
-        for (int cc = tid; cc < nact; cc += 256) {
-            const float f = expf(s_cf[cc] - M);
-            lloc = fmaf(ld_coh(pb + cc * cstride + 1), f, lloc);
-            s_cf[cc] = f;
-        }
-        const float inv = 1.0f / block_sum(lloc, s_red, 4);  // (its barriers publish s_cf)
-        for (int d = tid; d < HD; d += 256) {
-            float acc = 0.f;
-            for (int c0 = 0; c0 < nact; c0 += 8) {
-                float t[8];
+    for (int t = tid; t < QH * nact; t += 256) {
+        const int i = t / nact, cc = t - i * nact;
+        s_st[0][i][cc] = ld_coh(base + cc * cstride + i * (HD + 2));
+        s_st[1][i][cc] = ld_coh(base + cc * cstride + i * (HD + 2) + 1);
+    }
+    __syncthreads();
+    for (int t = tid; t < QH * HD; t += 256) {
+        const int i = t / HD, d = t - i * HD;
+        float vals[kAttnMaxChunks];
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    t[j] = c0 + j < nact ? ld_coh(pb + (size_t)(c0 + j) * cstride + 2 + d) : 0.f;
+        for (int cc = 0; cc < kAttnMaxChunks; ++cc)
+            vals[cc] = cc < nact ? ld_coh(base + cc * cstride + i * (HD + 2) + 2 + d) : 0.f;
+        float M = -INFINITY;
+        for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, s_st[0][i][cc]);
+        float L = 0.f, acc = 0.f;
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (c0 + j < nact) acc = fmaf(s_cf[c0 + j], t[j], acc);
-            }
-            a.out[(size_t)(h0 + i) * HD + d] = acc * inv;
+        for (int cc = 0; cc < kAttnMaxChunks; ++cc) {
+            if (cc >= nact) break;
+            const float f = expf(s_st[0][i][cc] - M);
+            L = fmaf(s_st[1][i][cc], f, L);
+            acc = fmaf(vals[cc], f, acc);
         }
-        __syncthreads();  // s_cf is rewritten for the next head
+        a.out[(size_t)(h0 + i) * HD + d] = acc / L;
     }
     if (tid == 0) reset_counter(a.counters + g);
 }
@@ -705,15 +716,21 @@ int attention_qh(int hpkv) {
     return 1;
 }
 
+int attention_chunk(int max_positions) {
+    const int sub = (max_positions + kAttnChunk - 1) / kAttnChunk;  // 64-position sub-chunks
+    return kAttnChunk * ((sub + kAttnMaxChunks - 1) / kAttnMaxChunks);
+}
+
 int attention_partial_floats(int num_heads, int head_dim, int max_positions) {
-    return num_heads * ((max_positions + kAttnChunk - 1) / kAttnChunk) * (head_dim + 2);
+    const int chunk = attention_chunk(max_positions);
+    return num_heads * ((max_positions + chunk - 1) / chunk) * (head_dim + 2);
 }
 
 int launch_attention(const AttnArgs& a, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (a.qh <= 0 || a.num_heads % a.qh || a.hpkv % a.qh) return (int)hipErrorInvalidValue;
-    const dim3 grid((unsigned)(a.num_heads / a.qh),
-                    (unsigned)((a.max_seq + kAttnChunk - 1) / kAttnChunk));
+    if (a.qh <= 0 || a.num_heads % a.qh || a.hpkv % a.qh || a.chunk != attention_chunk(a.max_seq))
+        return (int)hipErrorInvalidValue;
+    const dim3 grid((unsigned)(a.num_heads / a.qh), (unsigned)((a.max_seq + a.chunk - 1) / a.chunk));
     switch (a.head_dim) {
         case 64: return launch_attn_hd<64>(a, grid, st);
         case 128: return launch_attn_hd<128>(a, grid, st);

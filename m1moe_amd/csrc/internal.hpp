@@ -181,7 +181,9 @@ struct MvArgs {
 };
 
 // Decode attention of one query position.  Workgroup (g, c): q heads
-// g*qh .. g*qh+qh-1 (one kv head) over positions 64c .. 64c+63.
+// g*qh .. g*qh+qh-1 (one kv head) over positions c*chunk .. (c+1)*chunk - 1
+// (chunk = attention_chunk(max_seq): a multiple of 64, at most
+// kAttnMaxChunks workgroups per kv head).
 //   fused = 1: q, k_new, v_new are the raw projections of the current token;
 //     q and k get the per-head RMSNorm (q_norm/k_norm non-null) and RoPE at
 //     p = *pos, the new k/v row is stored at cache row p (flag 32 and no
@@ -206,12 +208,13 @@ struct AttnArgs {
     int32_t seq_len;             // fused = 0
     int32_t max_seq;             // cache rows (fused) / seq_len
     int32_t num_heads, num_kv_heads, hpkv, head_dim, qh;
+    int32_t chunk;               // positions per workgroup
     float scale, rope_theta, eps;
 };
 
 constexpr int kAttnChunk = 64;   // positions per attention workgroup
 constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
-constexpr int kAttnMaxChunks = 1024;  // 65536 positions
+constexpr int kAttnMaxChunks = 16;   // workgroups per kv head
 constexpr int kMvStageMax = 8192;   // largest staged (normalised / embedded) input, floats
 
 int launch_set_i32(int32_t* p, int32_t v, void* stream);
@@ -221,6 +224,8 @@ int matvec_workgroups(int rows);
 int launch_matvec_bf16(const MvArgs& a, void* stream);
 // q heads per attention workgroup (0: unsupported hpkv).
 int attention_qh(int hpkv);
+// Positions per attention workgroup for a cache of max_positions.
+int attention_chunk(int max_positions);
 int attention_partial_floats(int num_heads, int head_dim, int max_positions);
 int launch_attention(const AttnArgs& a, void* stream);
 // Greedy token of x[0..n) to *out (ties to the lower index; x[0] NaN gives 0).

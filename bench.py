@@ -263,9 +263,10 @@ def decoder_step_bytes(wl, eb: int, pos: int) -> int:
 
 def bench_decoder(args, m, synth) -> int:
     """cfg1 / cfg4: the whole decoder (Decoder, m1moe_dec_*), seeded random
-    weights, a random prompt forwarded token by token then greedy steps
-    (Sources/bench/main.swift:136-163).  One HIP graph holds one
-    sequence-mode step; a job replays it prompt + gen times after a reset."""
+    weights, a random prompt then greedy steps (Sources/bench/main.swift:
+    136-163; the reference forwards the prompt token by token, here it goes
+    through m1moe_dec_prefill in one batch per layer).  One HIP graph holds
+    one sequence-mode step, replayed once per greedy token."""
     from m1moe_amd import _lib
     from m1moe_amd.decoder import Decoder
     from oracle import oracle as orc
@@ -340,8 +341,21 @@ def bench_decoder(args, m, synth) -> int:
     cap = P + G + 1
     seq = ctx.alloc(4 * cap)
     init = np.concatenate([prompt, np.zeros(cap - P, np.int32)])
-    # eager sequence-mode run: the reference tokens for the graph replays
-    want = dec.generate(prompt, G)
+    dprompt = ctx.to_device(prompt)
+
+    def prefill():
+        # the prompt in one batch per layer; its greedy token lands at seq[P]
+        dec.prefill_device(dprompt, P, seq.addr + 4 * P)
+
+    # eager run (batched prefill, then sequence-mode steps): the reference
+    # tokens for the graph replays; it also grows the prefill scratch
+    seq.upload(init)
+    dec.reset()
+    prefill()
+    for _ in range(G):
+        dec.step_seq(seq, P, cap)
+    ctx.sync()
+    want = seq.download(np.int32)[P:]
     if args.eager:
         class _Eager:
             @staticmethod
@@ -360,8 +374,7 @@ def bench_decoder(args, m, synth) -> int:
         dec.reset()
         ctx.sync()
         ev[0].record()
-        for _ in range(P):
-            graph.launch()
+        prefill()
         ev[1].record()
         for _ in range(G):
             graph.launch()
@@ -394,7 +407,8 @@ def bench_decoder(args, m, synth) -> int:
                    "num_kv_heads": wl.num_kv_heads, "head_dim": wl.head_dim,
                    "num_experts": shape.num_experts, "top_k": shape.top_k,
                    "intermediate": shape.intermediate, "prompt_tokens": P, "gen_tokens": G,
-                   "step": "one job = reset + prompt + greedy steps, each token one " +
+                   "step": "one job = reset, the prompt in one batch per layer "
+                           "(m1moe_dec_prefill), then each greedy token one " +
                            ("host launch of its kernels" if args.eager else
                             "replay of a one-step HIP graph"),
                    "prefill_tok_s": round(pre_tok_s, 2)},

@@ -335,6 +335,19 @@ int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in,
  * flag (as a token outside the vocabulary). */
 int32_t m1moe_dec_step_seq(m1moe_dec_t dec, int32_t* d_seq, int32_t n_prompt,
                            int32_t seq_cap, float* d_logits);
+/* The prompt at once: the T tokens d_tokens (int32 device) at positions
+ * pos .. pos + T - 1 through every layer in one batch per layer (the
+ * reference forwards a prompt token by token, Sources/bench/main.swift:
+ * 139-141): q/k/v and o_proj as f32 GEMMs over the T rows, causal attention,
+ * the MoE block through the grouped prefill (m1moe_moe_prefill; its f16
+ * activations make this path agree with T m1moe_dec_step calls to ~1e-3).
+ * Their K/V rows enter the cache, the position advances by T, d_token_out
+ * receives the greedy token after the last one and d_logits (nullable) its
+ * logits.  1 <= T <= min(max_seq, 4096); positions past max_seq set the
+ * device error flag.  The first call with a larger T than any before grows
+ * the scratch (make it before capturing a graph). */
+int32_t m1moe_dec_prefill(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
+                          int32_t* d_token_out, float* d_logits);
 /* The current position (waits for the context stream). */
 int32_t m1moe_dec_position(m1moe_dec_t dec, int32_t* pos);
 

@@ -124,6 +124,7 @@ _PROTOTYPES = [
     ("m1moe_dec_reset", c_int32, [c_void_p]),
     ("m1moe_dec_step", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
     ("m1moe_dec_step_seq", c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    ("m1moe_dec_prefill", c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     ("m1moe_dec_position", c_int32, [c_void_p, POINTER(c_int32)]),
     ("m1moe_store_open", c_int32, [c_char_p, c_char_p, POINTER(c_void_p)]),
     ("m1moe_store_close", None, [c_void_p]),

@@ -69,6 +69,9 @@ struct m1moe_dec {
     float *res = nullptr, *res2 = nullptr;
     float *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float *logits = nullptr, *part = nullptr;
+    // prefill scratch for up to pf_cap tokens (grown on demand)
+    int32_t pf_cap = 0;
+    float *pf_res = nullptr, *pf_res2 = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr;
     uint32_t* cnt = nullptr;   // [2 + num_heads]: (unused), lm_head, attention groups
     float* ssq = nullptr;      // o_proj's per-workgroup sums of squares
     float* am_val = nullptr;   // lm_head's per-workgroup best logit
@@ -212,6 +215,9 @@ void m1moe_dec_destroy(m1moe_dec_t dec) {
     if (!dec) return;
     (void)hipSetDevice(dec->device);
     for (void* p : dec->allocs) (void)hipFree(p);
+    for (void* p : {(void*)dec->pf_res, (void*)dec->pf_res2, (void*)dec->pf_xn, (void*)dec->pf_qkv,
+                    (void*)dec->pf_attn})
+        if (p) (void)hipFree(p);
     delete dec;
 }
 
@@ -324,13 +330,8 @@ int32_t m1moe_dec_position(m1moe_dec_t dec, int32_t* pos) {
 
 namespace {
 
-// One step; seq_cap == 0: token from *tok_in, greedy token to *tok_out;
-// seq_cap > 0: sequence mode over tok_out[0 .. seq_cap) (tok_in == tok_out).
-int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32_t n_prompt,
-                 int32_t seq_cap, float* d_logits) {
-    int32_t rc;
-    if (!dec) return fail(M1MOE_ERR_INVALID, "null decoder");
-    if ((rc = check_dev_ptr(d_logits, "d_logits", true))) return rc;
+// Every dense tensor of the decoder and every MoE layer of its context uploaded.
+int32_t check_loaded(const m1moe_dec* dec) {
     const bool needs_qk = dec->sh.qk_norm != 0;
     for (int w = 0; w < kNumW; ++w) {
         if (!needs_qk && (w == M1MOE_W_Q_NORM || w == M1MOE_W_K_NORM)) continue;
@@ -338,10 +339,21 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
             if (!dec->loaded[(size_t)w * dec->L + l])
                 return fail(M1MOE_ERR_INVALID, "tensor %d of layer %d was not uploaded", w, l);
     }
-    m1moe_ctx_t ctx = dec->moe;
     for (int l = 0; l < dec->L; ++l)
-        if (!ctx->layer_loaded[l] || !ctx->router_loaded[l])
+        if (!dec->moe->layer_loaded[l] || !dec->moe->router_loaded[l])
             return fail(M1MOE_ERR_INVALID, "MoE layer %d was not uploaded", l);
+    return M1MOE_OK;
+}
+
+// One step; seq_cap == 0: token from *tok_in, greedy token to *tok_out;
+// seq_cap > 0: sequence mode over tok_out[0 .. seq_cap) (tok_in == tok_out).
+int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32_t n_prompt,
+                 int32_t seq_cap, float* d_logits) {
+    int32_t rc;
+    if (!dec) return fail(M1MOE_ERR_INVALID, "null decoder");
+    if ((rc = check_dev_ptr(d_logits, "d_logits", true))) return rc;
+    if ((rc = check_loaded(dec))) return rc;
+    m1moe_ctx_t ctx = dec->moe;
     if ((rc = set_device(ctx))) return rc;
     void* st = ctx->stream;
     const int32_t h = dec->h, qd = dec->qd, kvd = dec->kvd, V = dec->sh.vocab, hd = dec->sh.head_dim;
@@ -446,6 +458,126 @@ int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in, int32_t* d_to
     if (!aligned_i32(d_token_in) || !aligned_i32(d_token_out))
         return fail(M1MOE_ERR_INVALID, "d_token_in / d_token_out must be 4-byte aligned device pointers");
     return dec_step(dec, d_token_in, d_token_out, 0, 0, d_logits);
+}
+
+int32_t m1moe_dec_prefill(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T, int32_t* d_token_out,
+                          float* d_logits) {
+    int32_t rc;
+    if (!dec) return fail(M1MOE_ERR_INVALID, "null decoder");
+    if (!aligned_i32(d_tokens) || !aligned_i32(d_token_out))
+        return fail(M1MOE_ERR_INVALID, "d_tokens / d_token_out must be 4-byte aligned device pointers");
+    if ((rc = check_dev_ptr(d_logits, "d_logits", true))) return rc;
+    if (T < 1 || T > dec->sh.max_seq || T > 4096)
+        return fail(M1MOE_ERR_INVALID, "T=%d must be in [1, min(max_seq=%d, 4096)]", T, dec->sh.max_seq);
+    if ((rc = check_loaded(dec))) return rc;
+    m1moe_ctx_t ctx = dec->moe;
+    if ((rc = set_device(ctx))) return rc;
+    const int32_t h = dec->h, qd = dec->qd, kvd = dec->kvd, hd = dec->sh.head_dim;
+    const int32_t N = qd + 2 * kvd;
+    if (T > dec->pf_cap) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        for (float** b : {&dec->pf_res, &dec->pf_res2, &dec->pf_xn, &dec->pf_qkv, &dec->pf_attn}) {
+            if (*b) (void)hipFree(*b);
+            *b = nullptr;
+        }
+        dec->pf_cap = 0;
+        const uint64_t t = (uint64_t)T;
+        if ((rc = device_alloc((void**)&dec->pf_res, t * h * 4, "prefill residual")) ||
+            (rc = device_alloc((void**)&dec->pf_res2, t * h * 4, "prefill residual 2")) ||
+            (rc = device_alloc((void**)&dec->pf_xn, t * h * 4, "prefill normed rows")) ||
+            (rc = device_alloc((void**)&dec->pf_qkv, t * N * 4, "prefill q/k/v")) ||
+            (rc = device_alloc((void**)&dec->pf_attn, t * qd * 4, "prefill attention")))
+            return rc;
+        dec->pf_cap = T;
+    }
+    void* st = ctx->stream;
+    const float eps = dec->sh.rms_eps;
+    const bool qk = dec->sh.qk_norm != 0;
+    PfDenseArgs a{};
+    a.tokens = d_tokens;
+    a.embed = dec->embed;
+    a.res = dec->pf_res;
+    a.qkv = dec->pf_qkv;
+    a.attn = dec->pf_attn;
+    a.pos = dec->pos;
+    a.err = ctx->err;
+    a.T = T;
+    a.vocab = dec->sh.vocab;
+    a.h = h;
+    a.ldqkv = N;
+    a.qd = qd;
+    a.kvd = kvd;
+    a.num_heads = dec->sh.num_heads;
+    a.num_kv_heads = dec->sh.num_kv_heads;
+    a.hpkv = dec->sh.num_heads / dec->sh.num_kv_heads;
+    a.head_dim = hd;
+    a.max_seq = dec->sh.max_seq;
+    a.scale = 1.0f / sqrtf((float)hd);
+    a.rope_theta = dec->sh.rope_theta;
+    a.eps = eps;
+    auto gemm = [&](const float* A, int lda, const uint16_t* W, const float* R, float* C, int ldc, int n,
+                    int k, const char* what) {
+        GemmArgs g{};
+        g.A = A;
+        g.lda = lda;
+        g.W = W;
+        g.R = R;
+        g.C = C;
+        g.ldc = ldc;
+        g.M = T;
+        g.N = n;
+        g.K = k;
+        return launched(launch_gemm(g, st), what);
+    };
+    if ((rc = launched(launch_pf_embed(a, st), "prefill embedding"))) return rc;  // :129-131
+    const uint64_t cache_layer = (uint64_t)dec->sh.max_seq * kvd;
+    for (int l = 0; l < dec->L; ++l) {
+        // input RMSNorm, q/k/v for all T tokens (InferenceEngine.swift:177-192)
+        if ((rc = launched(launch_rmsnorm_rows(dec->pf_res, dec->in_norm + (size_t)l * h, dec->pf_xn, T, h,
+                                               eps, st),
+                           "prefill input norm")) ||
+            (rc = gemm(dec->pf_xn, h, dec->wq + (size_t)l * qd * h, nullptr, dec->pf_qkv, N, qd, h, "prefill q")) ||
+            (rc = gemm(dec->pf_xn, h, dec->wk + (size_t)l * kvd * h, nullptr, dec->pf_qkv + qd, N, kvd, h,
+                       "prefill k")) ||
+            (rc = gemm(dec->pf_xn, h, dec->wv + (size_t)l * kvd * h, nullptr, dec->pf_qkv + qd + kvd, N, kvd, h,
+                       "prefill v")))
+            return rc;
+        // q/k norms, RoPE, KV rows (:194-220); causal attention (:226)
+        a.q_norm = qk ? dec->q_norm + (size_t)l * hd : nullptr;
+        a.k_norm = qk ? dec->k_norm + (size_t)l * hd : nullptr;
+        a.kcache = dec->kcache + l * cache_layer;
+        a.vcache = dec->vcache + l * cache_layer;
+        if ((rc = launched(launch_pf_rope_kv(a, st), "prefill rope / kv rows")) ||
+            (rc = launched(launch_pf_attention(a, st), "prefill attention")))
+            return rc;
+        // o_proj + residual (:227-233), post-attention RMSNorm (:234-236)
+        if ((rc = gemm(dec->pf_attn, qd, dec->wo + (size_t)l * h * qd, dec->pf_res, dec->pf_res2, h, h, qd,
+                       "prefill o_proj")) ||
+            (rc = launched(launch_rmsnorm_rows(dec->pf_res2, dec->post_norm + (size_t)l * h, dec->pf_xn, T, h,
+                                               eps, st),
+                           "prefill post-attention norm")))
+            return rc;
+        // the MoE block for the T tokens, its output the next residual (:240-266)
+        if ((rc = m1moe_moe_prefill(ctx, l, T, dec->pf_xn, M1MOE_F32, dec->pf_res2, dec->pf_res, nullptr,
+                                    nullptr)))
+            return rc;
+    }
+    // the position moves past the prompt; the last token's final norm, lm_head
+    // and greedy token advance it by the last one (:138-155)
+    if ((rc = launched(launch_advance_pos(dec->pos, T - 1, dec->sh.max_seq, st), "prefill position")))
+        return rc;
+    MvArgs f = mv_one(dec->lm_head, dec->pf_res + (size_t)(T - 1) * h, nullptr,
+                      d_logits ? d_logits : dec->logits, dec->sh.vocab, h);
+    f.norm_w = dec->final_norm;
+    f.eps = eps;
+    f.counter = dec->cnt + 1;
+    f.am_val = dec->am_val;
+    f.am_idx = dec->am_idx;
+    f.tok_out = d_token_out;
+    f.pos = dec->pos;
+    f.max_seq = dec->sh.max_seq;
+    f.err = ctx->err;
+    return launched(launch_matvec_bf16(f, st), "prefill lm_head");
 }
 
 int32_t m1moe_dec_step_seq(m1moe_dec_t dec, int32_t* d_seq, int32_t n_prompt, int32_t seq_cap,

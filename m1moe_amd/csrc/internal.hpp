@@ -217,6 +217,46 @@ constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
 constexpr int kAttnMaxChunks = 16;   // workgroups per kv head
 constexpr int kMvStageMax = 8192;   // largest staged (normalised / embedded) input, floats
 
+// ---- decoder prefill (prefill_dense.hip) ----
+
+// C[M][N] = A[M][K] W[N][K]^T (+ R[M][N]); A f32 (row stride lda, lda % 4 ==
+// 0), W bf16 row-major, C and R with row stride ldc; K % 32 == 0.
+struct GemmArgs {
+    const float* A;
+    int32_t lda;
+    const uint16_t* W;
+    const float* R;
+    float* C;
+    int32_t ldc;
+    int32_t M, N, K;
+};
+
+// The T prompt tokens of a decoder prefill at positions *pos .. *pos + T - 1.
+struct PfDenseArgs {
+    const int32_t* tokens;       // [T]
+    const uint16_t* embed;       // [vocab][h]
+    float* res;                  // [T][h] residual stream
+    float* qkv;                  // [T][ldqkv]: q | k | v
+    float* attn;                 // [T][qd]
+    const uint16_t* q_norm;      // [head_dim] or null
+    const uint16_t* k_norm;
+    float* kcache;               // this layer's [max_seq][kvd]
+    float* vcache;
+    const int32_t* pos;
+    uint32_t* err;
+    int32_t T, vocab, h, ldqkv, qd, kvd;
+    int32_t num_heads, num_kv_heads, hpkv, head_dim, max_seq;
+    float scale, rope_theta, eps;
+};
+
+int launch_pf_embed(const PfDenseArgs& a, void* stream);
+int launch_rmsnorm_rows(const float* x, const uint16_t* w, float* out, int rows, int n, float eps,
+                        void* stream);
+int launch_gemm(const GemmArgs& g, void* stream);
+int launch_pf_rope_kv(const PfDenseArgs& a, void* stream);
+int launch_pf_attention(const PfDenseArgs& a, void* stream);
+int launch_advance_pos(int32_t* pos, int32_t by, int32_t max_seq, void* stream);
+
 int launch_set_i32(int32_t* p, int32_t v, void* stream);
 int launch_rmsnorm(const float* x, const uint16_t* w, float* out, int n, float eps, void* stream);
 // Workgroups of a matvec launch (the size of am_val / am_idx).

@@ -205,6 +205,25 @@ class Decoder:
         check(self.lib.m1moe_dec_step_seq(self.handle, _ptr(seq), int(n_prompt), int(seq_cap),
                                           _ptr(logits)), "m1moe_dec_step_seq")
 
+    def prefill_device(self, tokens, T: int, token_out, logits=None) -> None:
+        """The T prompt tokens (device int32) through the decoder in one batch
+        per layer (asynchronous); token_out receives the greedy next token."""
+        check(self.lib.m1moe_dec_prefill(self.handle, _ptr(tokens), int(T), _ptr(token_out),
+                                         _ptr(logits)), "m1moe_dec_prefill")
+
+    def prefill(self, prompt, return_logits: bool = False):
+        """The prompt at once from the current position; returns the greedy
+        token after its last token (and that token's logits when asked)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        d = self.ctx.to_device(prompt)
+        self.prefill_device(d, prompt.size, self._tok, self._logits)
+        self.ctx.sync()
+        d.free()
+        nxt = int(self._tok.download(np.int32, 1)[0])
+        if return_logits:
+            return nxt, self._logits.download(np.float32, self.shape.vocab)
+        return nxt
+
     def generate(self, prompt, n_gen: int):
         """Sources/bench/main.swift:136-163 at temperature 0: the prompt
         forwarded token by token, then n_gen greedy steps; returns the

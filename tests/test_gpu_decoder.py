@@ -307,6 +307,78 @@ def test_decoder_dense_only_is_tight():
         p.close()
 
 
+def _zero_experts(p):
+    zero = np.zeros_like(p.orc.images[0])
+    for l in range(p.orc.L):
+        p.ctx.upload_layer_experts(l, zero)
+        p.orc.images[l] = zero
+
+
+@pytest.mark.parametrize("Ts", [(1,), (17,), (130,), (5, 7)])
+def test_prefill_dense_path_is_tight(Ts):
+    """Batched prefill with the MoE block zeroed (it then adds only the
+    residual): the f32 GEMMs, causal attention, RoPE and KV rows against the
+    oracle's token-by-token run, logits of each prefill's last token to
+    relative L2 1e-5, then a greedy step from the prefilled cache."""
+    wl = synth.DECODERS["tiny_dec"]
+    p = Pair(wl, seed=31, max_seq=160)
+    try:
+        _zero_experts(p)
+        toks = synth.prompt_tokens(wl, 12, sum(Ts))
+        off = 0
+        for T in Ts:
+            say(f"prefill T={T} at position {off}")
+            g_tok, g_lg = p.dec.prefill(toks[off:off + T], return_logits=True)
+            for t in toks[off:off + T]:
+                w_tok, w_lg = p.orc.step(int(t))
+            off += T
+            rel = rel_l2(g_lg, w_lg)
+            assert rel < 1e-5, f"T={T}: rel L2 {rel:.2e}"
+            assert g_tok == w_tok or np.ptp(np.sort(w_lg)[-2:]) < 1e-4
+            assert p.dec.position() == off
+        g_tok, g_lg = p.dec.forward(int(toks[0]), return_logits=True)
+        w_tok, w_lg = p.orc.step(int(toks[0]))
+        assert rel_l2(g_lg, w_lg) < 1e-5
+    finally:
+        p.close()
+
+
+def test_prefill_whole_decoder_then_greedy():
+    """The whole decoder (MoE prefill included): the prompt's last logits and
+    the greedy steps after it against the oracle at the decoder bar."""
+    wl = synth.DECODERS["tiny_dec"]
+    p = Pair(wl, seed=32, max_seq=80)
+    try:
+        prompt = synth.prompt_tokens(wl, 13, 48)
+        say("prefill 48 + 8 greedy")
+        tok, g_lg = p.dec.prefill(prompt, return_logits=True)
+        for t in prompt:
+            w_tok, w_lg = p.orc.step(int(t))
+        check_step(tok, g_lg, w_tok, w_lg, "prefill")
+        for i in range(8):
+            feed = w_tok  # the oracle's token, so both see the same sequence
+            g_tok, g_lg = p.dec.forward(int(feed), return_logits=True)
+            w_tok, w_lg = p.orc.step(int(feed))
+            check_step(g_tok, g_lg, w_tok, w_lg, f"greedy {i}")
+    finally:
+        p.close()
+
+
+def test_prefill_past_the_cache_is_reported():
+    wl = synth.DECODERS["tiny_dec"]
+    p = Pair(wl, seed=33, max_seq=10)
+    try:
+        p.dec.prefill(synth.prompt_tokens(wl, 3, 6))
+        say("prefill past max_seq")
+        with pytest.raises(m.M1MoEError, match="KV cache full"):
+            p.dec.prefill(synth.prompt_tokens(wl, 4, 6))
+        p.dec.reset()
+        p.dec.prefill(synth.prompt_tokens(wl, 3, 10))  # exactly full is fine
+        assert p.dec.position() == 10
+    finally:
+        p.close()
+
+
 def test_decoder_olmoe_dims_two_layers():
     """Full OLMoE widths (h 2048, 16x128 heads, vocab 50304, 64 experts top-8),
     two layers, four prompt tokens and four greedy steps."""
@@ -324,6 +396,14 @@ def test_decoder_olmoe_dims_two_layers():
             w_tok, w_lg = p.orc.step(tok)
             check_step(g_tok, g_lg, w_tok, w_lg, f"greedy {i}")
             tok = w_tok
+        # the same prompt through the batched prefill
+        p.dec.reset()
+        p.orc.reset()
+        say("olmoe-width prefill of 8")
+        tok, g_lg = p.dec.prefill(synth.prompt_tokens(p.wl, 7, 8), return_logits=True)
+        for t in synth.prompt_tokens(p.wl, 7, 8):
+            w_tok, w_lg = p.orc.step(int(t))
+        check_step(tok, g_lg, w_tok, w_lg, "prefill")
     finally:
         p.close()
 

@@ -24,6 +24,7 @@ from . import _lib
 from ._lib import (DecShape, W_EMBED, W_FINAL_NORM, W_IN_NORM, W_K, W_K_NORM, W_LM_HEAD, W_O,
                    W_PER_LAYER, W_POST_NORM, W_Q, W_Q_NORM, W_V, check)
 from .engine import DeviceBuffer, HIPContext, _ptr
+from .sampling import sample_token
 
 WEIGHT_NAMES = {
     W_EMBED: "model.embed_tokens.weight",
@@ -240,15 +241,25 @@ class Decoder:
         seq.free()
         return out
 
-    def forward(self, token: int, return_logits: bool = False):
-        """InferenceEngine.forward(token:) at temperature 0: the greedy next
-        token (and the f32 logits when asked)."""
+    def forward(self, token: int, return_logits: bool = False, temperature: float = 0.0,
+                top_p: float = 1.0, rng: Optional[np.random.Generator] = None):
+        """InferenceEngine.forward(token:temperature:topP:) (:125-156): the next
+        token — greedy on the GPU at temperature <= 0, else sampled on the host
+        from the step's logits as the reference does (sampling.sample_token) —
+        and the f32 logits when asked."""
         self._tok.upload(np.array([token, 0, 0, 0], dtype=np.int32))
         self.step_device(self._tok, self._tok, self._logits)
         self.ctx.sync()
-        nxt = int(self._tok.download(np.int32, 1)[0])
+        logits = None
+        if temperature > 0:
+            logits = self._logits.download(np.float32, self.shape.vocab)
+            nxt = sample_token(logits, temperature, top_p, rng=rng)
+        else:
+            nxt = int(self._tok.download(np.int32, 1)[0])
         if return_logits:
-            return nxt, self._logits.download(np.float32, self.shape.vocab)
+            if logits is None:
+                logits = self._logits.download(np.float32, self.shape.vocab)
+            return nxt, logits
         return nxt
 
 

@@ -178,6 +178,22 @@ def test_decoder_tiny_teacher_forced_over_two_attention_chunks():
         p.close()
 
 
+def test_decoder_forward_samples_from_its_logits():
+    """forward(temperature > 0) samples on the host from the step's logits
+    (InferenceEngine.swift:557-574) with the caller's generator."""
+    from m1moe_amd.sampling import sample_token
+    p = Pair(synth.DECODERS["tiny_dec"], seed=17, max_seq=16)
+    try:
+        toks = synth.prompt_tokens(p.wl, 2, 4)
+        for i, t in enumerate(toks):
+            tok, lg = p.dec.forward(int(t), return_logits=True, temperature=0.8, top_p=0.9,
+                                    rng=np.random.default_rng(i))
+            assert tok == sample_token(lg, 0.8, 0.9, rng=np.random.default_rng(i))
+        assert p.dec.position() == len(toks)
+    finally:
+        p.close()
+
+
 def test_decoder_reset_restarts_the_sequence():
     p = Pair(synth.DECODERS["tiny_dec"], seed=12, max_seq=32)
     try:

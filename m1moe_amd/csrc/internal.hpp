@@ -214,7 +214,7 @@ struct AttnArgs {
 
 constexpr int kAttnChunk = 64;   // positions per attention workgroup
 constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
-constexpr int kAttnMaxChunks = 16;   // workgroups per kv head
+constexpr int kAttnMaxChunks = 32;   // workgroups per kv head
 constexpr int kMvStageMax = 8192;   // largest staged (normalised / embedded) input, floats
 
 // ---- decoder prefill (prefill_dense.hip) ----

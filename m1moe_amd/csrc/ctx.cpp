@@ -253,7 +253,7 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
     const uint64_t cap = m1moe::kPrefillCap;
     {
         // hand-off state of the fused decode kernel: kLogitRep replicas of
-        // the tagged logits, kNRep replicas of K padded slot counters, one
+        // the tagged logits, kNRep replicas of n_cnt padded tile counters, one
         // launch counter per workgroup
         m1moe::FusedArgs fa{};
         fa.h = g.h;
@@ -263,7 +263,7 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         const int grid = m1moe::decode_grid(fa);
         c->sync_gu_cnt = (uint64_t)m1moe::kLogitRep * m1moe::kRepStride * 8;
         c->sync_seen =
-            c->sync_gu_cnt + (uint64_t)m1moe::kNRep * g.K * m1moe::kCntStride * 4;
+            c->sync_gu_cnt + (uint64_t)m1moe::kNRep * fa.n_cnt * m1moe::kCntStride * 4;
         c->sync_bytes = c->sync_seen + ((uint64_t)grid * 4 + 255) / 256 * 256;
     }
     if ((rc = device_alloc((void**)&c->arena, L * E * g.expert_bytes, "expert arena")) ||

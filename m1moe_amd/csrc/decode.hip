@@ -15,13 +15,13 @@
 //                      workgroup's weight loads are issued at once (for a
 //                      few-MB working set the whole layer must be in flight
 //                      to cover the loaded HBM latency); it writes
-//                      act[k][rows] = silu(g) * u, then bumps one of kSub
-//                      spread counters of slot k.
+//                      act[k][rows] = silu(g) * u, then counts the tile
+//                      for the down unit that reads those rows.
 //   [n_gu, grid)       down workgroups: Rd output rows for all K slots.  Each
 //                      lane owns one (slot, 32-column chunk) of the down
 //                      projection; its weights for all Rd rows are loaded as
 //                      soon as the routing is known, then it waits for its
-//                      slot's counters, converts its chunk of act once and
+//                      unit's counters, converts its chunk of act once and
 //                      sweeps the rows.  Slots are combined in slot order in
 //                      LDS (deterministic, no atomics), plus the residual.
 //   Workgroup e < E first publishes router logit e (all four waves).
@@ -30,7 +30,7 @@
 // accesses are coherent across the XCDs' L2s), never release/acquire fences
 // (an L2 write-back or invalidate costs microseconds).  Logits are published as (launch tag,
 // value) pairs into kLogitRep replicas, and a workgroup polls replica
-// wg % kLogitRep; slot counters have kNRep replicas.  Nothing is
+// wg % kLogitRep; tile counters have kNRep replicas.  Nothing is
 // reset between launches: every workgroup counts its own launches (seen[wg]),
 // so all agree on the launch number `tag` and on the counters' targets
 // (graph replay needs no memset).  Every wait is bounded: on timeout the
@@ -63,6 +63,14 @@ constexpr int kDnTarget = 256;  // down workgroups
 constexpr int kGuMax = 512;     // gate/up workgroups (persistent beyond that many tiles)
 
 static_assert(kWaves >= 4, "the router splits a logit over four waves");
+
+// Expert weights are read once per launch: non-temporal loads keep them from
+// displacing the hand-off lines and router rows in the caches.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint8_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // ---- hand-off primitives ------------------------------------------------------
 
@@ -476,8 +484,8 @@ __device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int
             const uint32_t cc = (uint32_t)min(m.c0 + 64 * j, a.Cg - 1);
             const uint32_t wo = real ? rc * row_bytes + cc * 16u : 0u;
             const uint32_t sbw = real ? sb_word(rc * groups + (cc >> GSL)) : 0u;
-            t.gw[u][j] = *reinterpret_cast<const uint4*>(gw_b + wo);
-            t.uw[u][j] = *reinterpret_cast<const uint4*>(uw_b + wo);
+            t.gw[u][j] = ld_stream(gw_b + wo);
+            t.uw[u][j] = ld_stream(uw_b + wo);
             t.gs[u][j] = *reinterpret_cast<const uint32_t*>(gs_b + sbw);
             t.gb[u][j] = *reinterpret_cast<const uint32_t*>(gb_b + sbw);
             t.us[u][j] = *reinterpret_cast<const uint32_t*>(us_b + sbw);
@@ -534,15 +542,34 @@ __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, 
     }
 }
 
+// Counted unit of gate/up tile T (slot-major tiles of rows_tile act rows,
+// a power of two <= 1024): its slot (Cp < 64), or (slot, 2048-row block of
+// act) = the down unit that reads those rows (Cp >= 64).
+__device__ __forceinline__ int count_unit(const FusedArgs& a, int T) {
+    const int k = T / a.tiles_per_slot;
+    if (a.Cp < 64) return k;
+    return k * a.nb + (((T - k * a.tiles_per_slot) * a.rows_tile) >> 11);
+}
+// Tiles of counted unit c (what its parts add up to in one launch).
+__device__ __forceinline__ uint32_t count_tiles(const FusedArgs& a, int c) {
+    if (a.Cp < 64) return (uint32_t)a.tiles_per_slot;
+    const int tpb = 2048 / a.rows_tile;
+    const int b = c % a.nb;
+    return (uint32_t)min(tpb, a.tiles_per_slot - b * tpb);
+}
+
 // gate/up workgroup g: tiles T = g, g + n_gu, ... of the K * tiles_per_slot
 // (slot-major, so slot 0 completes first and its down work can start while
 // later slots stream), each tile = rows_tile rows of one slot; the next
 // tile's loads are in flight while a tile is computed.  When the workgroup
-// moves on to another slot (and at its end) it adds the number of tiles it
-// finished of the previous one to every replica of that slot's counter (a
-// consumer polls only its own replica): one add per slot, not per tile, since
-// adds to one counter serialise in the memory system and, being counted with
-// the loads, stall the next tile's wait.  Counts do not wait for the act
+// moves on to another counted unit (and at its end) it adds the number of
+// tiles it finished of the previous one to its part of every copy of that
+// unit's counter (a consumer polls one copy): one add per unit, not per tile,
+// since adds to one counter serialise in the memory system and, being counted
+// with the loads, stall the next tile's wait.  With several tiles per
+// workgroup each tile is its own unit (down units are 2048 act rows, tiles
+// are 512 tiles apart); there the count has kCntParts parts, so each counter
+// takes a quarter of the adds and a consumer adds four.  Counts do not wait for the act
 // stores to be acknowledged (that wait costs µs under the expert stream): the
 // consumer checks the tag bits of what it reads and reads again until they
 // are current.
@@ -559,12 +586,14 @@ __device__ void gu_role(const FusedArgs& a, const Layout& L, int g, int wave, in
         return (r.ok && e >= 0) ? e : -1;
     };
     auto row_of = [&](int T) { return (T % tps) * a.rows_tile + wave_row; };
-    int cnt_k = g / tps;  // slot being counted
-    uint32_t cnt_n = 0;   // its tiles finished by this workgroup
+    int cnt_c = count_unit(a, g);  // counted unit of the current tiles
+    uint32_t cnt_n = 0;            // its tiles finished by this workgroup
     auto flush = [&]() {
         __syncthreads();
-        if (threadIdx.x < (unsigned)kNRep)
-            add_u32(a.gu_cnt + ((size_t)threadIdx.x * a.K + cnt_k) * kCntStride, cnt_n);
+        if (threadIdx.x < (unsigned)(kNRep / a.cnt_parts))
+            add_u32(a.gu_cnt + (((size_t)threadIdx.x * a.cnt_parts + g % a.cnt_parts) * a.n_cnt +
+                                cnt_c) * kCntStride,
+                    cnt_n);
     };
     // this workgroup's tiles: i = 0 .. n_mine-1 -> T = g + i * n_gu.  Two
     // tiles are in flight from the start; every prefetch is issued (past the
@@ -579,9 +608,10 @@ __device__ void gu_role(const FusedArgs& a, const Layout& L, int g, int wave, in
     auto step = [&](int i, const GUTile<CPL, UG>& t) {
         const int T = g + i * a.n_gu;
         const int k = T / tps;
-        if (k != cnt_k) {
+        const int c = count_unit(a, T);
+        if (c != cnt_c) {
             flush();
-            cnt_k = k;
+            cnt_c = c;
             cnt_n = 0;
         }
         if (expert_of(T) >= 0) {
@@ -656,21 +686,27 @@ __device__ __forceinline__ void dn_load(const FusedArgs& a, const Layout& L, con
         const uint32_t rc = (uint32_t)min(row0 + r, a.h - 1);
         const uint32_t sbw = real ? sb_word(rc * groups + (cc >> GSL)) : 0u;
         const uint64_t wo = real ? (uint64_t)rc * row_bytes + cc * 16u : 0u;
-        t.w[r] = *reinterpret_cast<const uint4*>(w_b + wo);
+        t.w[r] = ld_stream(w_b + wo);
         t.s[r] = *reinterpret_cast<const uint32_t*>(s_b + sbw);
         t.b[r] = *reinterpret_cast<const uint32_t*>(b_b + sbw);
     }
 }
 
-// Waits until every gate/up workgroup of slots [k0, k0 + n) has been counted
-// (n <= K <= 32), polling replica wg % kNRep of the slot counters.
-__device__ bool wait_slots(const FusedArgs& a, int k0, int n, int lane, uint32_t tag) {
-    const bool mine = lane < n;
-    const uint32_t want = tag * (uint32_t)a.tiles_per_slot;
+// Waits until every gate/up tile of counted units [c0, c0 + n) has been
+// counted (n * cnt_parts <= 64), polling copy wg % (kNRep / cnt_parts): lane
+// j reads part j % cnt_parts of unit c0 + j / cnt_parts, the parts are added
+// across their lanes.
+__device__ bool wait_counts(const FusedArgs& a, int c0, int n, int lane, uint32_t tag) {
+    const int P = a.cnt_parts;
+    const bool mine = lane < n * P;
+    const int c = c0 + (mine ? lane / P : 0);
+    const uint32_t want = tag * count_tiles(a, c);
     const uint32_t* p = a.gu_cnt +
-        ((size_t)(blockIdx.x & (kNRep - 1)) * a.K + (size_t)(k0 + (mine ? lane : 0))) * kCntStride;
+        (((size_t)(blockIdx.x % (kNRep / P)) * P + (lane & (P - 1))) * a.n_cnt + c) * kCntStride;
     for (int it = 0;; ++it) {
-        const bool done = !mine || ld_u32(p) == want;
+        uint32_t v = ld_u32(p);
+        for (int m = 1; m < P; m <<= 1) v += __shfl_xor(v, m);
+        const bool done = !mine || v == want;
         if (__all(done)) return true;
         if (it >= a.spin_limit) return false;
         __builtin_amdgcn_s_sleep(2);
@@ -689,8 +725,9 @@ template <int GSL>
 __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave, int lane,
                         RouteLDS& r, float* s_part, uint32_t tag) {
     const bool ok_run = r.ok != 0;
-    const int row_base = dblk * a.Rd;
-    const int nsub = a.Rd / kRT;
+    const int Rd = a.Rd;
+    const int row_base = dblk * Rd;
+    const int nsub = Rd / kRT;
     const int total = a.units * nsub;
     const int per = (total + kWaves - 1) / kWaves;
     const int g0 = wave * per;
@@ -718,7 +755,7 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     asm volatile("" ::: "memory");
     if (wave == 0) routing_weights(a, lane, r);  // read by the combine after a barrier
     float res = 0.f;
-    if ((int)threadIdx.x < a.Rd && row_base + (int)threadIdx.x < a.h && a.residual)
+    if ((int)threadIdx.x < Rd && row_base + (int)threadIdx.x < a.h && a.residual)
         res = a.residual[row_base + threadIdx.x];
     const NibK nk = nib_consts();
     int cur = -1;
@@ -730,16 +767,16 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
         if (p.u != cur) {
             cur = p.u;
             d = dn_unit(a, p.u, lane);
-            int k0, n;
-            if (a.Cp < 64) {
-                k0 = p.u * a.spu;
-                n = min(a.spu, a.K - k0);
-            } else {
-                k0 = d.k;
+            int c0, n;
+            if (a.Cp < 64) {  // the unit's slots
+                c0 = p.u * a.spu;
+                n = min(a.spu, a.K - c0);
+            } else {          // (slot, block) = the unit itself
+                c0 = p.u;
                 n = 1;
             }
             bool ready = ok_run;
-            if (ready && !wait_slots(a, k0, n, lane, tag)) {
+            if (ready && !wait_counts(a, c0, n, lane, tag)) {
                 flag_error(a.err, 4u);
                 ready = false;
             }
@@ -767,7 +804,7 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
             inv = lane_scale_prep<1>(v, xc);
         }
         const uint32_t cc = (uint32_t)min(d.c, a.Cd - 1);
-        float* part = s_part + (d.k * a.nb + d.blk) * a.Rd + p.st * kRT;
+        float* part = s_part + (d.k * a.nb + d.blk) * Rd + p.st * kRT;
 #pragma unroll
         for (int rr = 0; rr < kRT; ++rr) {
             const uint32_t rc = (uint32_t)min(row_base + p.st * kRT + rr, a.h - 1);
@@ -785,13 +822,13 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     }
     __syncthreads();
     // combine in slot order, 64-chunk blocks summed in order (Shaders.metal:371-374)
-    for (int rr = threadIdx.x; rr < a.Rd; rr += kThreads) {
+    for (int rr = threadIdx.x; rr < Rd; rr += kThreads) {
         const int row = row_base + rr;
         if (row >= a.h) continue;
         float acc = (rr == (int)threadIdx.x) ? res : (a.residual ? a.residual[row] : 0.f);
         for (int k = 0; k < a.K; ++k) {
             float y = 0.f;
-            for (int b = 0; b < a.nb; ++b) y += s_part[(k * a.nb + b) * a.Rd + rr];
+            for (int b = 0; b < a.nb; ++b) y += s_part[(k * a.nb + b) * Rd + rr];
             acc = fmaf(slot_weight(a, r.w, k), y, acc);
         }
         a.out[row] = acc;
@@ -801,7 +838,7 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
 // ---- the kernel --------------------------------------------------------------------
 
 template <int CPL, int UG, int GSL>
-__global__ __launch_bounds__(kThreads) void moe_decode_kernel(FusedArgs a) {
+__global__ __launch_bounds__(kThreads, (CPL <= 2 ? 3 : 1)) void moe_decode_kernel(FusedArgs a) {
     __shared__ RouteLDS r;
     __shared__ uint32_t s_tag;
     __shared__ double s_lp[4];
@@ -947,6 +984,8 @@ int decode_grid(FusedArgs& a) {
     const int nsub = max(1, (a.h + kDnTarget * kRT - 1) / (kDnTarget * kRT));
     a.Rd = kRT * nsub;
     a.n_dn = (a.h + a.Rd - 1) / a.Rd;
+    a.n_cnt = a.Cp < 64 ? a.K : a.K * a.nb;
+    a.cnt_parts = a.n_gu < a.K * a.tiles_per_slot ? kCntParts : 1;
     return a.n_gu + a.n_dn;
 }
 

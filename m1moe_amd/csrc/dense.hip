@@ -602,21 +602,25 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         s_st[1][i][cc] = ld_coh(base + cc * cstride + i * (HD + 2) + 1);
     }
     __syncthreads();
+    constexpr int kBatch = 32;  // partial values in flight per thread
     for (int t = tid; t < QH * HD; t += 256) {
         const int i = t / HD, d = t - i * HD;
-        float vals[kAttnMaxChunks];
-#pragma unroll
-        for (int cc = 0; cc < kAttnMaxChunks; ++cc)
-            vals[cc] = cc < nact ? ld_coh(base + cc * cstride + i * (HD + 2) + 2 + d) : 0.f;
         float M = -INFINITY;
         for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, s_st[0][i][cc]);
         float L = 0.f, acc = 0.f;
+        for (int cb = 0; cb < nact; cb += kBatch) {
+            float vals[kBatch];
 #pragma unroll
-        for (int cc = 0; cc < kAttnMaxChunks; ++cc) {
-            if (cc >= nact) break;
-            const float f = expf(s_st[0][i][cc] - M);
-            L = fmaf(s_st[1][i][cc], f, L);
-            acc = fmaf(vals[cc], f, acc);
+            for (int j = 0; j < kBatch; ++j)
+                vals[j] = cb + j < nact ? ld_coh(base + (cb + j) * cstride + i * (HD + 2) + 2 + d)
+                                        : 0.f;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                if (cb + j >= nact) break;
+                const float f = expf(s_st[0][i][cb + j] - M);
+                L = fmaf(s_st[1][i][cb + j], f, L);
+                acc = fmaf(vals[j], f, acc);
+            }
         }
         a.out[(size_t)(h0 + i) * HD + d] = acc / L;
     }

@@ -58,7 +58,8 @@ struct FusedArgs {
     // agree on the launch number ("tag") without communicating.
     unsigned long long* slots;   // [kLogitRep][kRepStride] logits tagged with the launch number
     float* act;                  // [K][I] silu(gate) * up
-    uint32_t* gu_cnt;            // [kNRep][K] monotonic per-slot counters, kCntStride apart
+    uint32_t* gu_cnt;            // [kNRep][n_cnt] monotonic counters of finished gate/up
+                                 // tiles, kCntStride apart
     uint32_t* seen;              // [grid] launches completed by each workgroup
     uint32_t* err;               // sticky device error flag
     int32_t h, E, K, I, gs, norm, x_bf16, spin_limit;
@@ -71,6 +72,12 @@ struct FusedArgs {
                                  // segment, 64-lane blocks per slot (Cp >= 64)
     int32_t spu, units;          // slots per 64-lane unit (Cp < 64), units per row block
     int32_t cp_log2;             // log2(Cp) when Cp < 64
+    // counted units of gate/up tiles: one per slot (Cp < 64) or one per
+    // (slot, 64-chunk block of the down input) (Cp >= 64), so a down unit
+    // waits only for the act rows it reads.  Replica r = copy * cnt_parts +
+    // part: a gate/up workgroup adds to part (wg % cnt_parts) of every copy,
+    // a consumer sums the cnt_parts parts of one copy.
+    int32_t n_cnt, cnt_parts;
 };
 
 // Replicas of the hand-off words (published logits, slot counters), so that
@@ -78,6 +85,7 @@ struct FusedArgs {
 // (r * K + k) * kCntStride: consecutive 128-byte lines, which spreads them over
 // the L2 channels (replicas exactly 4 KiB apart would share one channel).
 constexpr int kNRep = 32;            // counter replicas
+constexpr int kCntParts = 4;         // parts of a count when gate/up workgroups take several tiles
 constexpr int kLogitRep = 8;         // logit replicas
 constexpr int kRepStride = 544;      // u64 words between logit replicas (4352 B)
 constexpr int kCntStride = 32;       // u32 words between counters (128 B)

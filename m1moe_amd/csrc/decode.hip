@@ -222,49 +222,57 @@ __device__ __forceinline__ float input_rms(const FusedArgs& a, int lane) {
     return rsqrtf(wave_sum(s) / (float)a.h + a.x_eps);
 }
 
-// x[d .. d+7] *= rms * w[d .. d+7] (the norm of Shaders.metal:121-134)
-__device__ __forceinline__ void norm8(const FusedArgs& a, int d, float rms, float* xv) {
-    const uint4 w = *reinterpret_cast<const uint4*>(a.x_norm_w + d);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = xv[i] * rms * bf16x8_at(w, i);
-}
 
-// rms / need_rms: a normalised input's scale, computed at the first call
-// (after this call's row loads are issued, so the two latencies overlap).
+// rms / need_rms: a normalised input's scale, computed at the first call.
+// All of a wave's loads (router row, x, norm weights, the partial sums of
+// squares) are issued before any is used: one memory round trip.  CPL =
+// ceil(h / 2048) column blocks per lane.
+template <int CPL>
 __device__ void produce_logit(const FusedArgs& a, int e, int wave, int lane, uint32_t* s_tag,
                               uint32_t tag_reg, double* s_lp, float& rms, bool& need_rms) {
     if (wave < 4) {
         const uint16_t* wr = a.router + (size_t)e * a.h;
         const int C = a.h / 32;
-        const int niter = (C + 63) / 64;
-        double acc = 0.0;
-        for (int it = 0; it < niter; ++it) {
+        const bool norm = !a.x_bf16 && a.x_norm_w;
+        uint4 wv[CPL], xb[CPL], nw[CPL];
+        float4 xf[CPL][2];
+        int dd[CPL];
+#pragma unroll
+        for (int it = 0; it < CPL; ++it) {
             const int c = lane + 64 * it;
-            const bool ok = c < C;
-            const int d = (ok ? c : 0) * 32 + wave * 8;
-            const uint4 wv = *reinterpret_cast<const uint4*>(wr + d);
+            dd[it] = (c < C ? c : 0) * 32 + wave * 8;
+            wv[it] = *reinterpret_cast<const uint4*>(wr + dd[it]);
+            if (a.x_bf16) {
+                xb[it] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + dd[it]);
+            } else {
+                const float* xr = static_cast<const float*>(a.x) + dd[it];
+                xf[it][0] = *reinterpret_cast<const float4*>(xr);
+                xf[it][1] = *reinterpret_cast<const float4*>(xr + 4);
+                if (norm) nw[it] = *reinterpret_cast<const uint4*>(a.x_norm_w + dd[it]);
+            }
+        }
+        if (norm && need_rms) {  // uniform: every lane of the wave is here
+            rms = input_rms(a, lane);
+            need_rms = false;
+        }
+        double acc = 0.0;
+#pragma unroll
+        for (int it = 0; it < CPL; ++it) {
             float xv[8];
             if (a.x_bf16) {
-                const uint4 xb = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + d);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xv[i] = bf16x8_at(xb, i);
+                for (int i = 0; i < 8; ++i) xv[i] = bf16x8_at(xb[it], i);
             } else {
-                const float* xr = static_cast<const float*>(a.x) + d;
-                const float4 x0 = *reinterpret_cast<const float4*>(xr);
-                const float4 x1 = *reinterpret_cast<const float4*>(xr + 4);
-                xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
-                xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
-                if (a.x_norm_w) {
-                    if (need_rms) {  // uniform: every lane of the wave is here
-                        rms = input_rms(a, lane);
-                        need_rms = false;
-                    }
-                    norm8(a, d, rms, xv);
+                xv[0] = xf[it][0].x; xv[1] = xf[it][0].y; xv[2] = xf[it][0].z; xv[3] = xf[it][0].w;
+                xv[4] = xf[it][1].x; xv[5] = xf[it][1].y; xv[6] = xf[it][1].z; xv[7] = xf[it][1].w;
+                if (norm) {  // the norm of Shaders.metal:121-134
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[i] = xv[i] * rms * bf16x8_at(nw[it], i);
                 }
             }
-            if (ok) {
+            if (lane + 64 * it < C) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv, i) * (double)xv[i];
+                for (int i = 0; i < 8; ++i) acc += (double)bf16x8_at(wv[it], i) * (double)xv[i];
             }
         }
         acc = wave_sum_f64_last(acc);
@@ -854,7 +862,7 @@ __global__ __launch_bounds__(kThreads, (CPL <= 2 ? 3 : 1)) void moe_decode_kerne
         float rms = 1.f;
         bool need_rms = a.x_norm_w != nullptr;
         for (int e = wg; e < a.E; e += gridDim.x)
-            produce_logit(a, e, wave, lane, &s_tag, tag_reg, s_lp, rms, need_rms);
+            produce_logit<CPL>(a, e, wave, lane, &s_tag, tag_reg, s_lp, rms, need_rms);
     } else {
         if (threadIdx.x == 0) s_tag = tag_reg;
         __syncthreads();
@@ -873,13 +881,23 @@ __global__ __launch_bounds__(kThreads, (CPL <= 2 ? 3 : 1)) void moe_decode_kerne
             load_chunk(a.x, a.x_bf16, min(c, a.Cg - 1), m.ok && c < a.Cg, v[j]);
         }
         if (a.x_norm_w) {
-            const float rms = input_rms(a, lane);
+            // the norm weights are loaded before the partial sums are waited for
+            uint4 nw[CPL][4];
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const int c = min(m.c0 + 64 * j, a.Cg - 1);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) norm8(a, 32 * c + 8 * q, rms, &v[j][8 * q]);
+                for (int q = 0; q < 4; ++q)
+                    nw[j][q] = *reinterpret_cast<const uint4*>(a.x_norm_w + 32 * c + 8 * q);
             }
+            const float rms = input_rms(a, lane);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        v[j][8 * q + i] = v[j][8 * q + i] * rms * bf16x8_at(nw[j][q], i);
         }
         inv = lane_scale_prep<CPL>(v, xc);
     }

@@ -403,8 +403,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (c0 < seq) {
         // this lane's K and V rows of a 64-position sub-chunk (row p, not yet
         // in the cache, comes from LDS once it is prepared)
-        float kr[IT][8], vr[IT][8];
-        auto load_rows = [&](int p0) {
+        // two sub-chunks of rows in flight (A, B alternate)
+        struct KVRows {
+            float k[IT][8], v[IT][8];
+        };
+        KVRows A, B;
+        auto load_rows = [&](int p0, KVRows& R) {
 #pragma unroll
             for (int it = 0; it < IT; ++it) {
                 const int pp = p0 + wave * PW + it * PPI + pg;
@@ -416,13 +420,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     v0 = *reinterpret_cast<const float4*>(a.vcache + off);
                     v1 = *reinterpret_cast<const float4*>(a.vcache + off + 4);
                 }
-                kr[it][0] = k0.x, kr[it][1] = k0.y, kr[it][2] = k0.z, kr[it][3] = k0.w;
-                kr[it][4] = k1.x, kr[it][5] = k1.y, kr[it][6] = k1.z, kr[it][7] = k1.w;
-                vr[it][0] = v0.x, vr[it][1] = v0.y, vr[it][2] = v0.z, vr[it][3] = v0.w;
-                vr[it][4] = v1.x, vr[it][5] = v1.y, vr[it][6] = v1.z, vr[it][7] = v1.w;
+                R.k[it][0] = k0.x, R.k[it][1] = k0.y, R.k[it][2] = k0.z, R.k[it][3] = k0.w;
+                R.k[it][4] = k1.x, R.k[it][5] = k1.y, R.k[it][6] = k1.z, R.k[it][7] = k1.w;
+                R.v[it][0] = v0.x, R.v[it][1] = v0.y, R.v[it][2] = v0.z, R.v[it][3] = v0.w;
+                R.v[it][4] = v1.x, R.v[it][5] = v1.y, R.v[it][6] = v1.z, R.v[it][7] = v1.w;
             }
         };
-        load_rows(c0);
+        // (head_dim 256 has the registers for one sub-chunk only)
+        constexpr bool kTwo = HD <= 128;
+        load_rows(c0, A);
+        if (kTwo && c0 + kAttnChunk < c1) load_rows(c0 + kAttnChunk, B);
 
         // q heads (and the new k when this workgroup holds row p): per-head
         // RMSNorm (InferenceEngine.swift:538-548), then RoPE (:521-536)
@@ -489,15 +496,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             s_l[tid] = 0.f;
         }
 
-        for (int p0 = c0; p0 < c1; p0 += kAttnChunk) {
+        auto sub = [&](int p0, KVRows& R) {
             if (mine_new && p >= p0 && p < p0 + kAttnChunk) {
 #pragma unroll
                 for (int it = 0; it < IT; ++it) {
                     if (p0 + wave * PW + it * PPI + pg != p) continue;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        kr[it][e] = s_kv[0][8 * lp + e];
-                        vr[it][e] = s_kv[1][8 * lp + e];
+                        R.k[it][e] = s_kv[0][8 * lp + e];
+                        R.v[it][e] = s_kv[1][8 * lp + e];
                     }
                 }
             }
@@ -509,7 +516,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 for (int i = 0; i < QH; ++i) {
                     float d = 0.f;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) d = fmaf(qv[i][e], kr[it][e], d);
+                    for (int e = 0; e < 8; ++e) d = fmaf(qv[i][e], R.k[it][e], d);
 #pragma unroll
                     for (int o = 1; o < LP; o <<= 1) d += __shfl_xor(d, o);
                     if (lp == 0) s_p[i][pl] = p0 + pl < c1 ? d * a.scale : -INFINITY;
@@ -546,12 +553,23 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 for (int i = 0; i < QH; ++i) {
                     const float w = s_p[i][pl];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[i][e] = fmaf(w, vr[it][e], acc[i][e]);
+                    for (int e = 0; e < 8; ++e) acc[i][e] = fmaf(w, R.v[it][e], acc[i][e]);
                 }
             }
+            if (p0 + kAttnChunk < c1) __syncthreads();  // s_p is rewritten by the next sub-chunk
+        };
+        if (!kTwo) {
+            for (int p0 = c0; p0 < c1; p0 += kAttnChunk) {
+                sub(p0, A);
+                if (p0 + kAttnChunk < c1) load_rows(p0 + kAttnChunk, A);
+            }
+        }
+        for (int p0 = c0; kTwo && p0 < c1; p0 += 2 * kAttnChunk) {
+            sub(p0, A);
+            if (p0 + 2 * kAttnChunk < c1) load_rows(p0 + 2 * kAttnChunk, A);
             if (p0 + kAttnChunk < c1) {
-                __syncthreads();  // s_p is rewritten by the next sub-chunk
-                load_rows(p0 + kAttnChunk);
+                sub(p0 + kAttnChunk, B);
+                if (p0 + 3 * kAttnChunk < c1) load_rows(p0 + 3 * kAttnChunk, B);
             }
         }
 #pragma unroll
@@ -596,33 +614,67 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (!last_workgroup(a.counters + g, nch, &s_flag)) return;
     const size_t cstride = (size_t)QH * (HD + 2);
     const float* base = a.partial + (size_t)g * nch * cstride;
-    for (int t = tid; t < QH * nact; t += 256) {
-        const int i = t / nact, cc = t - i * nact;
-        s_st[0][i][cc] = ld_coh(base + cc * cstride + i * (HD + 2));
-        s_st[1][i][cc] = ld_coh(base + cc * cstride + i * (HD + 2) + 1);
+    // The chunk statistics (one (max, sum) pair per thread, staged in LDS)
+    // and the first kMB chunks of each of the thread's OPT outputs are loaded
+    // together: one memory round trip for up to kMB chunks.
+    static_assert(kAttnMaxChunks <= 64, "the merge takes one chunk per lane");
+    constexpr int OPT = (QH * HD + 255) / 256;  // outputs per thread
+    constexpr int kMB = OPT == 1 ? 32 : OPT == 2 ? 28 : OPT <= 4 ? 12 : 6;
+    const bool has_st = tid < QH * nact;  // QH * nact <= 256
+    const int st_i = has_st ? tid / nact : 0, st_c = has_st ? tid - st_i * nact : 0;
+    float st_m = 0.f, st_l = 0.f;
+    if (has_st) {
+        st_m = ld_coh(base + st_c * cstride + st_i * (HD + 2));
+        st_l = ld_coh(base + st_c * cstride + st_i * (HD + 2) + 1);
     }
-    __syncthreads();
-    constexpr int kBatch = 32;  // partial values in flight per thread
-    for (int t = tid; t < QH * HD; t += 256) {
-        const int i = t / HD, d = t - i * HD;
-        float M = -INFINITY;
-        for (int cc = 0; cc < nact; ++cc) M = fmaxf(M, s_st[0][i][cc]);
-        float L = 0.f, acc = 0.f;
-        for (int cb = 0; cb < nact; cb += kBatch) {
-            float vals[kBatch];
+    float acc[OPT];
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j)
-                vals[j] = cb + j < nact ? ld_coh(base + (cb + j) * cstride + i * (HD + 2) + 2 + d)
-                                        : 0.f;
+    for (int o = 0; o < OPT; ++o) acc[o] = 0.f;
+    for (int cb = 0; cb < nact; cb += kMB) {
+        float vals[OPT][kMB];
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
+        for (int o = 0; o < OPT; ++o) {
+            const int t = tid + 256 * o;
+            const int i = t < QH * HD ? t / HD : 0, d = t < QH * HD ? t - i * HD : 0;
+#pragma unroll
+            for (int j = 0; j < kMB; ++j)
+                vals[o][j] = (t < QH * HD && cb + j < nact)
+                                 ? ld_coh(base + (cb + j) * cstride + i * (HD + 2) + 2 + d)
+                                 : 0.f;
+        }
+        if (cb == 0) {
+            // per head: M = max_c m_c, factors f_c = e^(m_c - M) (in place of
+            // m_c), L = sum_c l_c f_c -- once per (head, chunk), not per output
+            if (has_st) {
+                s_st[0][st_i][st_c] = st_m;
+                s_st[1][st_i][st_c] = st_l;
+            }
+            __syncthreads();
+            for (int i = wave; i < QH; i += 4) {  // lane = chunk (nact <= 64)
+                const bool ok = lane < nact;
+                const float m = ok ? s_st[0][i][lane] : -INFINITY;
+                const float mx = wave_max(m);
+                const float f = ok ? expf(m - mx) : 0.f;
+                const float l = wave_sum(ok ? s_st[1][i][lane] * f : 0.f);
+                if (ok) s_st[0][i][lane] = f;
+                if (lane == 0) s_l[i] = l;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int o = 0; o < OPT; ++o) {
+            const int i = min((tid + 256 * o) / HD, QH - 1);
+#pragma unroll
+            for (int j = 0; j < kMB; ++j) {
                 if (cb + j >= nact) break;
-                const float f = expf(s_st[0][i][cb + j] - M);
-                L = fmaf(s_st[1][i][cb + j], f, L);
-                acc = fmaf(vals[j], f, acc);
+                acc[o] = fmaf(vals[o][j], s_st[0][i][cb + j], acc[o]);
             }
         }
-        a.out[(size_t)(h0 + i) * HD + d] = acc / L;
+    }
+#pragma unroll
+    for (int o = 0; o < OPT; ++o) {
+        const int t = tid + 256 * o;
+        if (t < QH * HD) a.out[(size_t)(h0 + t / HD) * HD + (t % HD)] = acc[o] / s_l[t / HD];
     }
     if (tid == 0) reset_counter(a.counters + g);
 }

@@ -843,6 +843,69 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     }
 }
 
+// The gate/up input of one workgroup (h <= CPL * 2048, CPL <= 2): x is read
+// from memory once per workgroup, normalised if asked (x * rms * w, rms from
+// the partial sums of squares), and staged in LDS; each wave then takes its
+// lanes' 32-element chunks from there.  (Every wave reading x itself put
+// 4x the bytes through L2 at the start of the launch.)  Chunks are padded to
+// 36 floats against LDS bank conflicts.
+template <int CPL>
+__device__ __forceinline__ void stage_x(const FusedArgs& a, int wave, int lane, const GUGeo& m,
+                                        float (&v)[CPL][32]) {
+    constexpr int kG = CPL * 2048 / (4 * kThreads);  // groups of 4 elements per thread
+    __shared__ __attribute__((aligned(16))) float s_x[CPL * 64 * 36];
+    __shared__ float s_rms;
+    float4 xv[kG];
+    uint2 nw[kG];
+#pragma unroll
+    for (int q = 0; q < kG; ++q) {
+        const int e = 4 * ((int)threadIdx.x + kThreads * q);
+        const int ec = e < a.h ? e : 0;
+        if (a.x_bf16) {
+            const uint2 b = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.x) + ec);
+            xv[q] = float4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u),
+                           __uint_as_float(b.y << 16), __uint_as_float(b.y & 0xffff0000u)};
+        } else {
+            xv[q] = *reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + ec);
+        }
+        if (a.x_norm_w) nw[q] = *reinterpret_cast<const uint2*>(a.x_norm_w + ec);
+    }
+    if (a.x_norm_w && wave == 0) {
+        const float r = input_rms(a, lane);
+        if (lane == 0) s_rms = r;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kG; ++q) {
+        const int e = 4 * ((int)threadIdx.x + kThreads * q);
+        if (e >= a.h) continue;
+        float4 t = xv[q];
+        if (a.x_norm_w) {  // the norm of Shaders.metal:121-134
+            const float rms = s_rms;
+            t.x = t.x * rms * __uint_as_float(nw[q].x << 16);
+            t.y = t.y * rms * __uint_as_float(nw[q].x & 0xffff0000u);
+            t.z = t.z * rms * __uint_as_float(nw[q].y << 16);
+            t.w = t.w * rms * __uint_as_float(nw[q].y & 0xffff0000u);
+        }
+        *reinterpret_cast<float4*>(&s_x[(e >> 5) * 36 + (e & 31)]) = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = m.c0 + 64 * j;
+        const bool ok = m.ok && c < a.Cg;
+        const float* src = &s_x[(ok ? c : 0) * 36];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 t = *reinterpret_cast<const float4*>(src + 4 * i);
+            v[j][4 * i + 0] = ok ? t.x : 0.f;
+            v[j][4 * i + 1] = ok ? t.y : 0.f;
+            v[j][4 * i + 2] = ok ? t.z : 0.f;
+            v[j][4 * i + 3] = ok ? t.w : 0.f;
+        }
+    }
+}
+
 // ---- the kernel --------------------------------------------------------------------
 
 template <int CPL, int UG, int GSL>
@@ -875,6 +938,14 @@ __global__ __launch_bounds__(kThreads, (CPL <= 2 ? 3 : 1)) void moe_decode_kerne
     if (is_gu) {
         const GUGeo m = gu_geo(lane, a.Cg, a.seg_g);
         float v[CPL][32];
+        bool staged = false;
+        if constexpr (CPL <= 2) {
+            if (!a.x_bf16) {  // (a bf16 x is half the bytes: read per wave)
+                stage_x<CPL>(a, wave, lane, m, v);
+                staged = true;
+            }
+        }
+        if (!staged) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = m.c0 + 64 * j;
@@ -898,6 +969,7 @@ __global__ __launch_bounds__(kThreads, (CPL <= 2 ? 3 : 1)) void moe_decode_kerne
 #pragma unroll
                     for (int i = 0; i < 8; ++i)
                         v[j][8 * q + i] = v[j][8 * q + i] * rms * bf16x8_at(nw[j][q], i);
+        }
         }
         inv = lane_scale_prep<CPL>(v, xc);
     }

@@ -134,7 +134,6 @@ struct PrefillArgs {
     uint32_t* err;               // sticky device error flag
 };
 
-constexpr int kPfTM = 64;   // prefill GEMM: weight rows per workgroup tile
 constexpr int kPfTN = 64;   // prefill GEMM: (token, slot) pairs per workgroup tile
 
 // launchers (defined next to their kernels); return a hipError_t as int

@@ -44,7 +44,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kTM = kPfTM, kTN = kPfTN;
+constexpr int kTN = kPfTN;
 constexpr int kMaxE = 256;
 constexpr uint32_t kNibMask = 0x03C003C0u;  // f16 mantissa bits 6..9 of both halves
 
@@ -183,17 +183,21 @@ __device__ __forceinline__ f16x8 dequant_word(uint32_t w, f16x2 s2, f16x2 b2) {
 // scale group since KB/4 <= 32 <= group size); MFMA k-step s uses word s.
 // Blocks are pipelined two deep: the loads of block kb+2 are issued while
 // block kb is multiplied; B tiles go through a double-buffered LDS tile.
-template <int NMAT, int KB>
+template <int NMAT, int KB, int NW>
 struct PfStage {
     static constexpr int W = KB / 32;  // packed words per lane per block
+    static constexpr int NB = KB * kTN / (8 * 64 * NW);  // uint4 of the B tile per thread
     uint32_t aw[NMAT][W];
     uint32_t as[NMAT], ab[NMAT];
-    uint4 b[KB / 32];                  // this thread's share of the B tile (KB/4 f16)
+    uint4 b[NB];                       // this thread's share of the B tile
 };
 
-template <int NMAT, int KB, int GSL>
-__global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles) {
+template <int NMAT, int KB, int GSL, int NW>
+__global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_tiles) {
     constexpr int W = KB / 32;
+    constexpr int TM = 16 * NW;               // weight rows per workgroup
+    constexpr int TPP = 64 * NW / kTN;        // B-staging threads per pair
+    constexpr int NB = PfStage<NMAT, KB, NW>::NB;
     constexpr int kRow = KB * 2 + 16;  // LDS bytes per pair row (padded)
     __shared__ __attribute__((aligned(16))) unsigned char s_b[2][kTN * kRow];
     __shared__ int s_tok[kTN];
@@ -212,7 +216,7 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles
     const int K = NMAT == 2 ? a.h : a.I;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, kq = lane >> 4;
-    const int row = mt * kTM + wave * 16 + r;  // this lane's A row
+    const int row = mt * TM + wave * 16 + r;  // this lane's A row
     const int nblk = K / KB;
     const uint32_t groups = (uint32_t)K >> (5 + GSL);
 
@@ -240,16 +244,16 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles
     }
     __syncthreads();
 
-    // B staging: thread -> (pair j = tid / 4, quarter q = tid % 4: KB/4 elements)
-    const int bj = tid >> 2, bq = tid & 3;
+    // B staging: thread -> (pair j = tid / TPP, part q = tid % TPP: KB/TPP elements)
+    const int bj = tid / TPP, bq = tid % TPP;
     const bool b_ok = bj < np;
     const _Float16* b_src =
         (NMAT == 2 ? a.xq + (size_t)s_tok[bj] * a.h : a.act + (size_t)(p0 + (b_ok ? bj : 0)) * a.I) +
-        bq * (KB / 4);
-    auto load = [&](int kb, PfStage<NMAT, KB>& st) {
+        bq * (KB / TPP);
+    auto load = [&](int kb, PfStage<NMAT, KB, NW>& st) {
         const uint4* pb = reinterpret_cast<const uint4*>(b_src + kb * KB);
 #pragma unroll
-        for (int i = 0; i < KB / 32; ++i) st.b[i] = b_ok ? pb[i] : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < NB; ++i) st.b[i] = b_ok ? pb[i] : make_uint4(0, 0, 0, 0);
         const uint32_t g = ((uint32_t)kb * KB + (uint32_t)kq * (KB / 4)) >> (5 + GSL);
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
@@ -266,10 +270,10 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles
             st.ab[m] = brow[m][g];
         }
     };
-    auto store_b = [&](int buf, const PfStage<NMAT, KB>& st) {
-        uint4* d = reinterpret_cast<uint4*>(&s_b[buf][bj * kRow + bq * (KB / 2)]);
+    auto store_b = [&](int buf, const PfStage<NMAT, KB, NW>& st) {
+        uint4* d = reinterpret_cast<uint4*>(&s_b[buf][bj * kRow + bq * (KB / TPP) * 2]);
 #pragma unroll
-        for (int i = 0; i < KB / 32; ++i) d[i] = permute8(st.b[i]);
+        for (int i = 0; i < NB; ++i) d[i] = permute8(st.b[i]);
     };
 
     f32x4 acc[NMAT][kTN / 16];
@@ -279,7 +283,7 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles
         for (int j = 0; j < kTN / 16; ++j) acc[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     bool bad_scale = false;
-    auto compute = [&](int buf, const PfStage<NMAT, KB>& st) {
+    auto compute = [&](int buf, const PfStage<NMAT, KB, NW>& st) {
         f16x2 s2[NMAT], b2[NMAT];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles
         }
     };
 
-    PfStage<NMAT, KB> S0, S1;
+    PfStage<NMAT, KB, NW> S0, S1;
     load(0, S0);
     if (nblk > 1) load(1, S1);
     store_b(0, S0);
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(PrefillArgs a, int m_tiles
     if (bad_scale) flag_error(a.err, 8u);
 
     // epilogue: lane holds column (pair) j*16 + r, rows 4*kq..4*kq+3 of the wave's 16
-    const int row0 = mt * kTM + wave * 16 + 4 * kq;
+    const int row0 = mt * TM + wave * 16 + 4 * kq;
 #pragma unroll
     for (int j = 0; j < kTN / 16; ++j) {
         const int n = j * 16 + r;
@@ -382,15 +386,27 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     *reinterpret_cast<float4*>(a.out + (size_t)t * a.h + d) = acc;
 }
 
-template <int NMAT, int GSL>
-void launch_gemm(const PrefillArgs& a, hipStream_t st, int grid, int m_tiles) {
+template <int NMAT, int GSL, int NW>
+void launch_gemm_nw(const PrefillArgs& a, hipStream_t st, int groups8, int rows) {
     const int K = NMAT == 2 ? a.h : a.I;
+    const int m_tiles = rows / (16 * NW);
+    const dim3 grid((unsigned)(8 * groups8 * m_tiles));
     if (K % 128 == 0)
-        hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 128, GSL>), dim3((unsigned)grid), dim3(256), 0, st,
-                           a, m_tiles);
+        hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 128, GSL, NW>), grid, dim3(64 * NW), 0, st, a,
+                           m_tiles);
     else
-        hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 64, GSL>), dim3((unsigned)grid), dim3(256), 0, st,
-                           a, m_tiles);
+        hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 64, GSL, NW>), grid, dim3(64 * NW), 0, st, a,
+                           m_tiles);
+}
+
+// Eight waves (128 weight rows) per workgroup where the rows allow it: the
+// workgroup's B tile in LDS then feeds twice the rows, halving the B reads.
+template <int NMAT, int GSL>
+void launch_gemm(const PrefillArgs& a, hipStream_t st, int groups8, int rows) {
+    if (rows % 128 == 0)
+        launch_gemm_nw<NMAT, GSL, 8>(a, st, groups8, rows);
+    else
+        launch_gemm_nw<NMAT, GSL, 4>(a, st, groups8, rows);
 }
 
 template <int GSL>
@@ -398,18 +414,17 @@ int launch_gemms(const PrefillArgs& a, hipStream_t st) {
     const int P = a.T * a.K;
     const int ntiles_max = (P + kTN - 1) / kTN + a.E;
     const int groups8 = (ntiles_max + 7) / 8;
-    const int mt_gu = a.I / kTM, mt_dn = a.h / kTM;
-    launch_gemm<2, GSL>(a, st, 8 * groups8 * mt_gu, mt_gu);
+    launch_gemm<2, GSL>(a, st, groups8, a.I);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    launch_gemm<1, GSL>(a, st, 8 * groups8 * mt_dn, mt_dn);
+    launch_gemm<1, GSL>(a, st, groups8, a.h);
     return (int)hipGetLastError();
 }
 
 }  // namespace
 
 int launch_prefill(const PrefillArgs& a, void* stream) {
-    if (a.E > kMaxE || a.h > 16384 || a.h % kTM || a.I % kTM) return (int)hipErrorInvalidValue;
+    if (a.E > kMaxE || a.h > 16384 || a.h % 64 || a.I % 64) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(prep_x_kernel, dim3((unsigned)a.T), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();

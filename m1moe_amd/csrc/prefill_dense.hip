@@ -15,9 +15,10 @@
 //   rope_kv_rows   per token and head: the per-head q/k RMSNorm and RoPE at
 //                  the token's position (InferenceEngine.swift:521-548), k and
 //                  v rows into the caches (:215-220)
-//   attn_causal    causal attention of the T queries over positions 0 .. their
-//                  own (Shaders.metal:209-326 for every token), online softmax
-//                  over key blocks staged in LDS
+//   attn_mfma      causal attention of the T queries over positions 0 .. their
+//                  own (Shaders.metal:209-326 for every token) on f32 MFMA,
+//                  online softmax over key blocks staged in LDS (head_dim 64,
+//                  128; attn_causal, on the SIMD units, for head_dim 256)
 //
 // The MoE block runs through the grouped prefill (prefill.hip).
 #include <hip/hip_runtime.h>
@@ -300,12 +301,152 @@ int launch_pf_rope_kv(const PfDenseArgs& a, void* stream) {
     return (int)hipGetLastError();
 }
 
+// Causal attention on v_mfma_f32_16x16x4f32 (f32 operands and accumulation;
+// head_dim 64 or 128).  Workgroup = (head, 64 queries), wave = 16 queries.
+// Keys go in blocks of 32 through LDS, shared by the four waves: K row-major,
+// V transposed.  Per block a wave computes S = Q K^T (16 x 32), updates each
+// query row's running max and sum (the softmax of Shaders.metal:245-289 in
+// pieces), writes P = e^(S - m) to LDS and reads it back as the A operand of
+// O += P V.  Contraction orders: in k-step 4t+u lane (r, kq) supplies dim (or
+// key) 16t + 4kq + u, so each lane's four steps read 16 contiguous bytes.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(PfDenseArgs a) {
+    constexpr int QW = 16, QB = 64, KB = 32;
+    constexpr int NT = HD / 16;  // 16-wide dim groups: Q K^T k-step groups, output blocks
+    __shared__ __attribute__((aligned(16))) float sK[KB][HD + 4];
+    __shared__ __attribute__((aligned(16))) float sVt[HD][KB + 4];
+    __shared__ __attribute__((aligned(16))) float sP[4][QW][KB + 4];
+    const int h = blockIdx.x, tb = blockIdx.y * QB;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, kq = lane >> 4;
+    const int p0 = *a.pos;
+    const int kvh = h / a.hpkv;
+    const int qw0 = tb + wave * QW;  // the wave's first query (token index)
+    // the workgroup's last query position (keys beyond it are never needed)
+    const int last = min(p0 + min(tb + QB, a.T) - 1, a.max_seq - 1);
+
+    // Q as the A operand: row lr, dims 16t + 4kq .. +3
+    f32x4v qa[NT];
+    {
+        const int t = min(qw0 + lr, a.T - 1);
+        const float* q = a.qkv + (size_t)t * a.ldqkv + (size_t)h * HD + 4 * kq;
+#pragma unroll
+        for (int t4 = 0; t4 < NT; ++t4) qa[t4] = *reinterpret_cast<const f32x4v*>(q + 16 * t4);
+    }
+    // this lane's output rows: queries qw0 + 4kq + i
+    int qpos[4];
+    bool qlive[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = qw0 + 4 * kq + i;
+        qlive[i] = t < a.T;
+        qpos[i] = min(p0 + t, a.max_seq - 1);
+    }
+    float m[4], l[4];
+    f32x4v acc[NT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    const int wlast = min(p0 + min(qw0 + QW, a.T) - 1, a.max_seq - 1);  // this wave's last
+
+    for (int k0 = 0; k0 <= last; k0 += KB) {
+        __syncthreads();  // the previous block's sK / sVt consumed
+        // K rows: thread -> (key r, 4 dims c); V: (key r fastest) -> sVt[dims][r]
+        for (int e = tid; e < KB * HD / 4; e += 256) {
+            const int r = e / (HD / 4), c = (e - r * (HD / 4)) * 4;
+            const int kp = min(k0 + r, last);
+            *reinterpret_cast<float4*>(&sK[r][c]) = *reinterpret_cast<const float4*>(
+                a.kcache + (size_t)kp * a.kvd + (size_t)kvh * HD + c);
+            const int rv = e % KB, cv = (e / KB) * 4;
+            const int kv = min(k0 + rv, last);
+            const float4 v = *reinterpret_cast<const float4*>(a.vcache + (size_t)kv * a.kvd +
+                                                              (size_t)kvh * HD + cv);
+            sVt[cv + 0][rv] = v.x;
+            sVt[cv + 1][rv] = v.y;
+            sVt[cv + 2][rv] = v.z;
+            sVt[cv + 3][rv] = v.w;
+        }
+        __syncthreads();
+        if (k0 > wlast) continue;  // (uniform per wave) keys after every query of the wave
+
+        // S = Q K^T: 2 blocks of 16 keys; lane: key 16nb + lr, queries 4kq + i
+        f32x4v s[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            s[nb] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t4 = 0; t4 < NT; ++t4) {
+                const f32x4v kb = *reinterpret_cast<const f32x4v*>(&sK[16 * nb + lr][16 * t4 + 4 * kq]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    s[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t4][u], kb[u], s[nb], 0, 0, 0);
+            }
+        }
+        // online softmax per query row (the 16 lanes of a kq group hold its keys)
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sv[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const int kp = k0 + 16 * nb + lr;
+                sv[nb] = (qlive[i] && kp <= qpos[i]) ? s[nb][i] * a.scale : -INFINITY;
+            }
+            float bm = fmaxf(sv[0], sv[1]);
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
+            const float mn = fmaxf(m[i], bm);
+            f[i] = m[i] == -INFINITY ? 0.f : expf(m[i] - mn);
+            float ls = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const float pe = sv[nb] == -INFINITY ? 0.f : expf(sv[nb] - mn);
+                sP[wave][4 * kq + i][16 * nb + lr] = pe;
+                ls += pe;
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) ls += __shfl_xor(ls, o);
+            l[i] = fmaf(l[i], f[i], ls);
+            m[i] = mn;
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[j][i] *= f[i];
+        // O += P V: A = P (row lr, keys 16t + 4kq + u), B = V^T rows (dim 16j + lr)
+#pragma unroll
+        for (int t2 = 0; t2 < KB / 16; ++t2) {
+            const f32x4v pa = *reinterpret_cast<const f32x4v*>(&sP[wave][lr][16 * t2 + 4 * kq]);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const f32x4v vb = *reinterpret_cast<const f32x4v*>(&sVt[16 * j + lr][16 * t2 + 4 * kq]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[u], vb[u], acc[j], 0, 0, 0);
+            }
+        }
+    }
+    // lane: dims 16j + lr of queries 4kq + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (!qlive[i]) continue;
+        float* out = a.attn + (size_t)(qw0 + 4 * kq + i) * a.qd + (size_t)h * HD;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) out[16 * j + lr] = acc[j][i] / l[i];
+    }
+}
+
 int launch_pf_attention(const PfDenseArgs& a, void* stream) {
-    const dim3 grid((unsigned)a.num_heads, (unsigned)((a.T + 15) / 16));
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid_m((unsigned)a.num_heads, (unsigned)((a.T + 63) / 64));
+    const dim3 grid((unsigned)a.num_heads, (unsigned)((a.T + 15) / 16));
     switch (a.head_dim) {
-        case 64: hipLaunchKernelGGL(attn_causal_kernel<64>, grid, dim3(256), 0, st, a); break;
-        case 128: hipLaunchKernelGGL(attn_causal_kernel<128>, grid, dim3(256), 0, st, a); break;
+        case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid_m, dim3(256), 0, st, a); break;
+        case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid_m, dim3(256), 0, st, a); break;
         case 256: hipLaunchKernelGGL(attn_causal_kernel<256>, grid, dim3(256), 0, st, a); break;
         default: return (int)hipErrorInvalidValue;
     }

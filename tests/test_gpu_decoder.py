@@ -359,6 +359,32 @@ def test_prefill_dense_path_is_tight(Ts):
         p.close()
 
 
+@pytest.mark.parametrize("Ts", [(150,), (40, 90)])
+def test_prefill_dense_path_head_dim_128_gqa(Ts):
+    """The MFMA prefill attention at head_dim 128 with 4 q heads per kv head
+    (the Mixtral grouping), T crossing several 64-query and 32-key blocks,
+    a second prefill over a past context: last logits against the oracle's
+    token-by-token run to relative L2 1e-5 (MoE block zeroed)."""
+    wl = synth.DecoderWorkload("hd128_gqa", synth.CONFIGS["tiny_renorm"], 1, 300, 8, 2, 128,
+                               1e6, False, 8, 8)
+    p = Pair(wl, seed=41, max_seq=200)
+    try:
+        _zero_experts(p)
+        toks = synth.prompt_tokens(wl, 14, sum(Ts))
+        off = 0
+        for T in Ts:
+            say(f"prefill head_dim 128 T={T} at position {off}")
+            g_tok, g_lg = p.dec.prefill(toks[off:off + T], return_logits=True)
+            for t in toks[off:off + T]:
+                w_tok, w_lg = p.orc.step(int(t))
+            off += T
+            rel = rel_l2(g_lg, w_lg)
+            assert rel < 1e-5, f"T={T}: rel L2 {rel:.2e}"
+            assert p.dec.position() == off
+    finally:
+        p.close()
+
+
 def test_prefill_whole_decoder_then_greedy():
     """The whole decoder (MoE prefill included): the prompt's last logits and
     the greedy steps after it against the oracle at the decoder bar."""

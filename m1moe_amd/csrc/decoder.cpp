@@ -379,6 +379,7 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
     at.scale = 1.0f / sqrtf((float)hd);
     at.rope_theta = dec->sh.rope_theta;
     at.eps = eps;
+    at.defer = 1;  // short contexts: o_proj merges the attention partials
     const uint64_t cache_layer = (uint64_t)dec->sh.max_seq * kvd;
     for (int l = 0; l < dec->L; ++l) {
         // input RMSNorm and q/k/v in one launch (InferenceEngine.swift:177-192); layer 0
@@ -412,6 +413,15 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
         // o_proj + residual (:227-233), with the sums of squares of its rows
         MvArgs o = mv_one(dec->wo + (size_t)l * h * qd, dec->attn, dec->res, dec->res2, h, qd);
         o.ssq_out = dec->ssq;
+        // its input from the attention partials when that launch deferred their merge
+        o.attn_part = dec->part;
+        o.attn_heads = at.num_heads;
+        o.attn_qh = at.qh;
+        o.attn_hd = hd;
+        o.attn_chunk = at.chunk;
+        o.attn_nch = (at.max_seq + at.chunk - 1) / at.chunk;
+        o.pos = dec->pos;
+        o.max_seq = at.max_seq;
         if ((rc = launched(launch_matvec_bf16(o, st), "o_proj"))) return rc;
         // the post-attention RMSNorm (:234-236) applied by the MoE kernel to its
         // input, the MoE block with the residual, its output the next residual

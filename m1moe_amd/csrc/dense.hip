@@ -148,6 +148,64 @@ __device__ __forceinline__ RowRef mv_row(const MvArgs& a, int row) {
 // (InferenceEngine.swift:482-488), then (norm_w) RMS-normalised
 // (Shaders.metal:96-134).  Workgroup 0 stores the un-normalised input to
 // x_copy.
+// Active chunks of a fused decode-attention launch at position p if it
+// leaves their merge to the next launch, else 0 (one chunk: the attention
+// launch writes the output itself; many: the merge stays there, where the
+// partials are read once per kv head rather than once per matvec workgroup).
+// The attention launch and the matvec that stages its output both decide
+// with this function.
+__device__ __forceinline__ int attn_defer_nact(int p, int max_seq, int chunk, int num_heads) {
+    const int seq = p < max_seq ? p + 1 : max_seq;
+    const int nact = (seq + chunk - 1) / chunk;
+    return (nact > 1 && nact <= kAttnDeferChunks && nact * num_heads <= kAttnDeferHeadChunks)
+               ? nact
+               : 0;
+}
+
+// x[h * hd + d] of the deferred attention merge: per head M = max_c m_c,
+// x = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M) (chunks in order),
+// over the partials [groups][chunks][qh][hd + 2] of the attention launch.
+// Each thread takes 4 consecutive elements (one head); all of its loads are
+// issued before they are used.
+__device__ float mv_stage_attn(const MvArgs& a, int nact, float* s_x) {
+    const int n4 = a.cols >> 2;
+    const int hs = a.attn_hd + 2;
+    const size_t cstride = (size_t)a.attn_qh * hs;
+    float ss = 0.f;
+    for (int i4 = threadIdx.x; i4 < n4; i4 += 256) {
+        const int i = 4 * i4, h = i / a.attn_hd, d = i - h * a.attn_hd;
+        const int g = h / a.attn_qh, hq = h - g * a.attn_qh;
+        const float* base = a.attn_part + (size_t)g * a.attn_nch * cstride + (size_t)hq * hs;
+        float m[kAttnDeferChunks], l[kAttnDeferChunks], v[kAttnDeferChunks][4];
+#pragma unroll
+        for (int c = 0; c < kAttnDeferChunks; ++c) {
+            if (c >= nact) break;  // (nact is uniform)
+            const float* pc = base + (size_t)c * cstride;
+            m[c] = pc[0];
+            l[c] = pc[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[c][e] = pc[2 + d + e];
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < kAttnDeferChunks; ++c)
+            if (c < nact) M = fmaxf(M, m[c]);
+        float L = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < kAttnDeferChunks; ++c) {
+            if (c >= nact) break;
+            const float f = expf(m[c] - M);
+            L = fmaf(l[c], f, L);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(v[c][e], f, acc[e]);
+        }
+        const float4 o = {acc[0] / L, acc[1] / L, acc[2] / L, acc[3] / L};
+        reinterpret_cast<float4*>(s_x)[i4] = o;
+        ss += o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+    }
+    return ss;
+}
+
 __device__ void mv_stage(const MvArgs& a, float* s_x, float* s_red) {
     const int n4 = a.cols >> 2;
     float ss = 0.f;
@@ -171,6 +229,10 @@ __device__ void mv_stage(const MvArgs& a, float* s_x, float* s_red) {
             reinterpret_cast<float4*>(s_x)[i] = v;
             ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
+    } else if (a.attn_part &&
+               attn_defer_nact(*a.pos, a.max_seq, a.attn_chunk, a.attn_heads) > 0) {
+        ss = mv_stage_attn(a, attn_defer_nact(*a.pos, a.max_seq, a.attn_chunk, a.attn_heads),
+                           s_x);
     } else {
         const float4* x4 = reinterpret_cast<const float4*>(a.x);
         for (int i = threadIdx.x; i < n4; i += 256) {
@@ -398,6 +460,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const bool has_new = a.fused && p < a.max_seq;  // row p comes from k_new / v_new
     const int c0 = c * a.chunk, c1 = min(c0 + a.chunk, seq);
     const int nact = min(nch, (seq + a.chunk - 1) / a.chunk);  // workgroups with positions
+    const bool defer = a.defer && attn_defer_nact(p, a.max_seq, a.chunk, a.num_heads) > 0;
     float* part = a.partial + ((size_t)g * nch + c) * QH * (HD + 2);
 
     if (c0 < seq) {
@@ -597,17 +660,27 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
             return;
         }
+        // (a deferred merge reads the partials in the next launch: plain stores)
         for (int t = tid; t < QH * HD; t += 256) {
             const int i = t / HD, d = t - i * HD;
-            st_coh(part + i * (HD + 2) + 2 + d,
-                   ((s_acc[0][i][d] + s_acc[1][i][d]) + s_acc[2][i][d]) + s_acc[3][i][d]);
+            const float v = ((s_acc[0][i][d] + s_acc[1][i][d]) + s_acc[2][i][d]) + s_acc[3][i][d];
+            if (defer)
+                part[i * (HD + 2) + 2 + d] = v;
+            else
+                st_coh(part + i * (HD + 2) + 2 + d, v);
         }
         if (tid < QH) {
-            st_coh(part + tid * (HD + 2), s_m[tid]);
-            st_coh(part + tid * (HD + 2) + 1, s_l[tid]);
+            if (defer) {
+                part[tid * (HD + 2)] = s_m[tid];
+                part[tid * (HD + 2) + 1] = s_l[tid];
+            } else {
+                st_coh(part + tid * (HD + 2), s_m[tid]);
+                st_coh(part + tid * (HD + 2) + 1, s_l[tid]);
+            }
         }
     }
     if (nact == 1) return;  // (workgroups past the sequence are not read by the merge)
+    if (defer) return;      // merged by the next launch (mv_stage_attn)
 
     // the last workgroup of the group merges the nact partials:
     // out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M)

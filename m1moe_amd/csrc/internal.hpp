@@ -185,6 +185,11 @@ struct MvArgs {
     int32_t* pos;                // device position (read for the embedding, advanced by argmax)
     int32_t max_seq;
     uint32_t* err;
+    // x given as decode-attention partials when the attention launch left
+    // their merge to this one (attention_defers): attn_part is that launch's
+    // partial buffer, the other fields its AttnArgs geometry; null: x given
+    const float* attn_part;
+    int32_t attn_heads, attn_qh, attn_hd, attn_chunk, attn_nch;
 };
 
 // Decode attention of one query position.  Workgroup (g, c): q heads
@@ -217,11 +222,17 @@ struct AttnArgs {
     int32_t num_heads, num_kv_heads, hpkv, head_dim, qh;
     int32_t chunk;               // positions per workgroup
     float scale, rope_theta, eps;
+    // fused only: for 2 .. kAttnDeferChunks active chunks and num_heads x chunks
+    // <= kAttnDeferHeadChunks, write the partials and leave their merge to the
+    // next launch (the o_proj matvec, which stages them as its input)
+    int32_t defer;
 };
 
 constexpr int kAttnChunk = 64;   // positions per attention workgroup
 constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
 constexpr int kAttnMaxChunks = 32;   // workgroups per kv head
+constexpr int kAttnDeferChunks = 8;        // deferred merge: at most this many chunks
+constexpr int kAttnDeferHeadChunks = 64;   // and heads x chunks (the partials staged per matvec workgroup)
 constexpr int kMvStageMax = 8192;   // largest staged (normalised / embedded) input, floats
 
 // ---- decoder prefill (prefill_dense.hip) ----

@@ -450,6 +450,28 @@ def test_decoder_olmoe_dims_two_layers():
         p.close()
 
 
+def test_decoder_olmoe_dims_past_one_attention_chunk():
+    """OLMoE widths, two layers: a 100-token batched prefill, then greedy
+    steps at positions 100..103.  Two 64-position attention chunks are
+    active, 16 heads x 2 chunks: the attention launch leaves the chunk merge
+    to the o_proj launch, which merges the partials as its input."""
+    p = Pair(synth.DECODERS["cfg1"], seed=2027, max_seq=130, num_layers=2)
+    try:
+        prompt = synth.prompt_tokens(p.wl, 17, 100)
+        say("olmoe-width prefill of 100, then 4 greedy steps")
+        tok, g_lg = p.dec.prefill(prompt, return_logits=True)
+        for t in prompt:
+            w_tok, w_lg = p.orc.step(int(t))
+        check_step(tok, g_lg, w_tok, w_lg, "prefill")
+        for i in range(4):
+            feed = w_tok
+            g_tok, g_lg = p.dec.forward(int(feed), return_logits=True)
+            w_tok, w_lg = p.orc.step(int(feed))
+            check_step(g_tok, g_lg, w_tok, w_lg, f"greedy {i} (position {100 + i})")
+    finally:
+        p.close()
+
+
 def test_decoder_mixtral_gqa_dims_one_layer():
     """Mixtral widths (h 4096, 32 q / 8 kv heads, vocab 32000, 8 experts
     top-2, intermediate 14336), one layer, three steps."""

@@ -493,6 +493,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         constexpr bool kTwo = HD <= 128;
         load_rows(c0, A);
         if (kTwo && c0 + kAttnChunk < c1) load_rows(c0 + kAttnChunk, B);
+        // keep both sub-chunks' loads here (the compiler may otherwise sink
+        // the second to its first use, a memory round trip later)
+        asm volatile("" ::: "memory");
 
         // q heads (and the new k when this workgroup holds row p): per-head
         // RMSNorm (InferenceEngine.swift:538-548), then RoPE (:521-536)

@@ -789,7 +789,10 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* x, int n, int
 
 __global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
 
-int mv_rpw(int rows) { return rows >= 8192 ? 4 : rows >= 2048 ? 2 : 1; }
+// Rows per wave: more rows per workgroup for taller matrices (each workgroup
+// stages, and may normalise, the whole input; lm_head of a 50k vocabulary
+// reads 1% faster at 8 than at 4).
+int mv_rpw(int rows) { return rows >= 32768 ? 8 : rows >= 8192 ? 4 : rows >= 2048 ? 2 : 1; }
 
 template <int RPW>
 int launch_mv(const MvArgs& a, hipStream_t st) {
@@ -836,6 +839,7 @@ int launch_matvec_bf16(const MvArgs& a, void* stream) {
     if ((a.embed || a.norm_w) && a.cols > kMvStageMax) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (mv_rpw(a.rows)) {
+        case 8: return launch_mv<8>(a, st);
         case 4: return launch_mv<4>(a, st);
         case 2: return launch_mv<2>(a, st);
         default: return launch_mv<1>(a, st);

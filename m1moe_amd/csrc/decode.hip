@@ -577,10 +577,10 @@ __device__ __forceinline__ uint32_t count_tiles(const FusedArgs& a, int c) {
 // with the loads, stall the next tile's wait.  With several tiles per
 // workgroup each tile is its own unit (down units are 2048 act rows, tiles
 // are 512 tiles apart); there the count has kCntParts parts, so each counter
-// takes a quarter of the adds and a consumer adds four.  Counts do not wait for the act
-// stores to be acknowledged (that wait costs µs under the expert stream): the
-// consumer checks the tag bits of what it reads and reads again until they
-// are current.
+// takes a quarter of the adds and a consumer adds four.  Counts do not wait
+// for the act stores to be acknowledged (that wait costs µs under the expert
+// stream): the consumer checks the tag bits of what it reads and reads again
+// until they are current.
 template <int CPL, int UG, int GSL>
 __device__ void gu_role(const FusedArgs& a, const Layout& L, int g, int wave, int lane,
                         const RouteLDS& r, const GUChunk<CPL> (&xc)[CPL], float inv,
@@ -843,10 +843,10 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     }
 }
 
-// The gate/up input of one workgroup (h <= CPL * 2048, CPL <= 2): x is read
-// from memory once per workgroup, normalised if asked (x * rms * w, rms from
-// the partial sums of squares), and staged in LDS; each wave then takes its
-// lanes' 32-element chunks from there.  (Every wave reading x itself put
+// The f32 gate/up input of one workgroup (h <= CPL * 2048, CPL <= 2): x is
+// read from memory once per workgroup, normalised if asked (x * rms * w, rms
+// from the partial sums of squares), and staged in LDS; each wave then takes
+// its lanes' 32-element chunks from there.  (Every wave reading x itself put
 // 4x the bytes through L2 at the start of the launch.)  Chunks are padded to
 // 36 floats against LDS bank conflicts.
 template <int CPL>
@@ -861,13 +861,7 @@ __device__ __forceinline__ void stage_x(const FusedArgs& a, int wave, int lane, 
     for (int q = 0; q < kG; ++q) {
         const int e = 4 * ((int)threadIdx.x + kThreads * q);
         const int ec = e < a.h ? e : 0;
-        if (a.x_bf16) {
-            const uint2 b = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.x) + ec);
-            xv[q] = float4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u),
-                           __uint_as_float(b.y << 16), __uint_as_float(b.y & 0xffff0000u)};
-        } else {
-            xv[q] = *reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + ec);
-        }
+        xv[q] = *reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + ec);
         if (a.x_norm_w) nw[q] = *reinterpret_cast<const uint2*>(a.x_norm_w + ec);
     }
     if (a.x_norm_w && wave == 0) {

@@ -379,7 +379,9 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
     at.scale = 1.0f / sqrtf((float)hd);
     at.rope_theta = dec->sh.rope_theta;
     at.eps = eps;
-    at.defer = 1;  // short contexts: o_proj merges the attention partials
+    // short contexts: o_proj merges the attention partials while staging its
+    // input (only a staged input can: q widths up to kMvStageMax)
+    at.defer = qd <= kMvStageMax ? 1 : 0;
     const uint64_t cache_layer = (uint64_t)dec->sh.max_seq * kvd;
     for (int l = 0; l < dec->L; ++l) {
         // input RMSNorm and q/k/v in one launch (InferenceEngine.swift:177-192); layer 0
@@ -414,7 +416,7 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
         MvArgs o = mv_one(dec->wo + (size_t)l * h * qd, dec->attn, dec->res, dec->res2, h, qd);
         o.ssq_out = dec->ssq;
         // its input from the attention partials when that launch deferred their merge
-        o.attn_part = dec->part;
+        o.attn_part = at.defer ? dec->part : nullptr;
         o.attn_heads = at.num_heads;
         o.attn_qh = at.qh;
         o.attn_hd = hd;

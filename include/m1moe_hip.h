@@ -343,9 +343,11 @@ int32_t m1moe_dec_step_seq(m1moe_dec_t dec, int32_t* d_seq, int32_t n_prompt,
  * activations make this path agree with T m1moe_dec_step calls to ~1e-3).
  * Their K/V rows enter the cache, the position advances by T, d_token_out
  * receives the greedy token after the last one and d_logits (nullable) its
- * logits.  1 <= T <= min(max_seq, 4096); positions past max_seq set the
- * device error flag.  The first call with a larger T than any before grows
- * the scratch (make it before capturing a graph). */
+ * logits.  1 <= T <= max_seq (prompts longer than 4096 tokens go through in
+ * pieces of 4096, each from the position the previous one reached);
+ * positions past max_seq set the device error flag.  The first call with a
+ * larger piece than any before grows the scratch (make it before capturing a
+ * graph). */
 int32_t m1moe_dec_prefill(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
                           int32_t* d_token_out, float* d_logits);
 /* The current position (waits for the context stream). */

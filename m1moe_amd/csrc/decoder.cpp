@@ -472,6 +472,13 @@ int32_t m1moe_dec_step(m1moe_dec_t dec, const int32_t* d_token_in, int32_t* d_to
     return dec_step(dec, d_token_in, d_token_out, 0, 0, d_logits);
 }
 
+namespace {
+constexpr int32_t kPrefillPiece = 4096;  // tokens per batched pass (the MoE prefill's cap)
+
+int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
+                          int32_t* d_token_out, float* d_logits);
+}  // namespace
+
 int32_t m1moe_dec_prefill(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T, int32_t* d_token_out,
                           float* d_logits) {
     int32_t rc;
@@ -479,9 +486,24 @@ int32_t m1moe_dec_prefill(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T, i
     if (!aligned_i32(d_tokens) || !aligned_i32(d_token_out))
         return fail(M1MOE_ERR_INVALID, "d_tokens / d_token_out must be 4-byte aligned device pointers");
     if ((rc = check_dev_ptr(d_logits, "d_logits", true))) return rc;
-    if (T < 1 || T > dec->sh.max_seq || T > 4096)
-        return fail(M1MOE_ERR_INVALID, "T=%d must be in [1, min(max_seq=%d, 4096)]", T, dec->sh.max_seq);
+    if (T < 1 || T > dec->sh.max_seq)
+        return fail(M1MOE_ERR_INVALID, "T=%d must be in [1, max_seq=%d]", T, dec->sh.max_seq);
     if ((rc = check_loaded(dec))) return rc;
+    // longer prompts in pieces: each continues from the device position the
+    // previous one advanced; the last one gives the greedy token and logits
+    for (int32_t off = 0; off < T; off += kPrefillPiece) {
+        const int32_t n = T - off < kPrefillPiece ? T - off : kPrefillPiece;
+        const bool last = off + n == T;
+        if ((rc = dec_prefill_piece(dec, d_tokens + off, n, d_token_out, last ? d_logits : nullptr)))
+            return rc;
+    }
+    return M1MOE_OK;
+}
+
+namespace {
+int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
+                          int32_t* d_token_out, float* d_logits) {
+    int32_t rc;
     m1moe_ctx_t ctx = dec->moe;
     if ((rc = set_device(ctx))) return rc;
     const int32_t h = dec->h, qd = dec->qd, kvd = dec->kvd, hd = dec->sh.head_dim;
@@ -591,6 +613,7 @@ int32_t m1moe_dec_prefill(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T, i
     f.err = ctx->err;
     return launched(launch_matvec_bf16(f, st), "prefill lm_head");
 }
+}  // namespace
 
 int32_t m1moe_dec_step_seq(m1moe_dec_t dec, int32_t* d_seq, int32_t n_prompt, int32_t seq_cap,
                            float* d_logits) {

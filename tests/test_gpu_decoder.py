@@ -359,6 +359,26 @@ def test_prefill_dense_path_is_tight(Ts):
         p.close()
 
 
+def test_prefill_longer_than_one_piece():
+    """A 4100-token prompt goes through m1moe_dec_prefill in two pieces (4096
+    + 4): last logits against the oracle's token-by-token run to 1e-5 (MoE
+    block zeroed), and the position reaches 4100."""
+    wl = synth.DECODERS["tiny_dec"]
+    p = Pair(wl, seed=43, max_seq=4110)
+    try:
+        _zero_experts(p)
+        toks = synth.prompt_tokens(wl, 19, 4100)
+        say("prefill of 4100 tokens (two pieces)")
+        g_tok, g_lg = p.dec.prefill(toks, return_logits=True)
+        for t in toks:
+            w_tok, w_lg = p.orc.step(int(t))
+        rel = rel_l2(g_lg, w_lg)
+        assert rel < 1e-5, f"rel L2 {rel:.2e}"
+        assert p.dec.position() == 4100
+    finally:
+        p.close()
+
+
 @pytest.mark.parametrize("Ts", [(150,), (40, 90)])
 def test_prefill_dense_path_head_dim_128_gqa(Ts):
     """The MFMA prefill attention at head_dim 128 with 4 q heads per kv head

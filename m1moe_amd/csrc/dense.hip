@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
 // and sum (the softmax of attnSoftmax, Shaders.metal:245-289, in pieces).
 // Lanes take 8 dims of one position each (HD/8 lanes per position), so every
 // K or V row is one coalesced read shared by the QH heads.
-template <int HD, int QH>
+template <int HD, int QH, bool TWO>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     constexpr int LP = HD / 8;                 // lanes per position
     constexpr int PPI = 64 / LP;               // positions per wave and iteration
@@ -489,8 +489,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 R.v[it][4] = v1.x, R.v[it][5] = v1.y, R.v[it][6] = v1.z, R.v[it][7] = v1.w;
             }
         };
-        // (head_dim 256 has the registers for one sub-chunk only)
-        constexpr bool kTwo = HD <= 128;
+        // (TWO: chunks of several sub-chunks; head_dim 256 has the registers
+        // for one sub-chunk only)
+        constexpr bool kTwo = TWO && HD <= 128;
         load_rows(c0, A);
         if (kTwo && c0 + kAttnChunk < c1) load_rows(c0 + kAttnChunk, B);
         // keep both sub-chunks' loads here (the compiler may otherwise sink
@@ -695,7 +696,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // together: one memory round trip for up to kMB chunks.
     static_assert(kAttnMaxChunks <= 64, "the merge takes one chunk per lane");
     constexpr int OPT = (QH * HD + 255) / 256;  // outputs per thread
-    constexpr int kMB = OPT == 1 ? 32 : OPT == 2 ? 28 : OPT <= 4 ? 12 : 6;
+    constexpr int kMB = OPT <= 2 ? 34 : OPT <= 4 ? 12 : 6;
     const bool has_st = tid < QH * nact;  // QH * nact <= 256
     const int st_i = has_st ? tid / nact : 0, st_c = has_st ? tid - st_i * nact : 0;
     float st_m = 0.f, st_l = 0.f;
@@ -806,11 +807,18 @@ int launch_mv(const MvArgs& a, hipStream_t st) {
 
 template <int HD>
 int launch_attn_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
-    switch (a.qh) {
-        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, st, a); break;
+    // one-sub-chunk workgroups keep no second set of K/V registers, so two of
+    // them fit on a CU (more than 256 workgroups then run at once)
+    const bool two = a.chunk > kAttnChunk;
+    switch (a.qh * 2 + (two ? 1 : 0)) {
+        case 2: hipLaunchKernelGGL((attn_kernel<HD, 1, false>), grid, dim3(256), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((attn_kernel<HD, 1, true>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((attn_kernel<HD, 2, false>), grid, dim3(256), 0, st, a); break;
+        case 5: hipLaunchKernelGGL((attn_kernel<HD, 2, true>), grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((attn_kernel<HD, 4, false>), grid, dim3(256), 0, st, a); break;
+        case 9: hipLaunchKernelGGL((attn_kernel<HD, 4, true>), grid, dim3(256), 0, st, a); break;
+        case 16: hipLaunchKernelGGL((attn_kernel<HD, 8, false>), grid, dim3(256), 0, st, a); break;
+        case 17: hipLaunchKernelGGL((attn_kernel<HD, 8, true>), grid, dim3(256), 0, st, a); break;
         default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();

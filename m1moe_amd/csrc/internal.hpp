@@ -230,7 +230,7 @@ struct AttnArgs {
 
 constexpr int kAttnChunk = 64;   // positions per attention workgroup
 constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
-constexpr int kAttnMaxChunks = 32;   // workgroups per kv head
+constexpr int kAttnMaxChunks = 64;   // workgroups per kv head
 constexpr int kAttnDeferChunks = 8;        // deferred merge: at most this many chunks
 constexpr int kAttnDeferHeadChunks = 64;   // and heads x chunks (the partials staged per matvec workgroup)
 constexpr int kMvStageMax = 8192;   // largest staged (normalised / embedded) input, floats

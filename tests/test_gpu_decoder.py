@@ -74,8 +74,13 @@ def test_matvec_bf16(ops_ctx, rows, cols, with_res):
 
 @pytest.mark.parametrize("nh,nkv,hd,sl", [(16, 16, 128, 1), (4, 2, 64, 255), (4, 2, 64, 256),
                                            (4, 2, 64, 257), (32, 8, 128, 1000), (2, 1, 256, 700),
-                                           (16, 16, 128, 4096)])
+                                           (16, 16, 128, 4096), (32, 8, 128, 2112),
+                                           (8, 2, 128, 5000), (4, 4, 64, 8300)])
 def test_attention_decode(ops_ctx, nh, nkv, hd, sl):
+    """The attention building block against the oracle: one chunk, 64-position
+    chunks up to 64 per kv head (4096, and the Mixtral grouping at 2112),
+    multi-sub-chunk chunks past 4096 positions (two K/V register sets),
+    head_dim 64 / 128 / 256."""
     ctx, ops = ops_ctx
     kvd = nkv * hd
     q = RNG.normal(0, 1, nh * hd).astype(np.float32)

@@ -177,10 +177,10 @@ __device__ __forceinline__ f16x8 dequant_word(uint32_t w, f16x2 s2, f16x2 b2) {
 // NMAT = 2: gate and up (K = h, rows = I), B = xq rows of the pairs' tokens,
 //           epilogue act = silu(g) * u.
 // NMAT = 1: down (K = I, rows = h), B = act rows, epilogue y.
-// KB = k per block (64 or 128; K % KB == 0), GSL = log2(group_size / 32).
+// KB = k per block (64, 128 or 256; K % KB == 0), GSL = log2(group_size / 32).
 // Lane (r = row in the wave's 16, kq = lane / 16) owns the KB/4 contiguous
 // columns kq*KB/4.. of its row in each block (KB/32 packed words, one
-// scale group since KB/4 <= 32 <= group size); MFMA k-step s uses word s.
+// scale group since KB/4 <= group size); MFMA k-step s uses word s.
 // Blocks are pipelined two deep: the loads of block kb+2 are issued while
 // block kb is multiplied; B tiles go through a double-buffered LDS tile.
 template <int NMAT, int KB, int NW>
@@ -258,10 +258,13 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
             const uint32_t* pw = wrow[m] + (size_t)kb * (KB / 8);
-            if (W == 4) {
-                const uint4 q = *reinterpret_cast<const uint4*>(pw);
-                st.aw[m][0] = q.x; st.aw[m][W > 1 ? 1 : 0] = q.y;
-                st.aw[m][W > 2 ? 2 : 0] = q.z; st.aw[m][W > 3 ? 3 : 0] = q.w;
+            if constexpr (W % 4 == 0) {
+#pragma unroll
+                for (int v = 0; v < W / 4; ++v) {
+                    const uint4 q = *reinterpret_cast<const uint4*>(pw + 4 * v);
+                    st.aw[m][4 * v] = q.x; st.aw[m][4 * v + 1] = q.y;
+                    st.aw[m][4 * v + 2] = q.z; st.aw[m][4 * v + 3] = q.w;
+                }
             } else {
                 const uint2 q = *reinterpret_cast<const uint2*>(pw);
                 st.aw[m][0] = q.x; st.aw[m][W > 1 ? 1 : 0] = q.y;
@@ -391,6 +394,18 @@ void launch_gemm_nw(const PrefillArgs& a, hipStream_t st, int groups8, int rows)
     const int K = NMAT == 2 ? a.h : a.I;
     const int m_tiles = rows / (16 * NW);
     const dim3 grid((unsigned)(8 * groups8 * m_tiles));
+    // Eight-wave gate/up (two matrices: two waves per SIMD at any k-block)
+    // streams 256-wide k-blocks, twice the weight bytes in flight per wave at
+    // the same occupancy.  The down GEMM stays at 128: at 256 its registers
+    // would leave room for one workgroup per CU instead of two.  A lane's 64
+    // columns then still sit in one scale group (group size >= 64).
+    if constexpr (NMAT == 2 && NW == 8 && GSL >= 1) {
+        if (K % 256 == 0) {
+            hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 256, GSL, NW>), grid, dim3(64 * NW), 0, st,
+                               a, m_tiles);
+            return;
+        }
+    }
     if (K % 128 == 0)
         hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 128, GSL, NW>), grid, dim3(64 * NW), 0, st, a,
                            m_tiles);

@@ -105,6 +105,22 @@ def test_prefill_cfg2_mixtral_shape():
         c.close()
 
 
+@pytest.mark.parametrize("kw", [
+    dict(hidden=1024, num_experts=16, top_k=4, intermediate=512, group_size=128),
+    dict(hidden=1152, num_experts=8, top_k=2, intermediate=640, group_size=64),
+])
+def test_prefill_group_and_block_shapes(kw):
+    # gate/up on 256-wide k-blocks at group size 128 (two lanes' 64 columns
+    # share a scale group); h % 256 != 0 (gate/up back on 128-wide blocks)
+    synth.CONFIGS["_pf_shape"] = synth.Workload("_pf_shape", dict(kw, norm_topk_prob=False))
+    c = make_case("_pf_shape", seed=43)
+    try:
+        _check(c, 100, *_run_prefill(c, 100))
+    finally:
+        c.close()
+        del synth.CONFIGS["_pf_shape"]
+
+
 def test_prefill_is_deterministic(cfg3):
     a = _run_prefill(cfg3, 300, stream=4)[0]
     b = _run_prefill(cfg3, 300, stream=4)[0]

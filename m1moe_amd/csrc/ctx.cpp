@@ -118,10 +118,13 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
     return launched(m1moe::launch_router_topk(r, ctx->stream), "router_topk");
 }
 
-// Grows the prefill scratch to at least T tokens (the whole cap at once, so a
-// graph captured after one call at the largest T never allocates).
+// Grows the prefill scratch to exactly T tokens when a call needs more than
+// it holds.  Growth frees the old buffers, so it is refused during stream
+// capture, and a graph captured before a call with a larger T must be
+// captured again.
 int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
     if (T <= ctx->pf_cap) return M1MOE_OK;
+    if (int32_t rc = m1moe::refuse_growth_in_capture(ctx->stream, "the prefill scratch")) return rc;
     const m1moe::Geom& g = ctx->g;
     void** bufs[] = {(void**)&ctx->pf_xq,   (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
                      (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,

@@ -82,6 +82,19 @@ inline int32_t device_alloc(void** p, uint64_t bytes, const char* what) {
     return M1MOE_OK;
 }
 
+// Scratch that must grow is reallocated (synchronise, free, allocate): not
+// possible while the stream is being captured into a graph, and a graph
+// captured earlier would point at the freed buffers.  Growth under capture is
+// refused; the caller grows it first with one eager call at the largest size.
+inline int32_t refuse_growth_in_capture(hipStream_t stream, const char* what) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(M1MOE_ERR_INVALID, "%s must grow, which cannot happen during stream capture: "
+                    "make one eager call at the largest size before capturing", what);
+    return M1MOE_OK;
+}
+
 inline int32_t check_ctx(m1moe_ctx_t ctx) {
     if (!ctx) return fail(M1MOE_ERR_INVALID, "null context");
     return M1MOE_OK;

@@ -24,6 +24,8 @@ int32_t check_f32_vec(const void* p, const char* what) { return check_dev_ptr(p,
 constexpr int kAttnCounters = 1024;  // >= num_heads (num_heads * 64 <= 65536)
 
 int32_t ensure_attn_scratch(m1moe_ctx_t ctx, uint64_t floats) {
+    if (!ctx->attn_cnt || floats > ctx->attn_part_floats)
+        if (int32_t rc = refuse_growth_in_capture(ctx->stream, "the attention scratch")) return rc;
     if (!ctx->attn_cnt) {
         int32_t rc = device_alloc((void**)&ctx->attn_cnt, kAttnCounters * 4, "attention counters");
         if (rc) return rc;
@@ -46,6 +48,14 @@ int32_t check_attn_dims(int32_t nh, int32_t nkv, int32_t hd) {
     if (nh <= 0 || nkv <= 0 || nh % nkv)
         return fail(M1MOE_ERR_INVALID, "num_heads %d must be a positive multiple of num_kv_heads %d",
                     nh, nkv);
+    // the attention launch keeps one counter per group of q heads (at most
+    // num_heads groups), kAttnCounters of them; with head_dim >= 64 this
+    // bound keeps num_heads <= 1024
+    if ((int64_t)nh * hd > 65536)
+        return fail(M1MOE_ERR_INVALID, "num_heads * head_dim = %lld exceeds 65536",
+                    (long long)nh * hd);
+    if (nh > kAttnCounters)
+        return fail(M1MOE_ERR_INVALID, "num_heads %d exceeds %d", nh, kAttnCounters);
     return M1MOE_OK;
 }
 
@@ -233,8 +243,6 @@ int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* s, m1moe_dec_t*
         return fail(M1MOE_ERR_INVALID, "max_seq %d out of range [1, 65536]", s->max_seq);
     if (!(s->rope_theta > 0.f) || !(s->rms_eps >= 0.f))
         return fail(M1MOE_ERR_INVALID, "rope_theta must be > 0 and rms_eps >= 0");
-    if (s->num_heads * s->head_dim > 65536)
-        return fail(M1MOE_ERR_INVALID, "num_heads * head_dim exceeds 65536");
     if (moe->g.h > kMvStageMax)
         return fail(M1MOE_ERR_INVALID, "hidden %d exceeds the decoder's %d (normalised inputs are "
                     "staged in LDS)", moe->g.h, kMvStageMax);
@@ -509,6 +517,7 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
     const int32_t h = dec->h, qd = dec->qd, kvd = dec->kvd, hd = dec->sh.head_dim;
     const int32_t N = qd + 2 * kvd;
     if (T > dec->pf_cap) {
+        if ((rc = refuse_growth_in_capture(ctx->stream, "the decoder prefill scratch"))) return rc;
         HIP_TRY(hipStreamSynchronize(ctx->stream));
         for (float** b : {&dec->pf_res, &dec->pf_res2, &dec->pf_xn, &dec->pf_qkv, &dec->pf_attn}) {
             if (*b) (void)hipFree(*b);

@@ -697,12 +697,24 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     static_assert(kAttnMaxChunks <= 64, "the merge takes one chunk per lane");
     constexpr int OPT = (QH * HD + 255) / 256;  // outputs per thread
     constexpr int kMB = OPT <= 2 ? 34 : OPT <= 4 ? 12 : 6;
-    const bool has_st = tid < QH * nact;  // QH * nact <= 256
-    const int st_i = has_st ? tid / nact : 0, st_c = has_st ? tid - st_i * nact : 0;
-    float st_m = 0.f, st_l = 0.f;
-    if (has_st) {
-        st_m = ld_coh(base + st_c * cstride + st_i * (HD + 2));
-        st_l = ld_coh(base + st_c * cstride + st_i * (HD + 2) + 1);
+    // (head, chunk) statistics: QH * nact <= QH * kAttnMaxChunks entries,
+    // entry tid + 256 s for s < kSt
+    constexpr int kSt = (QH * kAttnMaxChunks + 255) / 256;
+    bool has_st[kSt];
+    int st_i[kSt], st_c[kSt];
+    float st_m[kSt], st_l[kSt];
+#pragma unroll
+    for (int s = 0; s < kSt; ++s) {
+        const int e = tid + 256 * s;
+        has_st[s] = e < QH * nact;
+        st_i[s] = has_st[s] ? e / nact : 0;
+        st_c[s] = has_st[s] ? e - st_i[s] * nact : 0;
+        st_m[s] = 0.f;
+        st_l[s] = 0.f;
+        if (has_st[s]) {
+            st_m[s] = ld_coh(base + st_c[s] * cstride + st_i[s] * (HD + 2));
+            st_l[s] = ld_coh(base + st_c[s] * cstride + st_i[s] * (HD + 2) + 1);
+        }
     }
     float acc[OPT];
 #pragma unroll
@@ -722,9 +734,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         if (cb == 0) {
             // per head: M = max_c m_c, factors f_c = e^(m_c - M) (in place of
             // m_c), L = sum_c l_c f_c -- once per (head, chunk), not per output
-            if (has_st) {
-                s_st[0][st_i][st_c] = st_m;
-                s_st[1][st_i][st_c] = st_l;
+#pragma unroll
+            for (int s = 0; s < kSt; ++s) {
+                if (has_st[s]) {
+                    s_st[0][st_i[s]][st_c[s]] = st_m[s];
+                    s_st[1][st_i[s]][st_c[s]] = st_l[s];
+                }
             }
             __syncthreads();
             for (int i = wave; i < QH; i += 4) {  // lane = chunk (nact <= 64)

@@ -161,7 +161,9 @@ int32_t parse_manifest(const std::string& text, m1moe_store* st) {
                     return fail(M1MOE_ERR_INVALID, "manifest: %s", j.err.c_str());
                 if (key == "offset") {
                     double d;
-                    if (!j.number(d) || d < 0)
+                    // (compared as a double before the cast: a cast of a value
+                    // >= 2^64 is undefined)
+                    if (!j.number(d) || !(d >= 0) || d > (double)st->size || d != (double)(uint64_t)d)
                         return fail(M1MOE_ERR_INVALID, "manifest: bad offset of %s", name.c_str());
                     info.offset = (uint64_t)d;
                     has_off = true;
@@ -172,7 +174,7 @@ int32_t parse_manifest(const std::string& text, m1moe_store* st) {
                     if (!j.peek(']')) {
                         for (;;) {
                             double d;
-                            if (!j.number(d) || d < 0 || info.ndim >= 4)
+                            if (!j.number(d) || !(d >= 0) || d > 9.0e15 || info.ndim >= 4)
                                 return fail(M1MOE_ERR_INVALID, "manifest: bad shape of %s", name.c_str());
                             info.shape[info.ndim++] = (int64_t)d;
                             if (j.peek(',')) {
@@ -204,10 +206,17 @@ int32_t parse_manifest(const std::string& text, m1moe_store* st) {
         if (!j.expect('}')) return fail(M1MOE_ERR_INVALID, "manifest: %s", j.err.c_str());
         if (!has_off || !has_shape || !has_dtype)
             return fail(M1MOE_ERR_INVALID, "manifest: %s lacks offset, shape or dtype", name.c_str());
+        // element count, refused once it passes the file size (no overflow:
+        // each factor is < 2^53 and the running product stays <= size)
         uint64_t n = 1;
-        for (int d = 0; d < info.ndim; ++d) n *= (uint64_t)info.shape[d];
-        info.bytes = n * (info.dtype == M1MOE_DT_BF16 ? 2 : 4);  // TensorInfo.byteWidth, :20-27
-        if (info.offset + info.bytes > st->size)
+        bool too_big = false;
+        for (int d = 0; d < info.ndim; ++d) {
+            const uint64_t f = (uint64_t)info.shape[d];
+            if (f != 0 && n > st->size / f) too_big = true;
+            else n *= f;
+        }
+        info.bytes = too_big ? UINT64_MAX : n * (info.dtype == M1MOE_DT_BF16 ? 2 : 4);  // TensorInfo.byteWidth, :20-27
+        if (too_big || info.bytes > st->size || info.offset > st->size - info.bytes)
             return fail(M1MOE_ERR_INVALID, "manifest: %s [%llu, +%llu) lies past the end of the %llu-byte file",
                         name.c_str(), (unsigned long long)info.offset, (unsigned long long)info.bytes,
                         (unsigned long long)st->size);

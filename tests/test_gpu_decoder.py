@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import m1moe_amd as m
-from m1moe_amd import _lib, synth
+from m1moe_amd import M1MoEError, _lib, synth
 from m1moe_amd.decoder import Decoder, DenseOps
 from oracle import oracle as orc
 
@@ -75,6 +75,7 @@ def test_matvec_bf16(ops_ctx, rows, cols, with_res):
 @pytest.mark.parametrize("nh,nkv,hd,sl", [(16, 16, 128, 1), (4, 2, 64, 255), (4, 2, 64, 256),
                                            (4, 2, 64, 257), (32, 8, 128, 1000), (2, 1, 256, 700),
                                            (16, 16, 128, 4096), (32, 8, 128, 2112),
+                                           (32, 4, 128, 2112), (16, 2, 64, 4096),
                                            (8, 2, 128, 5000), (4, 4, 64, 8300)])
 def test_attention_decode(ops_ctx, nh, nkv, hd, sl):
     """The attention building block against the oracle: one chunk, 64-position
@@ -92,6 +93,18 @@ def test_attention_decode(ops_ctx, nh, nkv, hd, sl):
     ctx.sync()
     want = orc.attention(q, kc, vc, nh, nkv, hd, sl)
     assert rel_l2(dout.download(np.float32), want) < 1e-5
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(2048, 1, 64), (1024, 8, 128)])
+def test_attention_decode_rejects_too_many_heads(ops_ctx, nh, nkv, hd):
+    """num_heads * head_dim > 65536 is refused before any launch (the launch
+    keeps one counter per q-head group, 1024 of them)."""
+    ctx, ops = ops_ctx
+    buf = ctx.alloc(1 << 16)
+    with pytest.raises(M1MoEError) as ei:
+        ops.attention_decode(buf, buf, buf, buf, nh, nkv, hd, 100)
+    assert ei.value.code == _lib.M1MOE_ERR_INVALID
+    assert "exceeds 65536" in str(ei.value)
 
 
 @pytest.mark.parametrize("case", ["random", "ties", "nan0", "nan_mid", "neg_inf", "one"])

@@ -83,6 +83,11 @@ m1moe::FusedArgs fused_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32
     a.act = ctx->act;
     a.gu_cnt = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_gu_cnt);
     a.seen = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_seen);
+    a.cu_seen = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_cu_seen);
+    a.cu_cnt = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_cu_cnt);
+    a.cu_part = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_cu_part);
+    a.dec_base = ctx->dec ? ctx->dec + (uint64_t)layer * g.E * ctx->dec_bytes : nullptr;
+    a.dec_bytes = ctx->dec_bytes;
     a.err = ctx->err;
     a.h = g.h;
     a.E = g.E;
@@ -93,6 +98,31 @@ m1moe::FusedArgs fused_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32
     a.x_bf16 = (x_dtype == M1MOE_BF16);
     a.spin_limit = kSpinLimit;
     return a;
+}
+
+// Rebuilds a layer's repacked copy when its canonical blocks may have been
+// written through m1moe_expert_block since it was made (enqueued before the
+// decode on the context stream; refused while the stream is captured).
+int32_t refresh_decode_copy(m1moe_ctx_t ctx, int32_t layer) {
+    if (!ctx->decode_cu || !ctx->dec_stale[layer]) return M1MOE_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(M1MOE_ERR_INVALID,
+                    "layer %d's expert blocks were handed out for writing since its repacked "
+                    "copy was made; decode it once outside stream capture first", layer);
+    const uint64_t lb = (uint64_t)ctx->g.E * ctx->g.expert_bytes;
+    HIP_TRY((hipError_t)m1moe::launch_decode_copy(
+        ctx->arena + (uint64_t)layer * lb, ctx->g.expert_bytes,
+        ctx->dec + (uint64_t)layer * ctx->g.E * ctx->dec_bytes, ctx->g.E, ctx->g.I, ctx->g.gs,
+        ctx->stream));
+    ctx->dec_stale[layer] = false;
+    return M1MOE_OK;
+}
+
+int enqueue_decode(m1moe_ctx_t ctx, const m1moe::FusedArgs& a) {
+    return ctx->decode_cu ? m1moe::launch_moe_decode_cu(a, ctx->stream)
+                          : m1moe::launch_moe_decode(a, ctx->stream);
 }
 
 int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
@@ -216,7 +246,7 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (void* p : ctx->allocs) (void)hipFree(p);
-    void* owned[] = {ctx->arena,   ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
+    void* owned[] = {ctx->arena,   ctx->dec,      ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
                      ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
                      ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part, ctx->attn_cnt};
@@ -267,7 +297,25 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         c->sync_gu_cnt = (uint64_t)m1moe::kLogitRep * m1moe::kRepStride * 8;
         c->sync_seen =
             c->sync_gu_cnt + (uint64_t)m1moe::kNRep * fa.n_cnt * m1moe::kCntStride * 4;
-        c->sync_bytes = c->sync_seen + ((uint64_t)grid * 4 + 255) / 256 * 256;
+        c->sync_cu_seen = c->sync_seen + ((uint64_t)grid * 4 + 255) / 256 * 256;
+        c->sync_cu_cnt = c->sync_cu_seen + (uint64_t)m1moe::kCuWorkgroups * 4;
+        c->sync_cu_part =
+            c->sync_cu_cnt + (uint64_t)m1moe::kCuRep * m1moe::kCuParts * m1moe::kCntStride * 4;
+        c->sync_bytes = c->sync_cu_part +
+            (uint64_t)m1moe::kCuWorkgroups * m1moe::kCuWorkgroups * 8 * 4;
+    }
+    {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+            return cleanup(fail(M1MOE_ERR_HIP, "hipDeviceGetAttribute(multiprocessor count)"));
+        c->decode_cu = cus >= m1moe::kCuWorkgroups &&
+                       m1moe::decode_cu_fits(g.h, g.E, g.K, g.I, g.gs);
+        c->dec_stale.assign(s->num_layers, false);
+        if (c->decode_cu) {
+            c->dec_bytes = m1moe::decode_copy_bytes(g.I, g.gs);
+            if ((rc = device_alloc((void**)&c->dec, L * E * c->dec_bytes, "repacked expert copy")))
+                return cleanup(rc);
+        }
     }
     if ((rc = device_alloc((void**)&c->arena, L * E * g.expert_bytes, "expert arena")) ||
         (rc = device_alloc((void**)&c->routers, L * E * g.h * 2, "routers")) ||
@@ -304,6 +352,13 @@ int32_t m1moe_upload_layer_experts(m1moe_ctx_t ctx, int32_t layer, const void* h
     if ((rc = set_device(ctx))) return rc;
     HIP_TRY(hipMemcpyAsync(ctx->arena + (uint64_t)layer * want, host_image, bytes,
                            hipMemcpyHostToDevice, ctx->stream));
+    if (ctx->decode_cu) {
+        HIP_TRY((hipError_t)m1moe::launch_decode_copy(
+            ctx->arena + (uint64_t)layer * want, ctx->g.expert_bytes,
+            ctx->dec + (uint64_t)layer * ctx->g.E * ctx->dec_bytes, ctx->g.E, ctx->g.I, ctx->g.gs,
+            ctx->stream));
+        ctx->dec_stale[layer] = false;
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     ctx->layer_loaded[layer] = true;
     return M1MOE_OK;
@@ -351,6 +406,7 @@ int32_t m1moe_expert_block(m1moe_ctx_t ctx, int32_t layer, int32_t expert, void*
         return fail(M1MOE_ERR_INVALID, "expert %d out of range [0, %d)", expert, ctx->g.E);
     if (!dev_ptr) return fail(M1MOE_ERR_INVALID, "null output");
     *dev_ptr = ctx->arena + ((uint64_t)layer * ctx->g.E + (uint64_t)expert) * ctx->g.expert_bytes;
+    if (ctx->decode_cu) ctx->dec_stale[layer] = true;  // the caller may write the block
     return M1MOE_OK;
 }
 
@@ -559,11 +615,11 @@ int32_t m1moe_moe_decode_given_topk(m1moe_ctx_t ctx, int32_t layer, const void* 
         (rc = check_dev_ptr(d_out, "d_out", false)))
         return rc;
     if ((rc = require_loaded(ctx, layer, false))) return rc;
-    if ((rc = set_device(ctx))) return rc;
+    if ((rc = set_device(ctx)) || (rc = refresh_decode_copy(ctx, layer))) return rc;
     m1moe::FusedArgs a = fused_args(ctx, layer, d_x, x_dtype, d_residual, d_out);
     a.given_idx = d_topk_idx;
     a.given_w = d_topk_w;
-    return launched(m1moe::launch_moe_decode(a, ctx->stream), "moe_decode (given routing)");
+    return launched(enqueue_decode(ctx, a), "moe_decode (given routing)");
 }
 
 int32_t m1moe_moe_decode(m1moe_ctx_t ctx, int32_t layer, const void* d_x, int32_t x_dtype,
@@ -578,11 +634,11 @@ int32_t m1moe_moe_decode(m1moe_ctx_t ctx, int32_t layer, const void* d_x, int32_
         (rc = check_dev_ptr(d_topk_w, "d_topk_w", true)))
         return rc;
     if ((rc = require_loaded(ctx, layer, true))) return rc;
-    if ((rc = set_device(ctx))) return rc;
+    if ((rc = set_device(ctx)) || (rc = refresh_decode_copy(ctx, layer))) return rc;
     m1moe::FusedArgs a = fused_args(ctx, layer, d_x, x_dtype, d_residual, d_out);
     a.user_idx = d_topk_idx;
     a.user_w = d_topk_w;
-    return launched(m1moe::launch_moe_decode(a, ctx->stream), "moe_decode");
+    return launched(enqueue_decode(ctx, a), "moe_decode");
 }
 
 }  // extern "C"
@@ -594,13 +650,13 @@ int32_t moe_decode_normed(m1moe_ctx_t ctx, int32_t layer, const float* d_x, cons
     int32_t rc;
     if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
     if ((rc = require_loaded(ctx, layer, true))) return rc;
-    if ((rc = set_device(ctx))) return rc;
+    if ((rc = set_device(ctx)) || (rc = refresh_decode_copy(ctx, layer))) return rc;
     m1moe::FusedArgs a = fused_args(ctx, layer, d_x, M1MOE_F32, d_residual, d_out);
     a.x_ssq = d_ssq;
     a.n_ssq = n_ssq;
     a.x_norm_w = d_norm_w;
     a.x_eps = eps;
-    return launched(m1moe::launch_moe_decode(a, ctx->stream), "moe_decode (normed input)");
+    return launched(enqueue_decode(ctx, a), "moe_decode (normed input)");
 }
 }  // namespace m1moe
 

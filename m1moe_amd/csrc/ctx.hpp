@@ -42,8 +42,20 @@ struct m1moe_ctx {
     float* topk_w = nullptr;         // [cap][K]
     uint32_t* counters = nullptr;    // [cap]
     float* act = nullptr;            // [K][I]
-    uint8_t* sync = nullptr;         // decode hand-off state: slots | gu_cnt | seen
+    uint8_t* sync = nullptr;         // decode hand-off state: slots | gu_cnt | seen |
+                                     // cu_seen | cu_cnt | cu_part
     uint64_t sync_bytes = 0, sync_gu_cnt = 0, sync_seen = 0;
+    uint64_t sync_cu_seen = 0, sync_cu_cnt = 0, sync_cu_part = 0;
+    // decode launches use the one-workgroup-per-CU kernel (decode_cu.hip):
+    // the shape fits it and the device has the CUs to hold all its
+    // workgroups at once.  That kernel reads a repacked copy of every expert
+    // block (dec, [L][E][dec_bytes]), made at upload; a layer whose canonical
+    // blocks were handed out for writing (m1moe_expert_block) is repacked
+    // again before its next decode (dec_stale).
+    bool decode_cu = false;
+    uint8_t* dec = nullptr;
+    uint64_t dec_bytes = 0;
+    std::vector<bool> dec_stale;
     uint32_t* err = nullptr;         // sticky device error flag
     // prefill scratch, grown on demand to the largest T seen (pf_cap tokens)
     int32_t pf_cap = 0;

@@ -167,6 +167,34 @@ __device__ __forceinline__ float nib_dot32(const uint4& w, const XChunk2& c, con
     return LO ? (a0 + a1) + (a2 + a3) : a0 + a1;
 }
 
+// Nibble dot product on exact f16 subnormals: masking a word's nibble pairs
+// (bits 0..3 / 16..19 and 4..7 / 20..23, then the same of the word >> 8)
+// leaves f16 bit patterns whose values are n * 2^-24 (or 16 n * 2^-24 for
+// the upper nibble of a byte, which meets the /16 of the odd chunk
+// elements).  The products with the scaled chunk are exact in f32, so the
+// result is sum_c n_c x_c * 2^-24 with no offset to cancel; the caller
+// multiplies by 2^24 (exact).  LO: the lo pairs of a split chunk take part.
+template <bool LO>
+__device__ __forceinline__ float nib_dot32_sub(const uint4& w, const XChunk2& c, uint32_t mlo,
+                                               uint32_t mhi) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t v = ws[i], v8 = v >> 8;
+        const uint32_t n0 = v & mlo, n1 = v & mhi, n2 = v8 & mlo, n3 = v8 & mhi;
+        a0 = dot2_f16(n0, c.X[4 * i + 0], a0);
+        a1 = dot2_f16(n1, c.X[4 * i + 1], a1);
+        if (LO) a2 = dot2_f16(n0, c.L[4 * i + 0], a2);
+        if (LO) a3 = dot2_f16(n1, c.L[4 * i + 1], a3);
+        a0 = dot2_f16(n2, c.X[4 * i + 2], a0);
+        a1 = dot2_f16(n3, c.X[4 * i + 3], a1);
+        if (LO) a2 = dot2_f16(n2, c.L[4 * i + 2], a2);
+        if (LO) a3 = dot2_f16(n3, c.L[4 * i + 3], a3);
+    }
+    return LO ? (a0 + a1) + (a2 + a3) : a0 + a1;
+}
+
 // v_perm_b32 selectors that move the low / high bf16 of a dword into the
 // upper half of an f32 and zero the lower half (selector byte 0x0C = 0x00).
 constexpr uint32_t kSelLo = 0x01000C0Cu, kSelHi = 0x03020C0Cu;

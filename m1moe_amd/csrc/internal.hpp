@@ -61,6 +61,13 @@ struct FusedArgs {
     uint32_t* gu_cnt;            // [kNRep][n_cnt] monotonic counters of finished gate/up
                                  // tiles, kCntStride apart
     uint32_t* seen;              // [grid] launches completed by each workgroup
+    // the one-workgroup-per-CU kernel (decode_cu.hip): the layer's repacked
+    // expert blocks, its own launch counters, counters and partial sums
+    const uint8_t* dec_base;     // [E][dec_bytes] repacked copy of the layer's experts
+    uint64_t dec_bytes;
+    uint32_t* cu_seen;           // [kCuWorkgroups]
+    uint32_t* cu_cnt;            // [kCuRep][kCuParts] counters, kCntStride apart
+    uint32_t* cu_part;           // [kCuWorkgroups][kCuWorkgroups][8] tagged partial sums
     uint32_t* err;               // sticky device error flag
     int32_t h, E, K, I, gs, norm, x_bf16, spin_limit;
     // work decomposition (filled by decode_grid)
@@ -90,6 +97,9 @@ constexpr int kLogitRep = 8;         // logit replicas
 constexpr int kRepStride = 544;      // u64 words between logit replicas (4352 B)
 constexpr int kCntStride = 32;       // u32 words between counters (128 B)
 constexpr int kDecodeWaves = 4;    // waves per decode workgroup
+constexpr int kCuWorkgroups = 256; // decode_cu.hip: workgroups (one per CU)
+constexpr int kCuRep = 4;          // decode_cu.hip: replicas of the counter
+constexpr int kCuParts = 16;       // decode_cu.hip: parts of the counter
 
 // Fills the work decomposition of the fused decode kernel for a shape and
 // returns its grid size (workgroups).
@@ -139,6 +149,16 @@ constexpr int kPfTN = 64;   // prefill GEMM: (token, slot) pairs per workgroup t
 // launchers (defined next to their kernels); return a hipError_t as int
 int launch_router_topk(const RouterArgs& a, void* stream);
 int launch_moe_decode(const FusedArgs& a, void* stream);
+// The one-workgroup-per-CU decode kernel: the shapes it takes (hidden 2048,
+// K * I = 8192 or 16384, I = 1024 or 2048, K <= 8 dividing 8) and its
+// launcher (all kCuWorkgroups workgroups must be resident together).
+bool decode_cu_fits(int h, int E, int K, int I, int gs);
+int launch_moe_decode_cu(const FusedArgs& a, void* stream);
+// Bytes of one expert's repacked block (decode_cu.hip) and the launch that
+// builds a layer's repacked blocks from its canonical ones.
+uint64_t decode_copy_bytes(int I, int gs);
+int launch_decode_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int I,
+                       int gs, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_dequant(const uint8_t* expert_base, const ProjView& p, int32_t gs, float* out,
                    void* stream);

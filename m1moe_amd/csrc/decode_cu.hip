@@ -112,23 +112,25 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
     }
     if (wave == 0) {
         const unsigned long long* rep = a.slots + (size_t)(g % kLogitRep) * kRepStride;
-        float v[4];
+        const int nj = (E + 63) >> 6;  // logits per lane (wave-uniform)
+        float v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         bool have[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            have[j] = (lane + 64 * j >= E);
-            v[j] = -INFINITY;
-        }
+        for (int j = 0; j < 4; ++j) have[j] = (lane + 64 * j >= E);
         bool ok = true;
         for (int it = 0;; ++it) {
+            // every missing logit of the lane is requested before any is examined
+            unsigned long long u[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                u[j] = (j < nj && !have[j]) ? ld_u64(rep + lane + 64 * j) : 0ull;
             bool all = true;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if (!have[j]) {
-                    const unsigned long long u = ld_u64(rep + lane + 64 * j);
-                    if ((uint32_t)(u >> 32) == tag) {
+                if (j < nj && !have[j]) {
+                    if ((uint32_t)(u[j] >> 32) == tag) {
                         have[j] = true;
-                        const float f = __uint_as_float((uint32_t)u);
+                        const float f = __uint_as_float((uint32_t)u[j]);
                         v[j] = (f != f) ? -INFINITY : f;  // NaN ranks last
                     } else {
                         all = false;
@@ -148,25 +150,30 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
         if (lane == 0) s.ok = ok ? 1 : 0;
     }
     __syncthreads();
-    const int ep = E <= 1 ? 1 : 1 << (32 - __clz(E - 1));
-    const int P = ep >= 4 ? min(ep / 4, kT / ep) : 1;  // lanes per expert: a power of two <= 8
-    const int M = ep / P;  // experts compared per lane: a multiple of 4 (ep >= 4), read 4 at a
-                           // time (ep < 4 reads padding, -inf at indices above every expert)
-    const int i = t / P, q = t - i * P;
+    // ep = E rounded up to a power of two; P (a power of two <= 8) lanes per
+    // expert, each comparing M = ep / P experts (a multiple of 4 for ep >= 4,
+    // read 4 at a time; ep < 4 reads padding, -inf at indices above every
+    // expert)
+    const int lep = E <= 1 ? 0 : 32 - __clz(E - 1);
+    const int lp = lep >= 2 ? min(lep - 2, 9 - lep) : 0;
+    const int lm = lep - lp;
+    const int i = t >> lp, q = t & ((1 << lp) - 1);
     float cnt = 0.f;
-    if (i < ep) {
+    if (i < (1 << lep)) {
         const float my = s.v[i];
+        const int j0 = q << lm;
 #pragma unroll 2
-        for (int m = 0; m < max(M, 4); m += 4) {
-            const float4 v4 = *reinterpret_cast<const float4*>(&s.v[q * M + m]);
+        for (int m = 0; m < max(1 << lm, 4); m += 4) {
+            const float4 v4 = *reinterpret_cast<const float4*>(&s.v[j0 + m]);
             const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int j = q * M + m + u;
+                const int j = j0 + m + u;
                 cnt += ((vv[u] > my) || (vv[u] == my && j < i)) ? 1.f : 0.f;
             }
         }
     }
+    const int P = 1 << lp;
     if (P > 1) cnt = seg_sum(cnt, P);  // total in the segment's last lane
     if (i < E && q == P - 1 && (int)cnt < K) s.idx[(int)cnt] = i;
     __syncthreads();

@@ -36,6 +36,26 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert getattr(lib, n) is not None
 
 
+def test_swift_binding_names_only_declared_symbols():
+    """The uncompiled SwiftPM binding (no Swift toolchain here) calls only
+    functions and constants the header declares, and links the library's
+    own name."""
+    sw = os.path.join(ROOT, "Sources")
+    mm = open(os.path.join(sw, "CM1MoEHIP", "module.modulemap")).read()
+    assert 'link "m1moe_hip"' in mm and 'header "shim.h"' in mm
+    assert os.path.basename(_lib.LIB_PATH) == "libm1moe_hip.so"
+    assert "#include <m1moe_hip.h>" in open(os.path.join(sw, "CM1MoEHIP", "shim.h")).read()
+    swift = re.sub(r"//[^\n]*", "", open(os.path.join(sw, "M1MoE", "HIPMoE.swift")).read())
+    header = open(HEADER).read()
+    calls = set(re.findall(r"\b(m1moe_[a-z0-9_]+)\s*\(", swift))
+    calls -= {"m1moe_moe_shape", "m1moe_dec_shape"}     # struct initialisers, checked below
+    assert calls and calls <= set(declared_functions()), calls - set(declared_functions())
+    for c in set(re.findall(r"\b(M1MOE_[A-Z0-9_]+)\b", swift)):
+        assert re.search(r"\b%s\s*=" % c, header), c
+    for t in set(re.findall(r"\b(m1moe_[a-z_]+_t|m1moe_[a-z_]+_shape)\b", swift)):
+        assert re.search(r"\b%s;" % t, header), t
+
+
 def test_abi_version():
     assert _lib.load().m1moe_abi_version() == 1
 

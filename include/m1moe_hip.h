@@ -214,6 +214,22 @@ int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T,
                           const float* d_residual, float* d_out,
                           int32_t* d_topk_idx, float* d_topk_w);
 
+/* m1moe_moe_prefill with the same arguments, kernels and results, that
+ * allocates nothing: no counterpart in the reference.  It is for callers that
+ * cannot allocate device memory (code under HIP graph capture without a
+ * warm-up call, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * scratch is a fixed 64 MiB static device array per GPU (looked up by
+ * m1moe_create, held until the process ends) instead of the context's
+ * buffers that m1moe_moe_prefill grows; a T whose scratch would not fit is
+ * rejected with M1MOE_ERR_INVALID naming the largest T that fits (779
+ * tokens at hidden 2048, 8 x 1024 experts; 682 at hidden 4096,
+ * 2 x 14336).  Every call on one GPU shares that array, so calls that overlap
+ * on one GPU (two streams, or two contexts on one device) race. */
+int32_t m1moe_moe_prefill_noalloc(m1moe_ctx_t ctx, int32_t layer, int32_t T,
+                                  const void* d_x, int32_t x_dtype,
+                                  const float* d_residual, float* d_out,
+                                  int32_t* d_topk_idx, float* d_topk_w);
+
 /* Writes the dequantised f32 weights of one projection of one expert,
  * row-major [rows x cols] (gate/up: intermediate x hidden; down: hidden x
  * intermediate), value f32(n)*f32(s)+f32(b), for the bit-exact weight check

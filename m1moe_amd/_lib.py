@@ -111,6 +111,8 @@ _PROTOTYPES = [
      [c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("m1moe_moe_prefill", c_int32,
      [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("m1moe_moe_prefill_noalloc", c_int32,
+     [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("m1moe_dequant_debug", c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p]),
     ("m1moe_rmsnorm", c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_float]),
     ("m1moe_matvec_bf16", c_int32,

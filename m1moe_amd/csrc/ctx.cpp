@@ -148,6 +148,30 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
     return launched(m1moe::launch_router_topk(r, ctx->stream), "router_topk");
 }
 
+// Sizes in bytes of the nine prefill scratch buffers for T tokens, in the
+// order of PrefillArgs: xq, xinv, pos, sorted_tok, expert_off, tile_off,
+// tile_expert, act, y.
+void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[9]) {
+    const uint64_t t = (uint64_t)T, P = t * (uint64_t)g.K, E = (uint64_t)g.E;
+    sz[0] = t * g.h * 2;
+    sz[1] = t * 4;
+    sz[2] = P * 4;
+    sz[3] = P * 4;
+    sz[4] = (E + 1) * 4;
+    sz[5] = (E + 1) * 4;
+    sz[6] = (P / m1moe::kPfTN + E + 1) * 4;
+    sz[7] = P * g.I * 2;
+    sz[8] = P * g.h * 4;
+}
+
+// Bytes of the nine buffers carved from one block, each 256-byte aligned.
+uint64_t prefill_scratch_packed(const m1moe::Geom& g, int32_t T) {
+    uint64_t sz[9], total = 0;
+    prefill_scratch_sizes(g, T, sz);
+    for (uint64_t b : sz) total += (b + 255) / 256 * 256;
+    return total;
+}
+
 // Grows the prefill scratch to exactly T tokens when a call needs more than
 // it holds.  Growth frees the old buffers, so it is refused during stream
 // capture, and a graph captured before a call with a larger T must be
@@ -155,29 +179,23 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
 int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
     if (T <= ctx->pf_cap) return M1MOE_OK;
     if (int32_t rc = m1moe::refuse_growth_in_capture(ctx->stream, "the prefill scratch")) return rc;
-    const m1moe::Geom& g = ctx->g;
-    void** bufs[] = {(void**)&ctx->pf_xq,   (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
-                     (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,
-                     (void**)&ctx->pf_texp, (void**)&ctx->pf_act,  (void**)&ctx->pf_y};
+    void** bufs[9] = {(void**)&ctx->pf_xq,   (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
+                      (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,
+                      (void**)&ctx->pf_texp, (void**)&ctx->pf_act,  (void**)&ctx->pf_y};
+    static const char* const names[9] = {
+        "prefill x",       "prefill x scales",   "prefill positions",
+        "prefill sorted tokens", "prefill expert offsets", "prefill tile offsets",
+        "prefill tile experts",  "prefill act",        "prefill expert outputs"};
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     for (void** b : bufs) {
         if (*b) (void)hipFree(*b);
         *b = nullptr;
     }
     ctx->pf_cap = 0;
-    const uint64_t t = (uint64_t)T, P = t * (uint64_t)g.K, E = (uint64_t)g.E;
-    int32_t rc;
-    if ((rc = device_alloc((void**)&ctx->pf_xq, t * g.h * 2, "prefill x")) ||
-        (rc = device_alloc((void**)&ctx->pf_xinv, t * 4, "prefill x scales")) ||
-        (rc = device_alloc((void**)&ctx->pf_pos, P * 4, "prefill positions")) ||
-        (rc = device_alloc((void**)&ctx->pf_sorted, P * 4, "prefill sorted tokens")) ||
-        (rc = device_alloc((void**)&ctx->pf_eoff, (E + 1) * 4, "prefill expert offsets")) ||
-        (rc = device_alloc((void**)&ctx->pf_toff, (E + 1) * 4, "prefill tile offsets")) ||
-        (rc = device_alloc((void**)&ctx->pf_texp, (P / m1moe::kPfTN + E + 1) * 4,
-                           "prefill tile experts")) ||
-        (rc = device_alloc((void**)&ctx->pf_act, P * g.I * 2, "prefill act")) ||
-        (rc = device_alloc((void**)&ctx->pf_y, P * g.h * 4, "prefill expert outputs")))
-        return rc;
+    uint64_t sz[9];
+    prefill_scratch_sizes(ctx->g, T, sz);
+    for (int i = 0; i < 9; ++i)
+        if (int32_t rc = device_alloc(bufs[i], sz[i], names[i])) return rc;
     ctx->pf_cap = T;
     return M1MOE_OK;
 }
@@ -188,6 +206,105 @@ int32_t require_loaded(m1moe_ctx_t ctx, int32_t layer, bool router) {
     if (router && !ctx->router_loaded[layer])
         return fail(M1MOE_ERR_INVALID, "layer %d router was never uploaded", layer);
     return M1MOE_OK;
+}
+
+// m1moe_moe_prefill and its allocation-free variant: the same kernels, with
+// the scratch either grown in the context (allocates when T exceeds every
+// earlier call) or carved from this device's fixed static scratch (allocates
+// nothing; T is limited by its size).
+int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_x,
+                       int32_t x_dtype, const float* d_residual, float* d_out,
+                       int32_t* d_topk_idx, float* d_topk_w, bool use_static) {
+    int32_t rc;
+    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
+    if (T < 1 || T > m1moe::kPrefillCap)
+        return fail(M1MOE_ERR_INVALID, "T=%d must be in [1, %d]", T, m1moe::kPrefillCap);
+    if ((rc = check_dtype(x_dtype)) || (rc = check_dev_ptr(d_x, "d_x", false)) ||
+        (rc = check_dev_ptr(d_residual, "d_residual", true)) ||
+        (rc = check_dev_ptr(d_out, "d_out", false)) ||
+        (rc = check_dev_ptr(d_topk_idx, "d_topk_idx", true)) ||
+        (rc = check_dev_ptr(d_topk_w, "d_topk_w", true)))
+        return rc;
+    if ((rc = require_loaded(ctx, layer, true))) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    uint8_t* sbase = nullptr;
+    if (use_static) {
+        const uint64_t need = prefill_scratch_packed(ctx->g, T);
+        if (need > m1moe::kStaticScratchBytes) {
+            int32_t tmax = 0;
+            for (int32_t lo = 1, hi = T; lo <= hi;) {   // bytes grow with T
+                const int32_t mid = lo + (hi - lo) / 2;
+                if (prefill_scratch_packed(ctx->g, mid) <= m1moe::kStaticScratchBytes) {
+                    tmax = mid;
+                    lo = mid + 1;
+                } else {
+                    hi = mid - 1;
+                }
+            }
+            return fail(M1MOE_ERR_INVALID,
+                        "T=%d needs %llu bytes of static prefill scratch, more than its %llu; "
+                        "at this shape T <= %d",
+                        T, (unsigned long long)need,
+                        (unsigned long long)m1moe::kStaticScratchBytes, tmax);
+        }
+        if (!ctx->static_scratch)
+            return fail(M1MOE_ERR_HIP, "the static scratch of device %d is not attached",
+                        ctx->device);
+        sbase = ctx->static_scratch;
+    } else if ((rc = ensure_prefill_scratch(ctx, T))) {
+        return rc;
+    }
+    if ((rc = enqueue_router(ctx, layer, T, d_x, x_dtype, d_topk_idx, d_topk_w, nullptr)))
+        return rc;
+    const m1moe::Geom& g = ctx->g;
+    m1moe::PrefillArgs a{};
+    a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
+    a.expert_bytes = g.expert_bytes;
+    a.x = d_x;
+    a.x_bf16 = (x_dtype == M1MOE_BF16);
+    a.residual = d_residual;
+    a.out = d_out;
+    a.idx = ctx->topk_idx;
+    a.w = ctx->topk_w;
+    a.T = T;
+    a.h = g.h;
+    a.E = g.E;
+    a.K = g.K;
+    a.I = g.I;
+    a.gs = g.gs;
+    if (sbase) {
+        // carve the nine buffers, 256-byte aligned; every one is written
+        // before it is read, so nothing left by an earlier call is used
+        uint64_t sz[9];
+        void* p[9];
+        prefill_scratch_sizes(g, T, sz);
+        for (int i = 0; i < 9; ++i) {
+            p[i] = sbase;
+            sbase += (sz[i] + 255) / 256 * 256;
+        }
+        a.xq = static_cast<_Float16*>(p[0]);
+        a.xinv = static_cast<float*>(p[1]);
+        a.pos = static_cast<int32_t*>(p[2]);
+        a.sorted_tok = static_cast<int32_t*>(p[3]);
+        a.expert_off = static_cast<int32_t*>(p[4]);
+        a.tile_off = static_cast<int32_t*>(p[5]);
+        a.tile_expert = static_cast<int32_t*>(p[6]);
+        a.act = static_cast<_Float16*>(p[7]);
+        a.y = static_cast<float*>(p[8]);
+    } else {
+        a.xq = ctx->pf_xq;
+        a.xinv = ctx->pf_xinv;
+        a.pos = ctx->pf_pos;
+        a.sorted_tok = ctx->pf_sorted;
+        a.expert_off = ctx->pf_eoff;
+        a.tile_off = ctx->pf_toff;
+        a.tile_expert = ctx->pf_texp;
+        a.act = ctx->pf_act;
+        a.y = ctx->pf_y;
+    }
+    a.err = ctx->err;
+    return launched(m1moe::launch_prefill(a, ctx->stream),
+                    use_static ? "moe_prefill_noalloc" : "moe_prefill");
 }
 
 }  // namespace
@@ -282,6 +399,9 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
     if (hipSetDevice(device) != hipSuccess) return cleanup(fail(M1MOE_ERR_HIP, "hipSetDevice"));
     if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess)
         return cleanup(fail(M1MOE_ERR_HIP, "hipStreamCreate failed"));
+    if (int e = m1moe::static_scratch_attach(device, &c->static_scratch))
+        return cleanup(fail(M1MOE_ERR_HIP, "static scratch address of device %d: %s", device,
+                            hipGetErrorString((hipError_t)e)));
     c->stream = c->own_stream;
     const uint64_t cap = m1moe::kPrefillCap;
     {
@@ -665,48 +785,15 @@ extern "C" {
 int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_x,
                           int32_t x_dtype, const float* d_residual, float* d_out,
                           int32_t* d_topk_idx, float* d_topk_w) {
-    int32_t rc;
-    if ((rc = check_ctx(ctx)) || (rc = check_layer(ctx, layer))) return rc;
-    if (T < 1 || T > m1moe::kPrefillCap)
-        return fail(M1MOE_ERR_INVALID, "T=%d must be in [1, %d]", T, m1moe::kPrefillCap);
-    if ((rc = check_dtype(x_dtype)) || (rc = check_dev_ptr(d_x, "d_x", false)) ||
-        (rc = check_dev_ptr(d_residual, "d_residual", true)) ||
-        (rc = check_dev_ptr(d_out, "d_out", false)) ||
-        (rc = check_dev_ptr(d_topk_idx, "d_topk_idx", true)) ||
-        (rc = check_dev_ptr(d_topk_w, "d_topk_w", true)))
-        return rc;
-    if ((rc = require_loaded(ctx, layer, true))) return rc;
-    if ((rc = set_device(ctx))) return rc;
-    if ((rc = ensure_prefill_scratch(ctx, T))) return rc;
-    if ((rc = enqueue_router(ctx, layer, T, d_x, x_dtype, d_topk_idx, d_topk_w, nullptr)))
-        return rc;
-    const m1moe::Geom& g = ctx->g;
-    m1moe::PrefillArgs a{};
-    a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
-    a.expert_bytes = g.expert_bytes;
-    a.x = d_x;
-    a.x_bf16 = (x_dtype == M1MOE_BF16);
-    a.residual = d_residual;
-    a.out = d_out;
-    a.idx = ctx->topk_idx;
-    a.w = ctx->topk_w;
-    a.T = T;
-    a.h = g.h;
-    a.E = g.E;
-    a.K = g.K;
-    a.I = g.I;
-    a.gs = g.gs;
-    a.xq = ctx->pf_xq;
-    a.xinv = ctx->pf_xinv;
-    a.pos = ctx->pf_pos;
-    a.sorted_tok = ctx->pf_sorted;
-    a.expert_off = ctx->pf_eoff;
-    a.tile_off = ctx->pf_toff;
-    a.tile_expert = ctx->pf_texp;
-    a.act = ctx->pf_act;
-    a.y = ctx->pf_y;
-    a.err = ctx->err;
-    return launched(m1moe::launch_prefill(a, ctx->stream), "moe_prefill");
+    return prefill_common(ctx, layer, T, d_x, x_dtype, d_residual, d_out, d_topk_idx, d_topk_w,
+                          false);
+}
+
+int32_t m1moe_moe_prefill_noalloc(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_x,
+                                  int32_t x_dtype, const float* d_residual, float* d_out,
+                                  int32_t* d_topk_idx, float* d_topk_w) {
+    return prefill_common(ctx, layer, T, d_x, x_dtype, d_residual, d_out, d_topk_idx, d_topk_w,
+                          true);
 }
 
 int32_t m1moe_dequant_debug(m1moe_ctx_t ctx, int32_t layer, int32_t expert, int32_t proj,

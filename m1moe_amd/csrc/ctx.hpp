@@ -68,6 +68,9 @@ struct m1moe_ctx {
     int32_t* pf_texp = nullptr;      // [cap*K/kPfTN + E + 1]
     _Float16* pf_act = nullptr;      // [cap*K][I]
     float* pf_y = nullptr;           // [cap*K][h]
+    // this device's static scratch (scratch.hip), for m1moe_moe_prefill_noalloc;
+    // shared with every other context on the device, never freed
+    uint8_t* static_scratch = nullptr;
     // attention scratch of m1moe_attention_decode, grown on demand
     float* attn_part = nullptr;
     uint64_t attn_part_floats = 0;

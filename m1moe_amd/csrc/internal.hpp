@@ -146,6 +146,15 @@ struct PrefillArgs {
 
 constexpr int kPfTN = 64;   // prefill GEMM: (token, slot) pairs per workgroup tile
 
+// m1moe_moe_prefill_noalloc: bytes of the per-GPU static scratch (scratch.hip)
+// that holds its prefill buffers.  64 MiB: 779 tokens at hidden 2048,
+// 8 x 1024 experts, 682 at hidden 4096, 2 x 14336.
+constexpr uint64_t kStaticScratchBytes = 64ull << 20;
+// Device address of this GPU's static scratch; `device` must be current.
+// Looks it up on the first call per device and returns the kept address
+// after that.  Returns a hipError_t as int.
+int static_scratch_attach(int device, uint8_t** out);
+
 // launchers (defined next to their kernels); return a hipError_t as int
 int launch_router_topk(const RouterArgs& a, void* stream);
 int launch_moe_decode(const FusedArgs& a, void* stream);

@@ -351,23 +351,25 @@ __device__ __forceinline__ void gu_load(const FusedArgs& a, const Layout& L, int
     }
 }
 
-// act values carry the launch number mod 2^kActTagBits in their lowest
-// mantissa bits, so a consumer can tell this launch's value from an earlier
-// one's; it clears them before use (a relative change below 2^(bits-23), the
-// same in every launch; the consumer rounds act to f16 anyway).
+// act values carry the launch number's parity in their lowest mantissa bit:
+// every launch rewrites every act entry (tagged zeros for a slot without an
+// expert), so an entry holds this launch's value or the previous launch's,
+// and the parity tells them apart.  The consumer clears the bit before use (a
+// relative change below 2^-22, the same in every launch) and splits the value
+// into hi + lo f16 halves (22 significant bits).
 #ifndef M1MOE_ACT_TAG_BITS
-#define M1MOE_ACT_TAG_BITS 8
+#define M1MOE_ACT_TAG_BITS 1
 #endif
 constexpr uint32_t kActTagMask = (1u << M1MOE_ACT_TAG_BITS) - 1u;
 __device__ __forceinline__ float act_tagged(float v, uint32_t tag) {
     return __uint_as_float((__float_as_uint(v) & ~kActTagMask) | (tag & kActTagMask));
 }
 
-// The gate/up input chunk: split hi + lo where the registers allow it
-// (one chunk per lane); two chunks per lane keep single f16 to stay within
-// the 168 VGPRs of three waves per SIMD.
+// The gate/up input chunk: split hi + lo (f32 inputs keep 22 significant
+// bits) for up to two chunks per lane, within the 256 VGPRs of two waves per
+// SIMD; wider inputs keep single f16 chunks.
 template <int CPL>
-using GUChunk = typename std::conditional<CPL == 1, XChunk2, XChunk>::type;
+using GUChunk = typename std::conditional<CPL <= 2, XChunk2, XChunk>::type;
 
 template <int CPL, int UG, int GSL, bool LO>
 __device__ __forceinline__ void gu_compute(const FusedArgs& a, int k, int row0, const GUGeo& m,
@@ -477,6 +479,15 @@ __device__ void gu_role(const FusedArgs& a, const Layout& L, int g, int wave, in
                 gu_compute<CPL, UG, GSL, true>(a, k, row_of(T), m, t, xc, inv, tag);
             else
                 gu_compute<CPL, UG, GSL, false>(a, k, row_of(T), m, t, xc, inv, tag);
+        } else if (m.writer) {
+            // no expert for this slot (a bad index or a failed hand-off, both
+            // flagged): its act rows still get this launch's tag, so every
+            // act entry is rewritten in every launch
+#pragma unroll
+            for (int u = 0; u < UG; ++u) {
+                const int row = row_of(T) + u * a.rpi_g;
+                if (row < a.I) st_f32(a.act + (size_t)k * a.I + row, act_tagged(0.f, tag));
+            }
         }
         ++cnt_n;
     };
@@ -617,7 +628,7 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
     const NibK nk = nib_consts();
     int cur = -1;
     DNUnit d{};
-    XChunk xc[1];
+    XChunk2 xc[1];
     float inv = 1.f;
     bool live = false;  // this lane's unit is ready and routed
     auto process = [&](const ItemPos& p, const DNTile& t) {
@@ -665,7 +676,8 @@ __device__ void dn_role(const FusedArgs& a, const Layout& L, int dblk, int wave,
 #pragma unroll
         for (int rr = 0; rr < kRT; ++rr) {
             const uint32_t rc = (uint32_t)min(row_base + p.st * kRT + rr, a.h - 1);
-            float q = chunk_term(t.w[rr], t.s[rr], t.b[rr], sb_sel(rc * groups + (cc >> GSL)), xc[0], nk) * inv;
+            float q = chunk_term<true>(t.w[rr], t.s[rr], t.b[rr], sb_sel(rc * groups + (cc >> GSL)),
+                                       xc[0], nk) * inv;
             q = live ? q : 0.f;
             q = seg_sum(q, a.seg_d);
             if (d.writer && d.k < a.K) part[rr] = q;
@@ -752,7 +764,7 @@ __device__ __forceinline__ void stage_x(const FusedArgs& a, int wave, int lane, 
 // ---- the kernel --------------------------------------------------------------------
 
 template <int CPL, int UG, int GSL>
-__global__ __launch_bounds__(kThreads, (CPL <= 2 ? 3 : 1)) void moe_decode_kernel(FusedArgs a) {
+__global__ __launch_bounds__(kThreads, (CPL <= 2 ? 2 : 1)) void moe_decode_kernel(FusedArgs a) {
     __shared__ RouteLDS r;
     __shared__ uint32_t s_tag;
     __shared__ double s_lp[4];

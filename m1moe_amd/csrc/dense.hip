@@ -49,17 +49,6 @@ __device__ __forceinline__ float block_sum(float v, float* s_red, int nw) {
     return t;
 }
 
-__device__ __forceinline__ float block_max(float v, float* s_red, int nw) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    v = wave_max(v);
-    if (lane == 0) s_red[wave] = v;
-    __syncthreads();
-    float t = -INFINITY;
-    for (int w = 0; w < nw; ++w) t = fmaxf(t, s_red[w]);
-    __syncthreads();
-    return t;
-}
-
 __device__ __forceinline__ void st_coh(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -27,6 +27,7 @@
  */
 #include "m1moe_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -105,9 +106,10 @@ void orc_dequant_proj(const orc_shape* s, const uint8_t* blk, int32_t proj,
     }
 }
 
-void orc_matvec4bit(const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                    const float* x, float* y, int32_t out_dim, int32_t in_dim,
-                    int32_t gs) {
+/* The restatement itself: lane by lane, one row at a time. */
+void orc_matvec4bit_lanes(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                          const float* x, float* y, int32_t out_dim, int32_t in_dim,
+                          int32_t gs) {
     const uint32_t num_words = (uint32_t)in_dim / 8;   /* :55 */
     const uint32_t num_groups = (uint32_t)in_dim / gs; /* :56 */
     float shared[64];
@@ -135,6 +137,87 @@ void orc_matvec4bit(const uint32_t* w, const uint16_t* s, const uint16_t* b,
             for (uint32_t lid = 0; lid < st; ++lid)
                 shared[lid] += shared[lid + st];
         y[row] = shared[0]; /* :91 */
+    }
+}
+
+/* The same arithmetic with eight lanes per AVX2 register: lane l of the
+ * restatement is element l % 8 of accumulator l / 8, and every lane performs
+ * exactly the restatement's operations in its order (the same fused
+ * multiply-adds and the same f32 product scale * x), so the result is equal
+ * bit for bit (pinned by a test against orc_matvec4bit_lanes).  Eight
+ * consecutive lanes read eight consecutive packed words; x is transposed
+ * once so that the eight x values of nibble bb of those words are
+ * contiguous. */
+__attribute__((target("avx2,fma"))) static void matvec4bit_avx2(
+    const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x, float* y,
+    int32_t out_dim, int32_t in_dim, int32_t gs, float* xt) {
+    const uint32_t num_words = (uint32_t)in_dim / 8;
+    const uint32_t num_groups = (uint32_t)in_dim / (uint32_t)gs;
+    for (uint32_t wi = 0; wi < num_words; ++wi)
+        for (uint32_t bb = 0; bb < 8; ++bb) xt[(size_t)bb * num_words + wi] = x[wi * 8 + bb];
+    const __m256i mask = _mm256_set1_epi32(0xF);
+    /* words per scale group: gs is a multiple of 8 (32, 64 or 128), and a
+     * lane block starts at a multiple of 8 words */
+    const uint32_t wpg = (uint32_t)gs / 8;
+    float shared[64];
+    for (int32_t row = 0; row < out_dim; ++row) {
+        const uint32_t* w_row = w + (size_t)row * num_words;
+        const uint16_t* s_row = s + (size_t)row * num_groups;
+        const uint16_t* b_row = b + (size_t)row * num_groups;
+        __m256 acc[8];
+        for (int lb = 0; lb < 8; ++lb) acc[lb] = _mm256_setzero_ps();
+        for (uint32_t k0 = 0; k0 < num_words; k0 += 64) {
+            for (uint32_t lb = 0; lb < 8; ++lb) {
+                const uint32_t wi0 = k0 + lb * 8;   /* lanes lb*8 .. lb*8+7 */
+                if (wi0 >= num_words) break;
+                __m256 scale, bias;
+                if (wpg >= 8) {   /* the eight words share one group */
+                    const uint32_t g = wi0 / wpg;
+                    scale = _mm256_set1_ps(orc_bf16_to_f32(s_row[g]));
+                    bias = _mm256_set1_ps(orc_bf16_to_f32(b_row[g]));
+                } else {
+                    float sv[8], bv[8];
+                    for (uint32_t j = 0; j < 8; ++j) {
+                        const uint32_t g = (wi0 + j) / wpg;
+                        sv[j] = orc_bf16_to_f32(s_row[g]);
+                        bv[j] = orc_bf16_to_f32(b_row[g]);
+                    }
+                    scale = _mm256_loadu_ps(sv);
+                    bias = _mm256_loadu_ps(bv);
+                }
+                const __m256i packed = _mm256_loadu_si256((const __m256i*)(w_row + wi0));
+                __m256 a = acc[lb];
+                for (uint32_t bb = 0; bb < 8; ++bb) {
+                    const __m256 nib = _mm256_cvtepi32_ps(
+                        _mm256_and_si256(_mm256_srli_epi32(packed, (int)(bb * 4)), mask));
+                    const __m256 xv = _mm256_loadu_ps(xt + (size_t)bb * num_words + wi0);
+                    a = _mm256_fmadd_ps(nib, _mm256_mul_ps(scale, xv),
+                                        _mm256_fmadd_ps(bias, xv, a));
+                }
+                acc[lb] = a;
+            }
+        }
+        for (int lb = 0; lb < 8; ++lb) _mm256_storeu_ps(shared + lb * 8, acc[lb]);
+        for (uint32_t st = 32; st > 0; st >>= 1)
+            for (uint32_t lid = 0; lid < st; ++lid) shared[lid] += shared[lid + st];
+        y[row] = shared[0];
+    }
+}
+
+/* Shaders.metal:39-92 (matvec4bit): the AVX2 form where the CPU has it and
+ * the row length is a whole number of eight-word lane blocks, else the
+ * lane-by-lane restatement. */
+void orc_matvec4bit(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                    const float* x, float* y, int32_t out_dim, int32_t in_dim,
+                    int32_t gs) {
+    const int have_avx2 = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    float* xt = NULL;
+    if (have_avx2 && in_dim % 64 == 0) xt = (float*)malloc((size_t)in_dim * sizeof(float));
+    if (xt) {
+        matvec4bit_avx2(w, s, b, x, y, out_dim, in_dim, gs, xt);
+        free(xt);
+    } else {
+        orc_matvec4bit_lanes(w, s, b, x, y, out_dim, in_dim, gs);
     }
 }
 

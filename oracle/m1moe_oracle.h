@@ -57,7 +57,12 @@ void orc_dequant_proj(const orc_shape* s, const uint8_t* expert_block,
                       int32_t proj, float* out);
 
 /* matvec4bit, Shaders.metal:39-92: 64 lane-strided partial sums of
- * fma(n, s*x, fma(b, x, acc)) followed by the threadgroup tree reduction. */
+ * fma(n, s*x, fma(b, x, acc)) followed by the threadgroup tree reduction.
+ * orc_matvec4bit_lanes is the restatement, lane by lane; orc_matvec4bit
+ * computes the same bits eight lanes at a time where the CPU has AVX2. */
+void orc_matvec4bit_lanes(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                          const float* x, float* y, int32_t out_dim, int32_t in_dim,
+                          int32_t gs);
 void orc_matvec4bit(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                     const float* x, float* y, int32_t out_dim, int32_t in_dim,
                     int32_t gs);

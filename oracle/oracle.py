@@ -52,6 +52,7 @@ def load() -> ctypes.CDLL:
         "orc_expert_offsets": (None, [POINTER(OrcShape), POINTER(OrcOffsets)]),
         "orc_dequant_proj": (None, [POINTER(OrcShape), P, c_int32, P]),
         "orc_matvec4bit": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
+        "orc_matvec4bit_lanes": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
         "orc_matvec4bit_f64": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
         "orc_swiglu": (None, [P, P, P, c_int32]),
         "orc_router_logits": (None, [P, P, c_int32, c_int32, P]),
@@ -113,10 +114,12 @@ def dequant_proj(s: OrcShape, block: np.ndarray, proj: int) -> np.ndarray:
     return out
 
 
-def matvec4bit(w, sc, bi, x, out_dim, in_dim, gs) -> np.ndarray:
+def matvec4bit(w, sc, bi, x, out_dim, in_dim, gs, lanes=False) -> np.ndarray:
+    """Shaders.metal:39-92; lanes=True runs the lane-by-lane restatement
+    instead of its eight-lanes-at-a-time form (same bits)."""
     y = np.empty(out_dim, dtype=np.float32)
-    load().orc_matvec4bit(_p(w), _p(sc), _p(bi), _p(np.ascontiguousarray(x, np.float32)), _p(y),
-                          out_dim, in_dim, gs)
+    fn = load().orc_matvec4bit_lanes if lanes else load().orc_matvec4bit
+    fn(_p(w), _p(sc), _p(bi), _p(np.ascontiguousarray(x, np.float32)), _p(y), out_dim, in_dim, gs)
     return y
 
 
@@ -309,11 +312,18 @@ class DecoderOracle:
     tensors[name] for name in embed, lm_head, final_norm (model level) and
     tensors[name][layer] for in_norm, post_norm, q, k, v, o, q_norm, k_norm:
     bf16 (uint16) arrays, matrices as [rows x cols].  images[layer] and
-    routers[layer]: the MoE block's expert image and bf16 router."""
+    routers[layer]: the MoE block's expert image and bf16 router.
+
+    nthreads > 1 spreads work that is independent in the restated arithmetic
+    over threads: the rows of a large matvec, the selected experts of a MoE
+    block, and the tokens of a prompt in prefill().  Every value is computed
+    by the same functions on the same operands as with one thread, so the
+    results are the same bits."""
 
     def __init__(self, moe: OrcShape, num_layers: int, vocab: int, num_heads: int,
                  num_kv_heads: int, head_dim: int, max_seq: int, qk_norm: bool,
-                 rope_theta: float, eps: float, tensors: dict, images, routers):
+                 rope_theta: float, eps: float, tensors: dict, images, routers,
+                 nthreads: int = 1):
         self.moe, self.L = moe, num_layers
         self.vocab, self.nh, self.nkv, self.hd = vocab, num_heads, num_kv_heads, head_dim
         self.max_seq, self.qk_norm = max_seq, bool(qk_norm)
@@ -323,10 +333,63 @@ class DecoderOracle:
         self.kc = np.zeros((num_layers, max_seq, kvd), dtype=np.float32)
         self.vc = np.zeros((num_layers, max_seq, kvd), dtype=np.float32)
         self.pos = 0
+        self.nthreads = max(1, int(nthreads))
+        self._pool = None
+        self._eb = None
+        self.split_min = 1 << 22     # matvecs with fewer weights stay on one thread
         # smallest gap, over the layers of the last step, between the K-th and
         # (K+1)-th router logit: where it is tiny the selected set (and so the
         # step's output) changes under arbitrarily small input perturbations
         self.route_margin = np.inf
+
+    def _map(self, fn, items):
+        items = list(items)
+        if self.nthreads == 1 or len(items) < 2:
+            return [fn(i) for i in items]
+        if self._pool is None:
+            from concurrent.futures import ThreadPoolExecutor
+            self._pool = ThreadPoolExecutor(self.nthreads)
+        return list(self._pool.map(fn, items))
+
+    def close(self) -> None:
+        if self._pool is not None:
+            self._pool.shutdown()
+            self._pool = None
+
+    def _matvec(self, w, x, residual=None, par=True) -> np.ndarray:
+        """matvec_bf16, its rows split over the threads when it is large."""
+        rows = w.shape[0]
+        if not par or self.nthreads == 1 or w.size < self.split_min:
+            return matvec_bf16(w, x, residual)
+        n = self.nthreads
+        cuts = [rows * i // n for i in range(n + 1)]
+        parts = self._map(lambda i: matvec_bf16(
+            w[cuts[i]:cuts[i + 1]], x,
+            None if residual is None else residual[cuts[i]:cuts[i + 1]]), range(n))
+        return np.concatenate(parts)
+
+    def _moe(self, layer: int, x, residual, par=True):
+        """moe_decode, the selected experts run on the threads (the same
+        router, top-K, expert_forward and combine as orc_moe_decode)."""
+        if not par or self.nthreads == 1:
+            out, _, _, lg = moe_decode(self.moe, self.images[layer], self.routers[layer], x,
+                                       residual=residual)
+            return out, lg
+        if self._eb is None:
+            self._eb = offsets(self.moe).expert_bytes
+        lg = router_logits(self.routers[layer], x)
+        idx, w = select_topk(lg, softmax(lg), self.moe.top_k, bool(self.moe.norm_topk_prob))
+        img, eb = self.images[layer], self._eb
+        outs = self._map(lambda e: expert_forward(self.moe, img[e * eb:(e + 1) * eb], x),
+                         [int(e) for e in idx])
+        return combine(np.stack(outs), w, residual), lg
+
+    def _note_margin(self, lg) -> float:
+        if self.moe.top_k >= self.moe.num_experts:
+            return np.inf
+        srt = np.sort(lg)[::-1]
+        k = self.moe.top_k
+        return float(srt[k - 1] - srt[k])
 
     def reset(self) -> None:
         """InferenceEngine.reset (:159-163)."""
@@ -334,36 +397,73 @@ class DecoderOracle:
         self.kc[:] = 0
         self.vc[:] = 0
 
+    def _qkv(self, layer: int, res, pos: int, par=True):
+        """:181-220: the normed input's q (returned) and k/v (into the cache)."""
+        t, nh, nkv, hd = self.t, self.nh, self.nkv, self.hd
+        xn = rmsnorm(res, t["in_norm"][layer], self.eps)                        # :181-184
+        q = self._matvec(t["q"][layer], xn, par=par)                            # :185-190
+        k = self._matvec(t["k"][layer], xn, par=par)
+        v = self._matvec(t["v"][layer], xn, par=par)
+        if self.qk_norm:                                                        # :199-208
+            q = head_rmsnorm(q, nh, hd, t["q_norm"][layer], self.eps)
+            k = head_rmsnorm(k, nkv, hd, t["k_norm"][layer], self.eps)
+        q = rope(q, nh, hd, self.theta, pos)                                    # :210-213
+        k = rope(k, nkv, hd, self.theta, pos)
+        self.kc[layer, pos] = k                                                 # :215-220
+        self.vc[layer, pos] = v
+        return q
+
+    def _after_attention(self, layer: int, res, q, pos: int, par=True):
+        """:226-266: attention over positions 0..pos, o_proj + residual, the
+        post-attention norm and the MoE block (with its residual).  Returns
+        the layer output and the router's K-th/(K+1)-th logit gap."""
+        t = self.t
+        a = attention(q, self.kc[layer], self.vc[layer], self.nh, self.nkv, self.hd, pos + 1)
+        res2 = self._matvec(t["o"][layer], a, residual=res, par=par)            # :227-233
+        hmid = rmsnorm(res2, t["post_norm"][layer], self.eps)                   # :234-236
+        out, lg = self._moe(layer, hmid, res2, par=par)                         # :240-266
+        return out, self._note_margin(lg)
+
+    def _logits(self, res):
+        xn = rmsnorm(res, self.t["final_norm"], self.eps)                       # :142-144
+        logits = self._matvec(self.t["lm_head"], xn)                            # :145-147
+        return argmax(logits), logits                                           # :151-155
+
     def step(self, token: int):
         """One forward step; returns (greedy next token, logits f32 [vocab])."""
         if self.pos >= self.max_seq:
             raise ValueError("KV cache full")
-        t, pos = self.t, self.pos
-        nh, nkv, hd = self.nh, self.nkv, self.hd
-        res = embed(t["embed"], token)                                          # :129-131
+        pos = self.pos
+        res = embed(self.t["embed"], token)                                     # :129-131
         self.route_margin = np.inf
         for layer in range(self.L):
-            xn = rmsnorm(res, t["in_norm"][layer], self.eps)                    # :181-184
-            q = matvec_bf16(t["q"][layer], xn)                                  # :185-190
-            k = matvec_bf16(t["k"][layer], xn)
-            v = matvec_bf16(t["v"][layer], xn)
-            if self.qk_norm:                                                    # :199-208
-                q = head_rmsnorm(q, nh, hd, t["q_norm"][layer], self.eps)
-                k = head_rmsnorm(k, nkv, hd, t["k_norm"][layer], self.eps)
-            q = rope(q, nh, hd, self.theta, pos)                                # :210-213
-            k = rope(k, nkv, hd, self.theta, pos)
-            self.kc[layer, pos] = k                                             # :215-220
-            self.vc[layer, pos] = v
-            a = attention(q, self.kc[layer], self.vc[layer], nh, nkv, hd, pos + 1)  # :226
-            res2 = matvec_bf16(t["o"][layer], a, residual=res)                  # :227-233
-            hmid = rmsnorm(res2, t["post_norm"][layer], self.eps)               # :234-236
-            res, _, _, lg = moe_decode(self.moe, self.images[layer], self.routers[layer],
-                                       hmid, residual=res2)                     # :240-266
-            if self.moe.top_k < self.moe.num_experts:
-                srt = np.sort(lg)[::-1]
-                k = self.moe.top_k
-                self.route_margin = min(self.route_margin, float(srt[k - 1] - srt[k]))
+            q = self._qkv(layer, res, pos)
+            res, m = self._after_attention(layer, res, q, pos)
+            self.route_margin = min(self.route_margin, m)
         self.pos += 1                                                           # :138
-        xn = rmsnorm(res, t["final_norm"], self.eps)                            # :142-144
-        logits = matvec_bf16(t["lm_head"], xn)                                  # :145-147
-        return argmax(logits), logits                                           # :151-155
+        return self._logits(res)
+
+    def prefill(self, tokens):
+        """The prompt, as len(tokens) step() calls would run it (the
+        reference forwards a prompt token by token, Sources/bench/main.swift:
+        139-141), but layer by layer with the tokens of a layer on the
+        threads: token i's values depend only on the cache rows of tokens
+        <= i of the same layer, and all of a layer's rows are written before
+        any of its attention runs.  Returns the last token's (greedy next
+        token, logits); the KV cache and position end as after the steps, bit
+        for bit, and route_margin is the last token's."""
+        tokens = [int(t) for t in tokens]
+        T, p0 = len(tokens), self.pos
+        if T < 1 or p0 + T > self.max_seq:
+            raise ValueError("KV cache full")
+        res = [embed(self.t["embed"], tok) for tok in tokens]                   # :129-131
+        margins = [np.inf] * T
+        for layer in range(self.L):
+            qs = self._map(lambda i: self._qkv(layer, res[i], p0 + i, par=False), range(T))
+            outs = self._map(lambda i: self._after_attention(layer, res[i], qs[i], p0 + i,
+                                                             par=False), range(T))
+            res = [o for o, _ in outs]
+            margins = [min(a, m) for a, (_, m) in zip(margins, outs)]
+        self.route_margin = margins[-1]
+        self.pos += T
+        return self._logits(res[-1])

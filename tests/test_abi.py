@@ -56,6 +56,43 @@ def test_swift_binding_names_only_declared_symbols():
         assert re.search(r"\b%s;" % t, header), t
 
 
+def _gfx950_code_objects(so_path):
+    """The gfx950 code objects embedded in a library built here (the
+    .hip_fatbin section holds one clang offload bundle per .hip file)."""
+    import struct
+    data = subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", so_path,
+                           "/dev/stdout"], capture_output=True, check=True).stdout
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    out = []
+    for m in re.finditer(re.escape(magic), data):
+        p = m.start()
+        (n,) = struct.unpack_from("<Q", data, p + len(magic))
+        q = p + len(magic) + 8
+        for _ in range(n):
+            off, size, tl = struct.unpack_from("<QQQ", data, q)
+            triple = data[q + 24:q + 24 + tl].decode()
+            q += 24 + tl
+            if triple.endswith("gfx950"):
+                out.append(data[p + off:p + off + size])
+    return out
+
+
+def test_device_code_has_no_packed_fp32(tmp_path):
+    """Packed-FP32 VALU instructions are disabled for every device pass."""
+    objdump = "/opt/rocm/lib/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not installed")
+    cos = _gfx950_code_objects(_lib.LIB_PATH)
+    assert len(cos) >= 7
+    for i, co in enumerate(cos):
+        f = tmp_path / f"co{i}.o"
+        f.write_bytes(co)
+        dis = subprocess.run([objdump, "-d", str(f)], capture_output=True, text=True,
+                             check=True).stdout
+        assert dis.count("\n") > 0
+        assert not re.search(r"\bv_pk_(fma|mul|add)_f32\b", dis), f"code object {i}"
+
+
 def test_abi_version():
     assert _lib.load().m1moe_abi_version() == 1
 

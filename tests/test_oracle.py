@@ -117,7 +117,8 @@ def test_dequant_constant_nibbles(nib):
 
 # ---- matvec --------------------------------------------------------------
 
-def test_matvec_integer_special_case_is_exact():
+@pytest.mark.parametrize("lanes", [False, True])
+def test_matvec_integer_special_case_is_exact(lanes):
     # s = 1, b = 0, small integer x: an integer matvec, exact in f32
     s = orc.shape(2048, 2, 1, 64, 64)
     blk = make_block(s, scale=1.0, bias=0.0)
@@ -125,18 +126,19 @@ def test_matvec_integer_special_case_is_exact():
     x = RNG.integers(-3, 4, size=2048).astype(np.float32)
     q = np.stack([(w >> (4 * j)) & 0xF for j in range(8)], axis=-1).reshape(64, 2048)
     want = (q.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
-    got = orc.matvec4bit(w, sc, bi, x, 64, 2048, 64)
+    got = orc.matvec4bit(w, sc, bi, x, 64, 2048, 64, lanes=lanes)
     assert np.array_equal(got, want)
 
 
-def test_matvec_all_zero_nibbles_reduces_to_bias_times_group_sums():
+@pytest.mark.parametrize("lanes", [False, True])
+def test_matvec_all_zero_nibbles_reduces_to_bias_times_group_sums(lanes):
     s = orc.shape(1024, 2, 1, 64, 64)
     blk = make_block(s, nib=0)
     w, sc, bi = orc.proj_arrays(s, blk, 0)
     x = RNG.normal(size=1024).astype(np.float32)
     gsum = x.astype(np.float64).reshape(16, 64).sum(axis=1)
     want = bf16_val(bi).astype(np.float64) @ gsum
-    got = orc.matvec4bit(w, sc, bi, x, 64, 1024, 64)
+    got = orc.matvec4bit(w, sc, bi, x, 64, 1024, 64, lanes=lanes)
     assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
 
 
@@ -152,10 +154,29 @@ def test_matvec_matches_f64_brute_force(gs):
             np.repeat(bf16_val(bi), gs, axis=1).astype(np.float64)   # unrounded weights
         x = RNG.normal(size=cols).astype(np.float32)
         want = W @ x.astype(np.float64)
-        got = orc.matvec4bit(w, sc, bi, x, rows, cols, gs)
+        got = orc.matvec4bit(w, sc, bi, x, rows, cols, gs, lanes=True)
         got64 = orc.matvec4bit_f64(w, sc, bi, x, rows, cols, gs)
         assert np.allclose(got64, want, rtol=1e-12, atol=1e-12)
         assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-6
+
+
+@pytest.mark.parametrize("cols,gs", [(64, 32), (128, 64), (576, 64), (1024, 32), (2048, 128),
+                                     (14336, 64)])
+def test_matvec_vector_form_equals_lanes_bit_for_bit(cols, gs):
+    """The eight-lanes-at-a-time form against the lane-by-lane restatement:
+    fewer words than lanes (64, 128 columns), a partial last stride (576),
+    two scale groups per eight words (gs 32), the Mixtral down row (14336).
+    x spans 2^-20..2^20 so any change of operation order changes bits."""
+    rows = 96
+    w = RNG.integers(0, 2**32, size=(rows, cols // 8), dtype=np.uint64).astype(np.uint32)
+    sc = (RNG.normal(size=(rows, cols // gs)).astype(np.float32).view(np.uint32) >> 16) \
+        .astype(np.uint16)
+    bi = (RNG.normal(size=(rows, cols // gs)).astype(np.float32).view(np.uint32) >> 16) \
+        .astype(np.uint16)
+    x = (RNG.normal(size=cols) * 2.0 ** RNG.integers(-20, 21, size=cols)).astype(np.float32)
+    a = orc.matvec4bit(w, sc, bi, x, rows, cols, gs)
+    b = orc.matvec4bit(w, sc, bi, x, rows, cols, gs, lanes=True)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 # ---- SwiGLU ------------------------------------------------------------------

@@ -295,3 +295,41 @@ def test_decoder_incremental_equals_whole_sequence(qk_norm, nh, nkv):
         nxt, lg = dec.step(int(tok))
         assert nxt == int(np.argmax(lg))
     assert dec.pos == 4
+
+
+@pytest.mark.parametrize("qk_norm,nh,nkv", [(True, 2, 1), (False, 4, 2)])
+def test_decoder_threads_and_prefill_equal_single_thread_steps(qk_norm, nh, nkv):
+    """Threaded steps (rows of every matvec and the selected experts on four
+    threads) and the batched prefill (tokens of a layer on four threads)
+    produce step()'s bits: logits, greedy tokens and every cache row."""
+    theta, eps = 10000.0, 1e-5
+    t, images, routers, cfg = tiny_decoder(qk_norm=qk_norm, nh=nh, nkv=nkv)
+    tokens = [int(v) for v in np.random.default_rng(11).integers(0, cfg["vocab"], 10)]
+
+    def make(n):
+        d = orc.DecoderOracle(TINY_MOE, cfg["L"], cfg["vocab"], nh, nkv, cfg["hd"], 16, qk_norm,
+                              theta, eps, t, images, routers, nthreads=n)
+        d.split_min = 0
+        return d
+    one, four, pre = make(1), make(4), make(4)
+    try:
+        for tok in tokens[:7]:
+            a, b = one.step(tok), four.step(tok)
+            assert a[0] == b[0] and np.array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+        c = pre.prefill(tokens[:7])
+        assert c[0] == a[0] and np.array_equal(c[1].view(np.uint32), a[1].view(np.uint32))
+        assert pre.pos == one.pos == 7
+        assert np.array_equal(pre.kc.view(np.uint32), one.kc.view(np.uint32))
+        assert np.array_equal(pre.vc.view(np.uint32), one.vc.view(np.uint32))
+        # a second piece from position 7, then a step
+        c = pre.prefill(tokens[7:])
+        for tok in tokens[7:]:
+            a = one.step(tok)
+        assert c[0] == a[0] and np.array_equal(c[1].view(np.uint32), a[1].view(np.uint32))
+        a, c = one.step(tokens[0]), pre.step(tokens[0])
+        assert np.array_equal(c[1].view(np.uint32), a[1].view(np.uint32))
+        with pytest.raises(ValueError):
+            pre.prefill(list(range(6)))            # 11 + 6 > 16 positions
+    finally:
+        four.close()
+        pre.close()

@@ -443,7 +443,7 @@ class DecoderOracle:
         self.pos += 1                                                           # :138
         return self._logits(res)
 
-    def prefill(self, tokens):
+    def prefill(self, tokens, log=None):
         """The prompt, as len(tokens) step() calls would run it (the
         reference forwards a prompt token by token, Sources/bench/main.swift:
         139-141), but layer by layer with the tokens of a layer on the
@@ -464,6 +464,8 @@ class DecoderOracle:
                                                              par=False), range(T))
             res = [o for o, _ in outs]
             margins = [min(a, m) for a, (_, m) in zip(margins, outs)]
+            if log:
+                log(f"  oracle prefill: layer {layer + 1}/{self.L} of {T} tokens done")
         self.route_margin = margins[-1]
         self.pos += T
         return self._logits(res[-1])

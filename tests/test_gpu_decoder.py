@@ -3,12 +3,16 @@ oracle (oracle/dense_oracle.c, oracle.DecoderOracle), through the C ABI.
 
 Tolerances: every sum on the GPU is f32 in its own order against the
 oracle's f64, so the building blocks are held to relative L2 1e-5 (argmax
-bit-exact).  The MoE block rounds its input and the SwiGLU activations to
-f16 for the nibble dot products (its own parity bar is relative L2 1e-2), so
-decoder logits are held to the north-star bar of relative L2 1e-2, and greedy
-tokens must agree wherever the oracle's top-2 logit margin exceeds the logit
-error bound.
+bit-exact).  The MoE decode splits its f32 inputs and activations into hi +
+lo f16 halves for the nibble dot products, the MoE prefill rounds them to
+one f16 (its own parity bar is relative L2 1e-2), so decoder logits are held
+to the north-star bar of relative L2 1e-2, and greedy tokens must agree
+wherever the oracle's top-2 logit margin exceeds the logit error bound.
+The long cases (cfg4 widths at 2048 positions, cfg1 at 16 layers and 128 +
+128 tokens) run the oracle's prompt layer by layer on up to 16 threads.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -26,6 +30,7 @@ NAMES = {_lib.W_EMBED: "embed", _lib.W_LM_HEAD: "lm_head", _lib.W_FINAL_NORM: "f
          _lib.W_IN_NORM: "in_norm", _lib.W_POST_NORM: "post_norm", _lib.W_Q: "q", _lib.W_K: "k",
          _lib.W_V: "v", _lib.W_O: "o", _lib.W_Q_NORM: "q_norm", _lib.W_K_NORM: "k_norm"}
 LOGIT_TOL = 1e-2
+NTHREADS = max(1, min(16, os.cpu_count() or 1))
 
 
 def bf16(a):
@@ -135,7 +140,7 @@ def test_argmax(ops_ctx, case):
 class Pair:
     """The same seeded model on the GPU (Decoder) and in the oracle."""
 
-    def __init__(self, wl, seed, max_seq, num_layers=None):
+    def __init__(self, wl, seed, max_seq, num_layers=None, nthreads=1):
         self.wl = wl
         L = num_layers or wl.num_layers
         shape = wl.moe.shape(L)
@@ -161,9 +166,11 @@ class Pair:
             routers.append(r)
         self.orc = orc.DecoderOracle(orc.from_moe_shape(shape), L, wl.vocab, wl.num_heads,
                                      wl.num_kv_heads, wl.head_dim, max_seq, wl.qk_norm,
-                                     wl.rope_theta, wl.rms_eps, tensors, images, routers)
+                                     wl.rope_theta, wl.rms_eps, tensors, images, routers,
+                                     nthreads=nthreads)
 
     def close(self):
+        self.orc.close()
         self.dec.close()
         self.ctx.close()
 
@@ -519,6 +526,79 @@ def test_decoder_mixtral_gqa_dims_one_layer():
             g_tok, g_lg = p.dec.forward(int(t), return_logits=True)
             w_tok, w_lg = p.orc.step(int(t))
             check_step(g_tok, g_lg, w_tok, w_lg, f"step {i}")
+    finally:
+        p.close()
+
+
+def _greedy_against_oracle(p, tok, n, pos0, where):
+    """n greedy steps, both sides fed the oracle's token; returns the logits
+    relative L2 of each step and the number of steps whose greedy tokens
+    differ (allowed only inside the top-2 margin, check_step)."""
+    errs, differ = [], 0
+    for i in range(n):
+        g_tok, g_lg = p.dec.forward(int(tok), return_logits=True)
+        w_tok, w_lg = p.orc.step(int(tok))
+        errs.append(check_step(g_tok, g_lg, w_tok, w_lg, f"{where} step {i} (position {pos0 + i})"))
+        differ += int(g_tok != w_tok)
+        tok = w_tok
+        if (i + 1) % 32 == 0:
+            say(f"  {where}: {i + 1}/{n} greedy steps, logits rel L2 max {max(errs):.2e}")
+    return errs, differ
+
+
+def test_decoder_mixtral_width_long_context():
+    """cfg4's regime at two of its 32 layers: Mixtral widths, a 2048-token
+    batched prefill (attention over 32 chunks of 64 positions, RoPE at theta
+    1e6, the grouped MoE prefill at about 512 (token, slot) pairs per
+    expert), then greedy steps at positions 2048..2051 against the oracle."""
+    wl = synth.DECODERS["cfg4"]
+    p = Pair(wl, seed=2048, max_seq=2056, num_layers=2, nthreads=NTHREADS)
+    try:
+        prompt = synth.prompt_tokens(wl, 2048, 2048)
+        say("mixtral-width prefill of 2048 tokens (GPU)")
+        tok, g_lg = p.dec.prefill(prompt, return_logits=True)
+        w_tok, w_lg = p.orc.prefill(prompt, log=say)
+        pre = check_step(tok, g_lg, w_tok, w_lg, "prefill of 2048")
+        assert p.dec.position() == 2048
+        errs, differ = _greedy_against_oracle(p, w_tok, 4, 2048, "mixtral")
+        say(f"  logits rel L2: prefill {pre:.2e}, greedy max {max(errs):.2e}, "
+            f"tokens differing {differ}/4")
+    finally:
+        p.close()
+
+
+def test_decoder_olmoe_16_layers_128_prompt_128_greedy():
+    """cfg1 at full depth and length: 16 OLMoE-width layers, the 128-token
+    prompt in one batch, then 128 greedy steps (positions 128..255)."""
+    wl = synth.DECODERS["cfg1"]
+    p = Pair(wl, seed=2026, max_seq=256, num_layers=16, nthreads=NTHREADS)
+    try:
+        prompt = synth.prompt_tokens(wl, 2026, 128)
+        say("olmoe 16 layers: prefill of 128 tokens")
+        tok, g_lg = p.dec.prefill(prompt, return_logits=True)
+        w_tok, w_lg = p.orc.prefill(prompt, log=say)
+        pre = check_step(tok, g_lg, w_tok, w_lg, "prefill of 128")
+        errs, differ = _greedy_against_oracle(p, w_tok, 128, 128, "olmoe-16")
+        say(f"[depth] layers=16 prefill {pre:.2e} greedy median {np.median(errs):.2e} "
+            f"max {max(errs):.2e} tokens differing {differ}/128")
+    finally:
+        p.close()
+
+
+@pytest.mark.parametrize("layers", [2, 8])
+def test_decoder_olmoe_logit_error_by_depth(layers):
+    """The same model family at 2 and 8 layers (16: the test above): 32-token
+    prompt, 32 greedy steps; records how the logits error grows with depth."""
+    wl = synth.DECODERS["cfg1"]
+    p = Pair(wl, seed=2026, max_seq=64, num_layers=layers, nthreads=NTHREADS)
+    try:
+        prompt = synth.prompt_tokens(wl, 2026, 32)
+        tok, g_lg = p.dec.prefill(prompt, return_logits=True)
+        w_tok, w_lg = p.orc.prefill(prompt)
+        pre = check_step(tok, g_lg, w_tok, w_lg, "prefill of 32")
+        errs, differ = _greedy_against_oracle(p, w_tok, 32, 32, f"olmoe-{layers}")
+        say(f"[depth] layers={layers} prefill {pre:.2e} greedy median {np.median(errs):.2e} "
+            f"max {max(errs):.2e} tokens differing {differ}/32")
     finally:
         p.close()
 

@@ -105,6 +105,20 @@ def test_prefill_cfg2_mixtral_shape():
         c.close()
 
 
+def test_prefill_cfg2_shape_2048_tokens():
+    """cfg4's MoE prefill regime: the Mixtral MoE shape at T=2048 (about 512
+    (token, slot) pairs per expert, eight 64-pair tiles each), every token
+    against the oracle."""
+    c = make_case("cfg2", seed=2048)
+    try:
+        got, gidx, gw, x32, res = _run_prefill(c, 2048)
+        counts = np.bincount(gidx.ravel(), minlength=c.shape.num_experts)
+        say(f"  pairs per expert: {counts.tolist()}")
+        _check(c, 2048, got, gidx, gw, x32, res)
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("kw", [
     dict(hidden=1024, num_experts=16, top_k=4, intermediate=512, group_size=128),
     dict(hidden=1152, num_experts=8, top_k=2, intermediate=640, group_size=64),

@@ -10,12 +10,17 @@ To keep the expert weights out of the 256 MB Infinity Cache, R distinct
 layer replicas (R * 216 MiB) are resident and each step runs one token
 through all R of them in order (one HIP graph launch); `value` counts
 layer-tokens per second.  All inputs are resident in HBM before timing.
+The inputs rotate over four graphs (graph j gives replica r the input drawn
+for replica (r + j) % R), so the expert selection changes from step to step;
+the replicas are not chained output -> input (the configured input is a bf16
+N(0,1) activation; the chained form is the whole decoder, cfg1 / cfg4).
 
 A step = one token through the MoE block of each of the R replicas
 (router + top-K, expert dispatch, gate/up/SwiGLU, down, combine + residual).
 
-The CPU baseline is the scalar oracle (oracle/, one thread) timed on a
-bounded sample of the same workload, in the same run.
+The CPU baseline is the scalar oracle (oracle/, its lane-by-lane matvec)
+timed on bounded samples of the same workload in the same run: one thread
+(`cpu_baseline`) and the box's 16-thread share (`cpu_baseline_all_cores`).
 """
 from __future__ import annotations
 
@@ -39,6 +44,60 @@ PREFILL_METRIC = "MoE-layer prefill tok/s (512 tokens, Zipf(1.1) expert loads); 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_kernel_name(shape) -> str:
+    """The decode kernel the library selects for this shape on a 256-CU
+    MI355X (ctx.cpp: decode_cu_fits and the CU count)."""
+    K, I = shape.top_k, shape.intermediate
+    fits = (shape.hidden == 2048 and shape.num_experts <= 256 and K <= 8 and 8 % K == 0
+            and shape.group_size in (32, 64, 128) and I in (1024, 2048)
+            and K * I in (8192, 16384))
+    return "moe_decode_cu_kernel" if fits else "moe_decode_kernel"
+
+
+def cpu_threads() -> int:
+    """Host threads for the all-cores CPU baseline: the box's CPU share."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_decode_baselines(args, synth, orc, oshape, img, router, xs, res):
+    """The scalar oracle (lane-by-lane matvec restatement) timed on the host:
+    one thread, token after token (BASELINE's primary figure), then all the
+    threads of the box's share, tokens in parallel (orc.moe_prefill: per-token
+    decode on each thread).  About args.cpu_seconds of work each."""
+    orc.set_scalar(True)
+    try:
+        x32 = synth.bf16_to_f32(xs)
+        n, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_seconds:
+            t1 = time.perf_counter()
+            orc.moe_decode(oshape, img, router, x32[n % len(x32)], res[n % len(res)])
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        one = {"value": round(n / t_cpu, 3), "unit": "layer-tok/s", "cores": 1, "kind": "port",
+               "sample": f"{n} tokens of {args.config} decode (replica-0 experts, the bench's "
+                         f"inputs) through the scalar oracle on 1 thread ({t_cpu:.1f}s); "
+                         f"host CPU: {cpu_model()}"}
+        log(f"cpu baseline (1 thread): {one['value']} layer-tok/s")
+        nt = cpu_threads()
+        T = 2 * nt
+        X = np.stack([x32[i % len(x32)] for i in range(T)])
+        Rs = np.stack([res[i % len(res)] for i in range(T)])
+        n, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_seconds:
+            t1 = time.perf_counter()
+            orc.moe_prefill(oshape, img, router, X, Rs, nthreads=nt)
+            t_cpu += time.perf_counter() - t1
+            n += T
+        allc = {"value": round(n / t_cpu, 3), "unit": "layer-tok/s", "cores": nt, "kind": "port",
+                "sample": f"{n} tokens of {args.config} decode through the scalar oracle, "
+                          f"{T} tokens at a time on {nt} threads ({t_cpu:.1f}s); "
+                          f"host CPU: {cpu_model()}"}
+        log(f"cpu baseline ({nt} threads): {allc['value']} layer-tok/s")
+    finally:
+        orc.set_scalar(False)
+    return one, allc
 
 
 def algorithmic_bytes(shape, expert_bytes: int, x_bytes: int, with_residual: bool) -> int:
@@ -86,8 +145,9 @@ def main() -> int:
                          "such job)")
     ap.add_argument("--replicas", type=int, default=0,
                     help="distinct layer replicas (default: >= 1 GiB of selected experts per pass)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="bound on the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="bound on each CPU-baseline sample, one thread and all threads "
+                         "(0 disables them)")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--eager", action="store_true",
                     help="cfg1/cfg4: launch every step's kernels from the host instead of "
@@ -167,19 +227,37 @@ def main() -> int:
         log("parity FAILED; not reporting throughput")
         return 1
 
-    ctx.graph_begin()
-    for r in range(R):
-        blk.forward(r, dx[r], "bf16", dres[r], dout[r])
-    graph = ctx.graph_end()
+    # The replicas are not chained output -> input: the configured input is a
+    # bf16 N(0,1) activation while a layer's output is the f32 residual stream,
+    # which without the decoder's RMSNorm grows from layer to layer (the chained
+    # form is the whole decoder, --config cfg1 / cfg4).  The inputs rotate
+    # instead: graph j feeds replica r the input and residual drawn for replica
+    # (r + j) % R, and the graphs are replayed in turn, so every replica's
+    # expert selection changes from step to step.
+    G = min(4, R)
+    sel = []
+    for j in range(G):
+        q = j % R
+        blk.forward(0, dx[q], "bf16", dres[q], dout[0], didx, None)
+        ctx.sync()
+        sel.append(sorted(didx.download(np.int32).tolist()))
+    log(f"replica 0 selects, over the {G} input rotations: {sel}")
+    graphs = []
+    for j in range(G):
+        ctx.graph_begin()
+        for r in range(R):
+            q = (r + j) % R
+            blk.forward(r, dx[q], "bf16", dres[q], dout[r])
+        graphs.append(ctx.graph_end())
 
-    for _ in range(args.warmup):
-        graph.launch()
+    for i in range(args.warmup):
+        graphs[i % G].launch()
     ctx.sync()
     ev0, ev1 = ctx.event(), ctx.event()
     ctx.sync()
     ev0.record()
-    for _ in range(args.steps):
-        graph.launch()
+    for i in range(args.steps):
+        graphs[i % G].launch()
     ev1.record()
     ctx.sync()
     ms = ev0.elapsed_ms(ev1)
@@ -190,19 +268,9 @@ def main() -> int:
     gbs = bytes_tok / (layer_us * 1e-6) / 1e9
     log(f"{ms_per_step:.4f} ms/step, {layer_us:.3f} us/layer-token, {gbs:.0f} GB/s")
 
-    cpu = None
+    cpu = cpu_all = None
     if args.cpu_seconds > 0:
-        x32 = synth.bf16_to_f32(xs[0])
-        n, t_cpu = 0, 0.0
-        while t_cpu < args.cpu_seconds:
-            t1 = time.perf_counter()
-            orc.moe_decode(oshape, img0, router0, x32, res[0])
-            t_cpu += time.perf_counter() - t1
-            n += 1
-        cpu = {"value": round(n / t_cpu, 3), "unit": "layer-tok/s", "cores": 1, "kind": "port",
-               "sample": f"{n} tokens of {args.config} replica-0 decode through the scalar "
-                         f"oracle on 1 thread ({t_cpu:.1f}s); host CPU: {cpu_model()}"}
-        log(f"cpu baseline: {cpu['value']} layer-tok/s")
+        cpu, cpu_all = cpu_decode_baselines(args, synth, orc, oshape, img0, router0, xs, res)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -223,19 +291,20 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4 weights x f16 inputs -> f32",
+        "dtype": "u4 weights x f16 pairs (bf16 x exact in f16; f32 act as hi+lo f16) -> f32",
         "data": "synthetic (seeded; random-init experts/router)",
         "config": {"workload": wl.description, "config": args.config, "hidden": h,
                    "num_experts": shape.num_experts, "top_k": K,
                    "intermediate": shape.intermediate, "group_size": shape.group_size,
                    "replicas": R, "tokens_per_step": 1, "x_dtype": "bf16",
-                   "residual": "f32"},
+                   "residual": "f32", "input_rotations": G},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "kernel": "moe_decode_kernel (the whole MoE block, one launch per "
-                               "layer-token)",
+                     "kernel": decode_kernel_name(shape) + " (the whole MoE block, one "
+                                                             "launch per layer-token)",
                      "bytes_per_launch": bytes_tok, "us_per_launch": round(layer_us, 4)},
         "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
         "parity": {"topk_exact": idx_ok, "rel_l2": rel},
     }
     print(json.dumps(line), flush=True)
@@ -503,6 +572,33 @@ def bench_prefill(args, m, synth) -> int:
     log(f"{us_layer:.2f} us per 512-token layer prefill, {tok_s:.0f} tok/s, "
         f"{tflops:.1f} TFLOP/s ({100 * tflops / PEAK_F16_TFLOPS:.1f}% of f16 MFMA peak), "
         f"{gbs:.0f} GB/s of weights+activations")
+    cpu = cpu_all = None
+    if args.cpu_seconds > 0:
+        # the 512-token prefill is 512 independent token decodes on the CPU (the
+        # reference forwards a prompt token by token): a bounded prefix of
+        # replica 0's tokens, one thread, then all threads
+        oshape = orc.from_moe_shape(shape)
+        x32, base = synth.bf16_to_f32(xs[0]), []
+        orc.set_scalar(True)
+        try:
+            for nt in (1, cpu_threads()):
+                n, t_cpu = 0, 0.0
+                while t_cpu < args.cpu_seconds and n < T:
+                    m_ = min(2 * nt, T - n)
+                    t1 = time.perf_counter()
+                    orc.moe_prefill(oshape, img0, router0, x32[n:n + m_], res[0][n:n + m_], bias,
+                                    nthreads=nt)
+                    t_cpu += time.perf_counter() - t1
+                    n += m_
+                base.append({"value": round(n / t_cpu, 3), "unit": "tok/s", "cores": nt,
+                             "kind": "port",
+                             "sample": f"the first {n} of the {T} cfg3 tokens (replica 0, Zipf "
+                                       f"bias) through the scalar oracle on {nt} thread(s) "
+                                       f"({t_cpu:.1f}s); host CPU: {cpu_model()}"})
+                log(f"cpu baseline ({nt} threads): {base[-1]['value']} tok/s")
+        finally:
+            orc.set_scalar(False)
+        cpu, cpu_all = base
     line = {
         "metric": PREFILL_METRIC, "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
@@ -516,7 +612,8 @@ def bench_prefill(args, m, synth) -> int:
                      "traffic": None, "flops_per_launch": flops,
                      "us_per_launch": round(us_layer, 3),
                      "hbm_gbs_of_algorithmic_bytes": round(gbs, 1)},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
         "parity": {"topk_exact": idx_ok, "rel_l2": rel, "moe_part_rel_l2": moe_rel},
     }
     print(json.dumps(line), flush=True)

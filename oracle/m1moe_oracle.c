@@ -204,13 +204,21 @@ __attribute__((target("avx2,fma"))) static void matvec4bit_avx2(
     }
 }
 
+/* Set by orc_set_scalar(): every matvec4bit runs the lane-by-lane
+ * restatement (the benchmark's scalar CPU baseline).  Set it before any
+ * thread uses the oracle. */
+static int g_scalar_only = 0;
+
+void orc_set_scalar(int32_t on) { g_scalar_only = on != 0; }
+
 /* Shaders.metal:39-92 (matvec4bit): the AVX2 form where the CPU has it and
  * the row length is a whole number of eight-word lane blocks, else the
  * lane-by-lane restatement. */
 void orc_matvec4bit(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                     const float* x, float* y, int32_t out_dim, int32_t in_dim,
                     int32_t gs) {
-    const int have_avx2 = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    const int have_avx2 = !g_scalar_only && __builtin_cpu_supports("avx2") &&
+                          __builtin_cpu_supports("fma");
     float* xt = NULL;
     if (have_avx2 && in_dim % 64 == 0) xt = (float*)malloc((size_t)in_dim * sizeof(float));
     if (xt) {

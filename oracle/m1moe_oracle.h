@@ -66,6 +66,8 @@ void orc_matvec4bit_lanes(const uint32_t* w, const uint16_t* s, const uint16_t* 
 void orc_matvec4bit(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                     const float* x, float* y, int32_t out_dim, int32_t in_dim,
                     int32_t gs);
+/* on != 0: orc_matvec4bit always runs the lane-by-lane restatement. */
+void orc_set_scalar(int32_t on);
 
 /* Double-precision brute force of the same matvec: sum_c (n*s+b)*x_c. */
 void orc_matvec4bit_f64(const uint32_t* w, const uint16_t* s, const uint16_t* b,

@@ -53,6 +53,7 @@ def load() -> ctypes.CDLL:
         "orc_dequant_proj": (None, [POINTER(OrcShape), P, c_int32, P]),
         "orc_matvec4bit": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
         "orc_matvec4bit_lanes": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
+        "orc_set_scalar": (None, [c_int32]),
         "orc_matvec4bit_f64": (None, [P, P, P, P, P, c_int32, c_int32, c_int32]),
         "orc_swiglu": (None, [P, P, P, c_int32]),
         "orc_router_logits": (None, [P, P, c_int32, c_int32, P]),
@@ -112,6 +113,13 @@ def dequant_proj(s: OrcShape, block: np.ndarray, proj: int) -> np.ndarray:
     out = np.empty((rows, cols), dtype=np.float32)
     load().orc_dequant_proj(ctypes.byref(s), _p(block), proj, _p(out))
     return out
+
+
+def set_scalar(on: bool) -> None:
+    """Every matvec4bit (and so every expert, decode and prefill) runs the
+    lane-by-lane scalar restatement while on (the benchmark's scalar CPU
+    baseline); the same bits either way."""
+    load().orc_set_scalar(1 if on else 0)
 
 
 def matvec4bit(w, sc, bi, x, out_dim, in_dim, gs, lanes=False) -> np.ndarray:

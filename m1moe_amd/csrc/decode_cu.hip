@@ -87,6 +87,30 @@ struct CuLDS {
 
 // ---- routing ---------------------------------------------------------------------
 
+// Expert i's rank = the number of experts ahead of it (a larger logit, or an
+// equal one at a lower index), counted by P = 2^LP lanes over M = 2^LEP / P
+// experts each (the 512 threads cover the 2^LEP experts exactly); the
+// segment's last lane writes s.idx[rank] = i for the K first ranks.
+template <int LEP>
+__device__ __forceinline__ void rank_cu(int t, int E, int K, CuLDS& s) {
+    constexpr int LP = LEP == 6 ? 3 : (LEP == 7 ? 2 : 1);
+    constexpr int P = 1 << LP, M = 1 << (LEP - LP);
+    static_assert((1 << LEP) * P == kT, "one thread per (expert, part)");
+    const int i = t >> LP, q = t & (P - 1), j0 = q * M;
+    const float my = s.v[i];
+    float cnt = 0.f;
+#pragma unroll
+    for (int m = 0; m < M; m += 4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(&s.v[j0 + m]);
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            cnt += ((vv[u] > my) || (vv[u] == my && j0 + m + u < i)) ? 1.f : 0.f;
+    }
+    cnt = seg_sum_c<P>(cnt);  // total in the segment's last lane
+    if (i < E && q == P - 1 && (int)cnt < K) s.idx[(int)cnt] = i;
+}
+
 // Obtains the routing: the given one, or the published logits (wave 0 polls
 // replica g % kLogitRep) ranked by all threads: expert i's rank is the
 // number of experts ahead of it (larger logit, or equal logit and lower
@@ -150,32 +174,15 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
         if (lane == 0) s.ok = ok ? 1 : 0;
     }
     __syncthreads();
-    // ep = E rounded up to a power of two; P (a power of two <= 8) lanes per
-    // expert, each comparing M = ep / P experts (a multiple of 4 for ep >= 4,
-    // read 4 at a time; ep < 4 reads padding, -inf at indices above every
-    // expert)
-    const int lep = E <= 1 ? 0 : 32 - __clz(E - 1);
-    const int lp = lep >= 2 ? min(lep - 2, 9 - lep) : 0;
-    const int lm = lep - lp;
-    const int i = t >> lp, q = t & ((1 << lp) - 1);
-    float cnt = 0.f;
-    if (i < (1 << lep)) {
-        const float my = s.v[i];
-        const int j0 = q << lm;
-#pragma unroll 2
-        for (int m = 0; m < max(1 << lm, 4); m += 4) {
-            const float4 v4 = *reinterpret_cast<const float4*>(&s.v[j0 + m]);
-            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = j0 + m + u;
-                cnt += ((vv[u] > my) || (vv[u] == my && j < i)) ? 1.f : 0.f;
-            }
-        }
-    }
-    const int P = 1 << lp;
-    if (P > 1) cnt = seg_sum(cnt, P);  // total in the segment's last lane
-    if (i < E && q == P - 1 && (int)cnt < K) s.idx[(int)cnt] = i;
+    // ranks over ep = 2^LEP experts (E rounded up, at least 64; the padding
+    // is -inf at indices above every expert)
+    const int lep = E <= 64 ? 6 : (E <= 128 ? 7 : 8);
+    if (lep == 6)
+        rank_cu<6>(t, E, K, s);
+    else if (lep == 7)
+        rank_cu<7>(t, E, K, s);
+    else
+        rank_cu<8>(t, E, K, s);
     __syncthreads();
 }
 
@@ -357,17 +364,20 @@ __device__ __forceinline__ void gu_load_cu(const FusedArgs& a, const Layout& L, 
     const uint8_t* uw_b = blk + (real ? L.up_w : 0);
     const uint8_t* sb_b = a.dec_base + eu * a.dec_bytes;
     constexpr uint32_t groups = kH >> (5 + GSL);
-#pragma unroll
-    for (int u = 0; u < UG; ++u) {
-        const uint32_t wo = real ? (uint32_t)(row0 + u) * (kH / 2) + (uint32_t)lane * 16u : 0u;
-        t.gw[u] = ld_stream(gw_b + wo);
-        t.uw[u] = ld_stream(uw_b + wo);
-    }
+    // the scales and biases first: loads return in issue order, so the
+    // compute of row 0 can start once its own words are in, while the
+    // later rows are still arriving
 #pragma unroll
     for (int q = 0; q < UG / 4; ++q) {
         const uint32_t so = real ? (((uint32_t)(row0 / 4 + q) * groups + ((uint32_t)lane >> GSL)) * 32u) : 0u;
         t.sb[2 * q] = ld_stream(sb_b + so);
         t.sb[2 * q + 1] = ld_stream(sb_b + so + 16);
+    }
+#pragma unroll
+    for (int u = 0; u < UG; ++u) {
+        const uint32_t wo = real ? (uint32_t)(row0 + u) * (kH / 2) + (uint32_t)lane * 16u : 0u;
+        t.gw[u] = ld_stream(gw_b + wo);
+        t.uw[u] = ld_stream(uw_b + wo);
     }
 }
 
@@ -391,6 +401,9 @@ __device__ __forceinline__ void gu_compute_cu(int wave, int lane, const GUTileCU
             v[2 * u] = fmaf(bf16_pick(gsb, kSelLo) * sc, dg, bf16_pick(gsb, kSelHi) * xc.xs * inv);
             v[2 * u + 1] =
                 fmaf(bf16_pick(usb, kSelLo) * sc, du, bf16_pick(usb, kSelHi) * xc.xs * inv);
+            // row by row as the rows arrive (the scheduler would otherwise
+            // gather every row's wait ahead of the first row's arithmetic)
+            __builtin_amdgcn_sched_barrier(0);
         }
         float pg, pu;
         reduce8_wave(v, lane, pg, pu);
@@ -564,7 +577,7 @@ __device__ __forceinline__ uint4 ld_coherent16(const uint32_t* p) {
 
 // UG = K * I / 2048: gate/up rows per wave; the workgroup's 8 * UG act rows
 // are UG / 4 chunks of 32.
-template <int UG, int GSL>
+template <int UG, int GSL, bool LO>
 __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     constexpr int NC = UG / 4;
     __shared__ CuLDS s;
@@ -701,26 +714,15 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     DNTileCU<NC> dt;
     dn_load_cu<NC, GSL>(a, eg, wg_row0 / 32, t, dt);
 
-    if (wave == kW - 1) {
-        weights_cu(a, lane, s);
-        if (g == 0 && ok_run && lane < K) {
-            if (a.user_idx) a.user_idx[lane] = s.idx[lane];
-            if (a.user_w) a.user_w[lane] = s.w[lane];
-        }
-    }
-
     // ---- gate/up + SwiGLU, then the act chunks ----------------------------------------
-    if (eg >= 0) {
-        // bf16 inputs are exact in f16: the lo half is 0
-        if (!a.x_bf16)
-            gu_compute_cu<UG, true>(wave, lane, gt, xc, inv, s);
-        else
-            gu_compute_cu<UG, false>(wave, lane, gt, xc, inv, s);
-    }
-    DNExpCU<NC> dx;
-    if (eg >= 0) dn_expand_cu<NC>(dt, dx);  // (waits for this wave's down loads)
+    // (LO: an f32 input's lo halves take part; a bf16 input is exact in f16)
+    if (eg >= 0) gu_compute_cu<UG, LO>(wave, lane, gt, xc, inv, s);
+    // the act chunks are prepared (wave 0) while the other waves expand their
+    // down nibbles (the down bytes, requested last, are the last to arrive)
     __syncthreads();
     if (wave == 0 && eg >= 0) prep_chunks<UG>(lane, s);
+    DNExpCU<NC> dx;
+    if (eg >= 0) dn_expand_cu<NC>(dt, dx);  // (waits for this wave's down loads)
     __syncthreads();
 
     // ---- down partials of all 2048 rows from this workgroup's columns ------------------
@@ -732,6 +734,16 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     for (int r = 0; r < 4; ++r)
         st_u32(a.cu_part + ((size_t)((t + (kH / 4) * r) >> 3) * kNG + g) * kRows + (t & 7),
                tagged(pr[r], parity));
+
+    // the combine weights, off the path to the partial stores (read after the
+    // barrier that follows the reduction)
+    if (wave == kW - 1) {
+        weights_cu(a, lane, s);
+        if (g == 0 && ok_run && lane < K) {
+            if (a.user_idx) a.user_idx[lane] = s.idx[lane];
+            if (a.user_w) a.user_w[lane] = s.w[lane];
+        }
+    }
 
     // ---- reduce: thread t takes source workgroup t % 256, rows 4 (t / 256) .. +3, ------
     // reading until every value carries this launch's parity (a source still
@@ -785,12 +797,20 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     if (t == 0) st_u32(a.cu_seen + g, tag);
 }
 
+template <int UG, int GSL>
+void launch_lo(const FusedArgs& a, hipStream_t st) {
+    if (a.x_bf16)
+        hipLaunchKernelGGL((moe_decode_cu_kernel<UG, GSL, false>), dim3(kNG), dim3(kT), 0, st, a);
+    else
+        hipLaunchKernelGGL((moe_decode_cu_kernel<UG, GSL, true>), dim3(kNG), dim3(kT), 0, st, a);
+}
+
 template <int UG>
 int launch_ug(const FusedArgs& a, hipStream_t st) {
     switch (a.gs) {
-        case 32: hipLaunchKernelGGL((moe_decode_cu_kernel<UG, 0>), dim3(kNG), dim3(kT), 0, st, a); break;
-        case 64: hipLaunchKernelGGL((moe_decode_cu_kernel<UG, 1>), dim3(kNG), dim3(kT), 0, st, a); break;
-        case 128: hipLaunchKernelGGL((moe_decode_cu_kernel<UG, 2>), dim3(kNG), dim3(kT), 0, st, a); break;
+        case 32: launch_lo<UG, 0>(a, st); break;
+        case 64: launch_lo<UG, 1>(a, st); break;
+        case 128: launch_lo<UG, 2>(a, st); break;
         default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();

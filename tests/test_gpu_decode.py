@@ -204,10 +204,12 @@ def test_decode_small(name):
     dict(hidden=64, num_experts=4, top_k=1, intermediate=64, group_size=32),
     # hidden 2048 shapes of the one-workgroup-per-CU kernel: 8 act rows per
     # lane (K * I = 16384), two waves per slot (K = 4), E = 256 with gs 32,
-    # E = K (every expert selected)
+    # E = 128 (ranked over 128 slots), E = K (every expert selected)
     dict(hidden=2048, num_experts=32, top_k=8, intermediate=2048, group_size=128),
     dict(hidden=2048, num_experts=16, top_k=4, intermediate=2048, group_size=32),
     dict(hidden=2048, num_experts=256, top_k=8, intermediate=1024, group_size=32),
+    dict(hidden=2048, num_experts=128, top_k=8, intermediate=1024, group_size=64),
+    dict(hidden=2048, num_experts=96, top_k=4, intermediate=2048, group_size=64),
     dict(hidden=2048, num_experts=8, top_k=8, intermediate=1024, group_size=64),
 ])
 def test_decode_ragged_shapes(kw):

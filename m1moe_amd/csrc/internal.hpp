@@ -5,6 +5,13 @@
 
 #include "m1moe_hip.h"
 
+// constructors shared by host code and kernels
+#if defined(__HIPCC__)
+#define M1MOE_HD __host__ __device__
+#else
+#define M1MOE_HD
+#endif
+
 namespace m1moe {
 
 // Geometry of one expert block in the reference's planar layout
@@ -120,10 +127,33 @@ struct RouterArgs {
     uint32_t* counters;          // [T] zero-initialised, self-resetting
 };
 
+// Per-expert scale block of the prefill GEMMs, made on the device at upload
+// (launch_pf_scale_copy): for gate and up (I rows of h/gs groups) and down (h
+// rows of I/gs groups), one u32 per (row, group) = f16(s * 2^(18 - k)) |
+// f16(b * 2^-k) << 16, then one int8 k per row (gate rows, up rows, down
+// rows).  k, the smallest k >= 0 that keeps s * 2^(18 - k) and every
+// dequantised weight (15|s| + |b|) * 2^-k within f16 range, is undone on the
+// row's accumulator (x 2^k, exact).
+struct PfScaleLayout {
+    uint64_t gate, up, down, kg, ku, kd, bytes;
+    M1MOE_HD PfScaleLayout(int h, int I, int gs) {
+        const uint64_t gh = (uint64_t)(h / gs), gi = (uint64_t)(I / gs);
+        gate = 0;
+        up = (uint64_t)I * gh * 4;
+        down = up + (uint64_t)I * gh * 4;
+        kg = down + (uint64_t)h * gi * 4;
+        ku = kg + (uint64_t)I;
+        kd = ku + (uint64_t)I;
+        bytes = (kd + (uint64_t)h + 255) / 256 * 256;
+    }
+};
+
 // Arguments of the prefill kernels (T tokens through one layer).
 struct PrefillArgs {
     const uint8_t* layer_base;   // first expert block of the layer
     uint64_t expert_bytes;
+    const uint8_t* pfs_base;     // the layer's first scale block (PfScaleLayout)
+    uint64_t pfs_bytes;          // bytes per expert of those blocks
     const void* x;               // [T][h] f32 or bf16
     int32_t x_bf16;
     const float* residual;       // [T][h] or null
@@ -169,6 +199,10 @@ uint64_t decode_copy_bytes(int I, int gs);
 int launch_decode_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int I,
                        int gs, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
+// Writes the PfScaleLayout blocks of E experts (layer image at `layer`) to
+// dst; a non-finite scale or bias raises device error flag 8.
+int launch_pf_scale_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E,
+                         int h, int I, int gs, uint32_t* err, void* stream);
 int launch_dequant(const uint8_t* expert_base, const ProjView& p, int32_t gs, float* out,
                    void* stream);
 

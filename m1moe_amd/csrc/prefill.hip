@@ -22,12 +22,14 @@
 // Dequantisation into MFMA operands.  A lane's A fragment is one packed
 // word (8 nibbles = 8 columns of one weight row).  Each nibble is moved to
 // f16 mantissa bits 6..9, which makes it the exact subnormal n * 2^-18; one
-// v_pk_fma_f16 with (s * 2^18, b) then gives f16(n * s + b), a single
-// rounding of the exact value (n * s has at most 12 significant bits and the
-// FMA is fused).  This needs |s| < 0.25 so that s * 2^18 is a finite f16; a
-// larger scale raises the device error flag.  The pairs come out in column
-// order (0,4), (1,5), (2,6), (3,7); the B fragments are stored in LDS in the
-// same permuted order (the sum over k does not depend on the order).
+// v_pk_fma_f16 with (s * 2^(18-k), b * 2^-k) then gives f16((n * s + b) *
+// 2^-k), a single rounding of the exact value (n * s has at most 12
+// significant bits and the FMA is fused).  k is a per-row power of two
+// (0 unless the row has a group scale |s| >= 0.25 or a weight beyond f16
+// range), made at upload with the f16 scale/bias pairs (PfScaleLayout) and
+// undone on the row's f32 accumulator.  The pairs come out in column order
+// (0,4), (1,5), (2,6), (3,7); the B fragments are stored in LDS in the same
+// permuted order (the sum over k does not depend on the order).
 //
 // MFMA v_mfma_f32_16x16x32_f16: A 16x32 (lane l: row l%16, k 8(l/16)..+7),
 // B 32x16 (lane l: column l%16, the same k), D 16x16 (lane l: column l%16,
@@ -188,7 +190,7 @@ struct PfStage {
     static constexpr int W = KB / 32;  // packed words per lane per block
     static constexpr int NB = KB * kTN / (8 * 64 * NW);  // uint4 of the B tile per thread
     uint32_t aw[NMAT][W];
-    uint32_t as[NMAT], ab[NMAT];
+    uint32_t sb[NMAT];                 // f16 s * 2^(18-k) | f16 b * 2^-k << 16
     uint4 b[NB];                       // this thread's share of the B tile
 };
 
@@ -222,18 +224,17 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
 
     // expert sub-blocks (planar [gate W|S|B][up W|S|B][down W|S|B])
     const uint8_t* ex = a.layer_base + (uint64_t)e * a.expert_bytes;
+    const uint8_t* px = a.pfs_base + (uint64_t)e * a.pfs_bytes;
     const Layout L(a.h, a.I, a.gs);
+    const PfScaleLayout PL(a.h, a.I, a.gs);
     const uint32_t* wrow[NMAT];
-    const uint16_t* srow[NMAT];
-    const uint16_t* brow[NMAT];
+    const uint32_t* sbrow[NMAT];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
         const uint64_t wo = NMAT == 2 ? (m == 0 ? L.gate_w : L.up_w) : L.down_w;
-        const uint64_t so = NMAT == 2 ? (m == 0 ? L.gate_s : L.up_s) : L.down_s;
-        const uint64_t bo = NMAT == 2 ? (m == 0 ? L.gate_b : L.up_b) : L.down_b;
+        const uint64_t so = NMAT == 2 ? (m == 0 ? PL.gate : PL.up) : PL.down;
         wrow[m] = reinterpret_cast<const uint32_t*>(ex + wo) + (size_t)row * (K / 8) + kq * W;
-        srow[m] = reinterpret_cast<const uint16_t*>(ex + so) + (size_t)row * groups;
-        brow[m] = reinterpret_cast<const uint16_t*>(ex + bo) + (size_t)row * groups;
+        sbrow[m] = reinterpret_cast<const uint32_t*>(px + so) + (size_t)row * groups;
     }
 
     if (tid < kTN) {
@@ -269,8 +270,7 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
                 const uint2 q = *reinterpret_cast<const uint2*>(pw);
                 st.aw[m][0] = q.x; st.aw[m][W > 1 ? 1 : 0] = q.y;
             }
-            st.as[m] = srow[m][g];
-            st.ab[m] = brow[m][g];
+            st.sb[m] = sbrow[m][g];
         }
     };
     auto store_b = [&](int buf, const PfStage<NMAT, KB, NW>& st) {
@@ -285,17 +285,13 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
 #pragma unroll
         for (int j = 0; j < kTN / 16; ++j) acc[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    bool bad_scale = false;
     auto compute = [&](int buf, const PfStage<NMAT, KB, NW>& st) {
         f16x2 s2[NMAT], b2[NMAT];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
-            const float sf = bf16_to_f32(st.as[m]);
-            bad_scale |= !(fabsf(sf) < 0.25f);
-            const _Float16 s16 = (_Float16)(sf * 262144.0f);  // s * 2^18, exact
-            const _Float16 b16 = (_Float16)bf16_to_f32(st.ab[m]);
-            s2[m] = f16x2{s16, s16};
-            b2[m] = f16x2{b16, b16};
+            const uint32_t lo = st.sb[m] & 0xffffu, hi = st.sb[m] >> 16;
+            s2[m] = __builtin_bit_cast(f16x2, lo | (lo << 16));
+            b2[m] = __builtin_bit_cast(f16x2, hi | (hi << 16));
         }
         // two k-steps at a time: their B fragments are read from LDS and their
         // A fragments unpacked before the 2 * 4 * NMAT MFMAs that use them
@@ -341,10 +337,18 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
         if (kb + 2 < nblk) store_b(0, S0);
         __syncthreads();
     }
-    if (bad_scale) flag_error(a.err, 8u);
-
-    // epilogue: lane holds column (pair) j*16 + r, rows 4*kq..4*kq+3 of the wave's 16
+    // epilogue: lane holds column (pair) j*16 + r, rows 4*kq..4*kq+3 of the wave's 16;
+    // each row's 2^k comes back on its accumulator
     const int row0 = mt * TM + wave * 16 + 4 * kq;
+    float rs[NMAT][4];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+        const uint64_t ko = NMAT == 2 ? (m == 0 ? PL.kg : PL.ku) : PL.kd;
+        const uint32_t k4 = *reinterpret_cast<const uint32_t*>(px + ko + row0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            rs[m][i] = __uint_as_float((uint32_t)(127 + ((k4 >> (8 * i)) & 0xffu)) << 23);
+    }
 #pragma unroll
     for (int j = 0; j < kTN / 16; ++j) {
         const int n = j * 16 + r;
@@ -354,7 +358,8 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
             _Float16 o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float g = acc[0][j][i] * inv, u = acc[NMAT - 1][j][i] * inv;
+                const float g = acc[0][j][i] * rs[0][i] * inv;
+                const float u = acc[NMAT - 1][j][i] * rs[NMAT - 1][i] * inv;
                 float v = (g / (1.0f + expf(-g))) * u;  // Shaders.metal:148
                 v = fminf(fmaxf(v, -65504.f), 65504.f);
                 o[i] = (_Float16)v;
@@ -362,8 +367,57 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
             *reinterpret_cast<uint2*>(a.act + (size_t)(p0 + n) * a.I + row0) =
                 __builtin_bit_cast(uint2, o);
         } else {
-            *reinterpret_cast<f32x4*>(a.y + (size_t)(p0 + n) * a.h + row0) = acc[0][j];
+            const f32x4 y = acc[0][j];
+            *reinterpret_cast<f32x4*>(a.y + (size_t)(p0 + n) * a.h + row0) =
+                f32x4{y[0] * rs[0][0], y[1] * rs[0][1], y[2] * rs[0][2], y[3] * rs[0][3]};
         }
+    }
+}
+
+// ---- the scale blocks of the prefill GEMMs (PfScaleLayout), made at upload -----------
+
+// One thread per (expert, weight row): the row's power of two k and its
+// groups' f16 (s * 2^(18-k), b * 2^-k) pairs.
+__global__ __launch_bounds__(256) void pf_scale_copy_kernel(const uint8_t* src, uint64_t src_bytes,
+                                                            uint8_t* dst, uint64_t dst_bytes, int E,
+                                                            int h, int I, int gs, uint32_t* err) {
+    const int rows = 2 * I + h;
+    const uint64_t gid = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (uint64_t)E * rows) return;
+    const int e = (int)(gid / rows), ri = (int)(gid - (uint64_t)e * rows);
+    const int m = ri < I ? 0 : (ri < 2 * I ? 1 : 2);
+    const int row = m == 2 ? ri - 2 * I : ri - m * I;
+    const int groups = (m == 2 ? I : h) / gs;
+    const Layout L(h, I, gs);
+    const PfScaleLayout P(h, I, gs);
+    const uint8_t* b = src + (uint64_t)e * src_bytes;
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(
+        b + (m == 0 ? L.gate_s : (m == 1 ? L.up_s : L.down_s))) + (size_t)row * groups;
+    const uint16_t* bp = reinterpret_cast<const uint16_t*>(
+        b + (m == 0 ? L.gate_b : (m == 1 ? L.up_b : L.down_b))) + (size_t)row * groups;
+    float ms = 0.f, mw = 0.f;
+    bool finite = true;
+    for (int g = 0; g < groups; ++g) {
+        const float sf = bf16_to_f32(sp[g]), bf = bf16_to_f32(bp[g]);
+        finite = finite && isfinite(sf) && isfinite(bf);
+        ms = fmaxf(ms, fabsf(sf));
+        mw = fmaxf(mw, 15.f * fabsf(sf) + fabsf(bf));
+    }
+    int k = 0;
+    if (!finite) {
+        flag_error(err, 8u);
+    } else {
+        while (k < 100 && (ldexpf(ms, 18 - k) > 65504.f || ldexpf(mw, -k) > 65504.f)) ++k;
+    }
+    uint8_t* d = dst + (uint64_t)e * dst_bytes;
+    d[(m == 0 ? P.kg : (m == 1 ? P.ku : P.kd)) + row] = (uint8_t)k;
+    uint32_t* o = reinterpret_cast<uint32_t*>(d + (m == 0 ? P.gate : (m == 1 ? P.up : P.down))) +
+                  (size_t)row * groups;
+    for (int g = 0; g < groups; ++g) {
+        const _Float16 s16 = (_Float16)ldexpf(bf16_to_f32(sp[g]), 18 - k);
+        const _Float16 b16 = (_Float16)ldexpf(bf16_to_f32(bp[g]), -k);
+        o[g] = (uint32_t)__builtin_bit_cast(uint16_t, s16) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, b16) << 16);
     }
 }
 
@@ -437,6 +491,16 @@ int launch_gemms(const PrefillArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+
+int launch_pf_scale_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E,
+                         int h, int I, int gs, uint32_t* err, void* stream) {
+    const PfScaleLayout P(h, I, gs);
+    const uint64_t threads = (uint64_t)E * (uint64_t)(2 * I + h);
+    hipLaunchKernelGGL(pf_scale_copy_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), layer, expert_bytes, dst, P.bytes, E,
+                       h, I, gs, err);
+    return (int)hipGetLastError();
+}
 
 int launch_prefill(const PrefillArgs& a, void* stream) {
     if (a.E > kMaxE || a.h > 16384 || a.h % 64 || a.I % 64) return (int)hipErrorInvalidValue;

@@ -162,25 +162,67 @@ def test_prefill_agrees_with_decode(cfg3):
     assert rel_l2(got, dec) <= REL_L2_TOL
 
 
-def test_prefill_rejects_scales_outside_f16_range():
+def _set_groups(img, base, row, groups, first, count, bf16_bits):
+    """bf16 words [first, first + count) of row `row` of the [rows][groups]
+    scale or bias array at byte offset `base` of a layer image."""
+    v = img[base:].view(np.uint16)
+    v[row * groups + first:row * groups + first + count] = bf16_bits
+
+
+def _scale_pow2(img, base, count, p):
+    """Multiplies `count` bf16 scales at byte offset `base` by 2^p (exponent
+    field + p; the synthetic scales are normal and nonzero)."""
+    v = img[base:base + 2 * count].view(np.uint16)
+    v[:] = (v.astype(np.int32) + (p << 7)).astype(np.uint16)
+
+
+def test_prefill_takes_large_scales():
+    """Group scales |s| >= 0.25 (s * 2^18 alone would overflow f16) go through
+    the per-row power of two: whole matrices scaled by 2^6 .. 2^12 (down of
+    experts 0 and 4, gate of 1 and 5, up of 2 and 6) and single rows set to
+    s = 0.5 and 8 (gate of 3 and 7), against the oracle at the usual bar."""
     c = make_case("tiny", seed=8)
     try:
         s = c.shape
         eb = c.ctx.expert_bytes
+        offs = m.expert_offsets(s)  # gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b
+        gh = s.hidden // s.group_size
+        n_gu, n_d = s.intermediate * gh, s.hidden * (s.intermediate // s.group_size)
+        img = c.images[0].copy()
+        for e in range(s.num_experts):
+            o = e * eb
+            if e % 4 == 0:
+                _scale_pow2(img, o + offs[7], n_d, 12)      # down s ~ 0.02 * 4096
+            elif e % 4 == 1:
+                _scale_pow2(img, o + offs[1], n_gu, 6)      # gate s ~ 0.02 * 64
+            elif e % 4 == 2:
+                _scale_pow2(img, o + offs[4], n_gu, 8)      # up s ~ 0.02 * 256
+            else:
+                _set_groups(img, o + offs[1], 0, gh, 0, gh, 0x3F00)   # gate row 0: s = 0.5
+                _set_groups(img, o + offs[1], 1, gh, 0, 1, 0x4100)    # gate row 1, group 0: s = 8
+        c.ctx.upload_layer_experts(0, img)
+        c.images[0] = img
+        c.ctx.sync()
+        T = 64
+        say("prefill with group scales up to ~100")
+        got, gidx, gw, x32, res = _run_prefill(c, T, stream=12)
+        assert np.all(np.isfinite(got))
+        _check(c, T, got, gidx, gw, x32, res)
+    finally:
+        c.close()
+
+
+def test_prefill_reports_a_non_finite_scale():
+    c = make_case("tiny", seed=9)
+    try:
+        s = c.shape
         offs = m.expert_offsets(s)
         img = c.images[0].copy()
-        groups = s.hidden // s.group_size
-        for e in range(s.num_experts):  # every expert's gate scales of row 0 -> 0.5
-            base = e * eb + offs[1]
-            img[base:base + 2 * groups].view(np.uint16)[:] = 0x3F00
+        _set_groups(img, 3 * c.ctx.expert_bytes + offs[1], 7, s.hidden // s.group_size, 1, 1,
+                    0x7F80)  # +inf
+        say("upload with an infinite gate scale (expect a device error)")
         c.ctx.upload_layer_experts(0, img)
-        blk = MoEBlock(c.ctx)
-        T = 4
-        dx = c.ctx.to_device(c.x_bf16(T))
-        dout = c.ctx.alloc(T * s.hidden * 4)
-        say("prefill with scale 0.5 (expect a device error)")
-        blk.prefill(0, T, dx, "bf16", None, dout)
-        with pytest.raises(m.M1MoEError, match="scale"):
+        with pytest.raises(m.M1MoEError, match="non-finite"):
             c.ctx.sync()
         c.ctx.sync()  # the flag was cleared
     finally:

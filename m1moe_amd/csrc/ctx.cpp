@@ -114,7 +114,8 @@ int32_t refresh_decode_copy(m1moe_ctx_t ctx, int32_t layer) {
     const uint64_t lb = (uint64_t)ctx->g.E * ctx->g.expert_bytes;
     HIP_TRY((hipError_t)m1moe::launch_decode_copy(
         ctx->arena + (uint64_t)layer * lb, ctx->g.expert_bytes,
-        ctx->dec + (uint64_t)layer * ctx->g.E * ctx->dec_bytes, ctx->g.E, ctx->g.I, ctx->g.gs,
+        ctx->dec + (uint64_t)layer * ctx->g.E * ctx->dec_bytes, ctx->g.E, ctx->g.h, ctx->g.I,
+        ctx->g.gs,
         ctx->stream));
     ctx->dec_stale[layer] = false;
     return M1MOE_OK;
@@ -446,8 +447,9 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         c->sync_cu_cnt = c->sync_cu_seen + (uint64_t)m1moe::kCuWorkgroups * 4;
         c->sync_cu_part =
             c->sync_cu_cnt + (uint64_t)m1moe::kCuRep * m1moe::kCuParts * m1moe::kCntStride * 4;
-        c->sync_bytes = c->sync_cu_part +
-            (uint64_t)m1moe::kCuWorkgroups * m1moe::kCuWorkgroups * 8 * 4;
+        // per-CU kernels: [256 row blocks][256 sources][8 or 16 rows] f32 partials
+        c->sync_bytes = c->sync_cu_part + (uint64_t)m1moe::kCuWorkgroups *
+                                              m1moe::kCuWorkgroups * (g.h > 2048 ? 16 : 8) * 4;
     }
     {
         int cus = 0;
@@ -457,7 +459,7 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
                        m1moe::decode_cu_fits(g.h, g.E, g.K, g.I, g.gs);
         c->dec_stale.assign(s->num_layers, false);
         if (c->decode_cu) {
-            c->dec_bytes = m1moe::decode_copy_bytes(g.I, g.gs);
+            c->dec_bytes = m1moe::decode_copy_bytes(g.h, g.I, g.gs);
             if ((rc = device_alloc((void**)&c->dec, L * E * c->dec_bytes, "repacked expert copy")))
                 return cleanup(rc);
         }
@@ -503,7 +505,8 @@ int32_t m1moe_upload_layer_experts(m1moe_ctx_t ctx, int32_t layer, const void* h
     if (ctx->decode_cu) {
         HIP_TRY((hipError_t)m1moe::launch_decode_copy(
             ctx->arena + (uint64_t)layer * want, ctx->g.expert_bytes,
-            ctx->dec + (uint64_t)layer * ctx->g.E * ctx->dec_bytes, ctx->g.E, ctx->g.I, ctx->g.gs,
+            ctx->dec + (uint64_t)layer * ctx->g.E * ctx->dec_bytes, ctx->g.E, ctx->g.h, ctx->g.I,
+            ctx->g.gs,
             ctx->stream));
         ctx->dec_stale[layer] = false;
     }

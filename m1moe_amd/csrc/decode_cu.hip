@@ -91,8 +91,8 @@ struct CuLDS {
 // equal one at a lower index), counted by P = 2^LP lanes over M = 2^LEP / P
 // experts each (the 512 threads cover the 2^LEP experts exactly); the
 // segment's last lane writes s.idx[rank] = i for the K first ranks.
-template <int LEP>
-__device__ __forceinline__ void rank_cu(int t, int E, int K, CuLDS& s) {
+template <int LEP, class S>
+__device__ __forceinline__ void rank_cu(int t, int E, int K, S& s) {
     constexpr int LP = LEP == 6 ? 3 : (LEP == 7 ? 2 : 1);
     constexpr int P = 1 << LP, M = 1 << (LEP - LP);
     static_assert((1 << LEP) * P == kT, "one thread per (expert, part)");
@@ -117,8 +117,9 @@ __device__ __forceinline__ void rank_cu(int t, int E, int K, CuLDS& s) {
 // index), counted by P lanes over ep / P experts each (ep = E rounded up to
 // a power of two, padding at -inf).  Ends with a barrier; s.idx and s.ok are
 // valid after it (and s.w for a given routing).
+template <class S>
 __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, uint32_t tag,
-                         CuLDS& s) {
+                         S& s) {
     const int E = a.E, K = a.K;
     if (a.given_idx) {
         if (t < K) {
@@ -190,7 +191,8 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
 // 501-506), renormalised over the selection in slot order when
 // norm_topk_prob is set (:514-517), into s.w.  One wave; a given routing
 // keeps the supplied weights.
-__device__ void weights_cu(const FusedArgs& a, int lane, CuLDS& s) {
+template <class S>
+__device__ void weights_cu(const FusedArgs& a, int lane, S& s) {
     if (a.given_idx) return;
     const int E = a.E, K = a.K;
     float v[4], mx = -INFINITY;
@@ -230,19 +232,22 @@ struct DecLayout {
     }
 };
 
-// One thread per 16 bytes of the repacked block, all experts of a layer.
+// One thread per 16 bytes of the repacked block, all experts of a layer
+// (H = hidden width: 2048, or 4096 for moe_decode_cuw_kernel).
+template <int H>
 __global__ __launch_bounds__(256) void decode_copy_kernel(const uint8_t* src, uint64_t src_bytes,
                                                           uint8_t* dst, uint64_t dst_bytes,
                                                           int E, int I, int gs) {
-    const Layout L(kH, I, gs);
-    const DecLayout D(kH, I, gs);
+    constexpr int RPT = H / 512;  // down rows per thread: t + 512 r, r < RPT
+    const Layout L(H, I, gs);
+    const DecLayout D(H, I, gs);
     const uint64_t n16 = D.bytes / 16;
     const uint64_t gi = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (gi >= n16 * (uint64_t)E) return;
     const uint64_t e = gi / n16, o = (gi - e * n16) * 16;
     const uint8_t* b = src + e * src_bytes;
     uint8_t* d = dst + e * dst_bytes;
-    const int groups_h = kH / gs, groups_i = I / gs;
+    const int groups_h = H / gs, groups_i = I / gs;
     auto bf = [&](uint64_t off, uint64_t elem) {
         return (uint32_t)reinterpret_cast<const uint16_t*>(b + off)[elem];
     };
@@ -262,14 +267,16 @@ __global__ __launch_bounds__(256) void decode_copy_kernel(const uint8_t* src, ui
         v = make_uint4(w[0], w[1], w[2], w[3]);
     } else if (o < D.dsb) {
         const uint64_t k16 = (o - D.dw) / 16;      // (chunk, row)
-        const uint64_t row = k16 % kH, c = k16 / kH;
+        const uint64_t row = k16 % H, c = k16 / H;
         v = *reinterpret_cast<const uint4*>(b + L.down_w + row * (uint64_t)(I / 2) + c * 16);
-    } else if (o < D.dsb + (uint64_t)groups_i * kH * 4) {
-        const uint64_t k16 = (o - D.dsb) / 16;     // (group, t): rows t + 512 r, r = 0..3
-        const uint64_t t = k16 % (kH / 4), grp = k16 / (kH / 4);
+    } else if (o < D.dsb + (uint64_t)groups_i * H * 4) {
+        // (group, t, quarter): rows t + 512 r, r = 4 quarter .. 4 quarter + 3
+        const uint64_t k16 = (o - D.dsb) / 16;
+        const uint64_t qt = k16 % (RPT / 4), t = (k16 / (RPT / 4)) % 512;
+        const uint64_t grp = k16 / (RPT / 4) / 512;
         uint32_t w[4];
         for (int k = 0; k < 4; ++k) {
-            const uint64_t el = (t + (uint64_t)(kH / 4) * k) * groups_i + grp;
+            const uint64_t el = (t + (uint64_t)512 * (4 * qt + k)) * groups_i + grp;
             w[k] = bf(L.down_s, el) | (bf(L.down_b, el) << 16);
         }
         v = make_uint4(w[0], w[1], w[2], w[3]);
@@ -816,30 +823,461 @@ int launch_ug(const FusedArgs& a, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
+// ---- hidden 4096 (Mixtral): moe_decode_cuw_kernel ------------------------------------
+//
+// The same one-launch, one-workgroup-per-CU scheme for hidden width 4096 and
+// top-K <= 2: working workgroup g < K * I / 128 owns 128 consecutive act rows
+// of one slot (4 chunks of 32; wave w: rows 16 w .. 16 w + 15), streams their
+// gate/up rows in batches of 4 rows x one 32-column chunk per lane (two
+// batches in flight), then its down columns chunk by chunk (rows t + 512 r, r
+// < 8, per thread), and stores 4096 partial sums.  Every workgroup (working
+// or not) then reduces output rows 16 g .. 16 g + 15 over the working
+// workgroups of each slot, in a fixed order, and combines the slots.
+
+constexpr int kHW = 4096;
+constexpr int kRowsW = kHW / kNG;   // output rows per workgroup in the reduce
+constexpr int kRPT = kHW / kT;      // down rows per thread
+constexpr int kWRows = 128;         // act rows per working workgroup
+constexpr int kWChunks = kWRows / 32;
+constexpr int kMaxKW = 2;
+
+struct CuwLDS {
+    alignas(16) float x[128 * 36];      // staged input, chunk c at 36 c
+    alignas(16) float v[kMaxE];         // logits
+    alignas(16) uint32_t xq[128][36];   // prepared gate/up input chunks (hi, lo, sum, 2^-e)
+    alignas(16) uint32_t xp[kWChunks][36];  // this workgroup's prepared act chunks
+    double lp[kW];
+    float act[kWRows];
+    float y[kMaxKW][kRowsW];
+    int idx[kMaxK];
+    float w[kMaxK];
+    float rms;
+    uint32_t tag;
+    int ok;
+};
+
+// One batch: 4 act rows x one 32-column chunk per lane, gate and up, and the
+// (4-row, group) scale/bias quad of that chunk.
+struct GUBatchW {
+    uint4 gw[4], uw[4];
+    uint4 sb[2];
+};
+
+template <int GSL>
+__device__ __forceinline__ void guw_load(const FusedArgs& a, const Layout& L, int e, int row0,
+                                         int c, GUBatchW& b) {
+    const bool real = e >= 0;
+    const uint64_t eu = real ? (uint64_t)__builtin_amdgcn_readfirstlane(e) : 0;
+    const uint8_t* blk = a.layer_base + eu * a.expert_bytes;
+    const uint8_t* sb_b = a.dec_base + eu * a.dec_bytes;
+    constexpr uint32_t groups = kHW >> (5 + GSL);
+    const uint32_t so = ((uint32_t)(row0 / 4) * groups + ((uint32_t)c >> GSL)) * 32u;
+    b.sb[0] = ld_stream(sb_b + so);
+    b.sb[1] = ld_stream(sb_b + so + 16);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t wo = (uint32_t)(row0 + u) * (kHW / 2) + (uint32_t)c * 16u;
+        b.gw[u] = ld_stream(blk + L.gate_w + wo);
+        b.uw[u] = ld_stream(blk + L.up_w + wo);
+    }
+}
+
+// The down columns of one chunk for rows t + 512 r: nibble words and the
+// (scale | bias) words of the chunk's group.
+struct DNChunkW {
+    uint4 w[kRPT];
+    uint4 sb[kRPT / 4];
+};
+
+template <int GSL>
+__device__ __forceinline__ void dnw_load(const FusedArgs& a, int e, int cg, int t, DNChunkW& d) {
+    const bool real = e >= 0;
+    const uint64_t eu = real ? (uint64_t)__builtin_amdgcn_readfirstlane(e) : 0;
+    const DecLayout D(kHW, a.I, a.gs);
+    const uint8_t* blk = a.dec_base + eu * a.dec_bytes;
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r)
+        d.w[r] = ld_stream(blk + D.dw + ((uint64_t)cg * kHW + t + 512 * r) * 16);
+    const uint64_t so = D.dsb + (((uint64_t)(cg >> GSL) * 512 + t) * (kRPT / 4)) * 16;
+#pragma unroll
+    for (int q = 0; q < kRPT / 4; ++q) d.sb[q] = ld_stream(blk + so + 16 * q);
+}
+
+// acc[r] += the chunk's contribution to row t + 512 r (act chunk prepared in xp).
+__device__ __forceinline__ void dnw_compute(const DNChunkW& d, const uint32_t* xp, float (&acc)[kRPT]) {
+    const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+    const uint32_t mhi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
+    uint32_t p[kChunkWords];
+#pragma unroll
+    for (int k = 0; k < kChunkWords; k += 2) {
+        const uint2 q = *reinterpret_cast<const uint2*>(&xp[k]);
+        p[k] = q.x;
+        p[k + 1] = q.y;
+    }
+    const float xs = __uint_as_float(p[32]), inv = __uint_as_float(p[33]);
+    const float sc = inv * 16777216.f;
+    const uint32_t sbw[kRPT] = {d.sb[0].x, d.sb[0].y, d.sb[0].z, d.sb[0].w,
+                                d.sb[1].x, d.sb[1].y, d.sb[1].z, d.sb[1].w};
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r) {
+        const uint32_t ws[4] = {d.w[r].x, d.w[r].y, d.w[r].z, d.w[r].w};
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // word q: pairs 4q .. 4q + 3 (hi at 2k, lo at 2k + 1)
+            const uint32_t v = ws[q], v8 = v >> 8;
+            const uint32_t n[4] = {v & mlo, v & mhi, v8 & mlo, v8 & mhi};
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+                const int k = 4 * q + j;
+                const half2_t n0 = __builtin_bit_cast(half2_t, n[j]);
+                const half2_t n1 = __builtin_bit_cast(half2_t, n[j + 1]);
+                a0 = __builtin_amdgcn_fdot2(n0, __builtin_bit_cast(half2_t, p[2 * k]), a0, false);
+                a1 = __builtin_amdgcn_fdot2(n1, __builtin_bit_cast(half2_t, p[2 * k + 2]), a1, false);
+                a2 = __builtin_amdgcn_fdot2(n0, __builtin_bit_cast(half2_t, p[2 * k + 1]), a2, false);
+                a3 = __builtin_amdgcn_fdot2(n1, __builtin_bit_cast(half2_t, p[2 * k + 3]), a3, false);
+            }
+        }
+        const float dsum = (a0 + a1) + (a2 + a3);
+        acc[r] += fmaf(bf16_pick(sbw[r], kSelLo) * sc, dsum, bf16_pick(sbw[r], kSelHi) * xs * inv);
+    }
+}
+
+template <int GSL, bool LO>
+__global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
+    __shared__ CuwLDS s;
+    const int g = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int E = a.E, K = a.K, I = a.I;
+    const int wps = I / kWRows;               // working workgroups per slot
+    const int nwork = K * wps;
+    const bool producer = !a.given_idx && g < E;
+
+    // ---- input, launch number, router row --------------------------------------------
+    if (t == 0) s.tag = ld_u32(a.cu_seen + g) + 1u;
+    float res = 0.f;
+    if (t < kRowsW && a.residual) res = a.residual[g * kRowsW + t];
+    const bool normed = !a.x_bf16 && a.x_norm_w;
+    float xv[8];
+    uint4 nw = make_uint4(0u, 0u, 0u, 0u);
+    if (a.x_bf16) {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + 8 * t);
+        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xv[2 * i] = __uint_as_float(qq[i] << 16);
+            xv[2 * i + 1] = __uint_as_float(qq[i] & 0xffff0000u);
+        }
+    } else {
+        const float4 q0 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + 8 * t);
+        const float4 q1 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + 8 * t + 4);
+        xv[0] = q0.x; xv[1] = q0.y; xv[2] = q0.z; xv[3] = q0.w;
+        xv[4] = q1.x; xv[5] = q1.y; xv[6] = q1.z; xv[7] = q1.w;
+        if (normed) nw = *reinterpret_cast<const uint4*>(a.x_norm_w + 8 * t);
+    }
+    uint4 rw = make_uint4(0u, 0u, 0u, 0u);
+    if (producer) rw = *reinterpret_cast<const uint4*>(a.router + (size_t)g * kHW + 8 * t);
+    if (normed && wave == 0) {
+        const float r = input_rms(a, lane);
+        if (lane == 0) s.rms = r;
+    }
+    __syncthreads();
+    if (normed) {  // the norm of Shaders.metal:121-134
+        const float rms = s.rms;
+        const uint32_t ww[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xv[2 * i] = xv[2 * i] * rms * __uint_as_float(ww[i] << 16);
+            xv[2 * i + 1] = xv[2 * i + 1] * rms * __uint_as_float(ww[i] & 0xffff0000u);
+        }
+    }
+    {
+        float* dx = &s.x[(t >> 2) * 36 + (t & 3) * 8];
+        *reinterpret_cast<float4*>(dx) = float4{xv[0], xv[1], xv[2], xv[3]};
+        *reinterpret_cast<float4*>(dx + 4) = float4{xv[4], xv[5], xv[6], xv[7]};
+    }
+    if (producer) {  // InferenceEngine.swift:490-500, exact products summed in f64
+        const uint32_t rr[4] = {rw.x, rw.y, rw.z, rw.w};
+        double acc = 0.0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc += (double)__uint_as_float(rr[i] << 16) * (double)xv[2 * i];
+            acc += (double)__uint_as_float(rr[i] & 0xffff0000u) * (double)xv[2 * i + 1];
+        }
+        acc = wave_sum_f64_last(acc);
+        if (lane == 63) s.lp[wave] = acc;
+    }
+    __syncthreads();
+    const uint32_t tag = s.tag, parity = tag & 1u;
+    if (producer && t < kLogitRep) {
+        double sum = s.lp[0];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) sum += s.lp[w];
+        float l = (float)sum;
+        if (a.bias) l = l + a.bias[g];
+        st_u64(a.slots + (size_t)t * kRepStride + g,
+               ((unsigned long long)tag << 32) | __float_as_uint(l));
+    }
+    // the gate/up input chunks (lane l of every wave uses chunks l and l + 64),
+    // prepared once per workgroup by waves 1 and 2 while wave 0 awaits the logits
+    if (wave == 1 || wave == 2) {
+        const int c = lane + 64 * (wave - 1);
+        float v[1][32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 q = *reinterpret_cast<const float4*>(&s.x[c * 36 + 4 * i]);
+            v[0][4 * i + 0] = q.x;
+            v[0][4 * i + 1] = q.y;
+            v[0][4 * i + 2] = q.z;
+            v[0][4 * i + 3] = q.w;
+        }
+        XChunk2 c1[1];
+        const float vinv = lane_scale_prep<1>(v, c1);
+        uint32_t* d = s.xq[c];
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+            d[p] = __builtin_bit_cast(uint32_t, c1[0].X[p]);
+            d[16 + p] = __builtin_bit_cast(uint32_t, c1[0].L[p]);
+        }
+        d[32] = __float_as_uint(c1[0].xs);
+        d[33] = __float_as_uint(vinv);
+    }
+
+    route_cu(a, g, t, wave, lane, tag, s);
+    const bool ok_run = s.ok != 0;
+
+    // ---- working workgroups: gate/up of 128 act rows, then their down columns ------
+    const bool working = g < nwork;
+    const int kg = working ? g / wps : 0;
+    const int eg = (working && ok_run) ? s.idx[kg] : -1;
+    const int r0 = working ? (g - kg * wps) * kWRows : 0;
+    const Layout L(kHW, I, a.gs);
+    float pr[kRPT];
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r) pr[r] = 0.f;
+    if (eg >= 0) {
+        // batch b: row quad b / 2 of this wave's 16 rows, chunk half b % 2 (lane
+        // l: chunk l, then chunk l + 64); two batches in flight
+        const int wrow = r0 + 16 * wave;
+        GUBatchW B0, B1;
+        guw_load<GSL>(a, L, eg, wrow, lane, B0);
+        guw_load<GSL>(a, L, eg, wrow, lane + 64, B1);
+        const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+        const uint32_t mhi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
+        float pg[4], pu[4];
+#pragma unroll
+        for (int bi = 0; bi < 8; ++bi) {
+            const int q = bi >> 1, ch = bi & 1;
+            GUBatchW& B = ch ? B1 : B0;
+            const uint32_t* d = s.xq[lane + 64 * ch];
+            XChunk2 xc;
+#pragma unroll
+            for (int p = 0; p < 16; p += 4) {
+                const uint4 qh = *reinterpret_cast<const uint4*>(d + p);
+                xc.X[p] = __builtin_bit_cast(half2_t, qh.x);
+                xc.X[p + 1] = __builtin_bit_cast(half2_t, qh.y);
+                xc.X[p + 2] = __builtin_bit_cast(half2_t, qh.z);
+                xc.X[p + 3] = __builtin_bit_cast(half2_t, qh.w);
+                if (LO) {
+                    const uint4 ql = *reinterpret_cast<const uint4*>(d + 16 + p);
+                    xc.L[p] = __builtin_bit_cast(half2_t, ql.x);
+                    xc.L[p + 1] = __builtin_bit_cast(half2_t, ql.y);
+                    xc.L[p + 2] = __builtin_bit_cast(half2_t, ql.z);
+                    xc.L[p + 3] = __builtin_bit_cast(half2_t, ql.w);
+                }
+            }
+            const uint2 m2 = *reinterpret_cast<const uint2*>(d + 32);
+            xc.xs = __uint_as_float(m2.x);
+            xc.off = 0.f;
+            const float inv = __uint_as_float(m2.y);
+            const float sc = inv * 16777216.f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t gsb = word_of(B.sb, 2 * u), usb = word_of(B.sb, 2 * u + 1);
+                const float dg = nib_dot32_sub<LO>(B.gw[u], xc, mlo, mhi);
+                const float du = nib_dot32_sub<LO>(B.uw[u], xc, mlo, mhi);
+                const float tg = fmaf(bf16_pick(gsb, kSelLo) * sc, dg, bf16_pick(gsb, kSelHi) * xc.xs * inv);
+                const float tu = fmaf(bf16_pick(usb, kSelLo) * sc, du, bf16_pick(usb, kSelHi) * xc.xs * inv);
+                pg[u] = ch ? pg[u] + tg : tg;
+                pu[u] = ch ? pu[u] + tu : tu;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (bi + 2 < 8) guw_load<GSL>(a, L, eg, wrow + 4 * ((bi + 2) >> 1), lane + 64 * ch, B);
+            if (ch) {
+                const float v8[8] = {pg[0], pu[0], pg[1], pu[1], pg[2], pu[2], pg[3], pu[3]};
+                float gg, uu;
+                reduce8_wave(v8, lane, gg, uu);
+                if (lane < 4)
+                    s.act[16 * wave + 4 * q + ((lane >> 1) & 1) + 2 * (lane & 1)] = silu_fast(gg) * uu;
+            }
+        }
+    }
+    // the down columns of the first two chunks are requested before the act
+    // rows are complete
+    DNChunkW D0, D1;
+    const int cg0 = r0 / 32;
+    if (eg >= 0) {
+        dnw_load<GSL>(a, eg, cg0, t, D0);
+        dnw_load<GSL>(a, eg, cg0 + 1, t, D1);
+    }
+    __syncthreads();
+    if (eg >= 0 && wave < kWChunks / 2) {
+        // act chunks 2 w and 2 w + 1 (lanes 0-31, 32-63)
+        const int h = lane >> 5, i = lane & 31, c = 2 * wave + h;
+        const float x = s.act[32 * c + i];
+        const float mx = half_max(fabsf(x));
+        float scale, inv;
+        pow2_scale(mx, scale, inv);
+        _Float16 hi, lo;
+        split_f16(x * scale * ((i & 1) ? 0.0625f : 1.f), hi, lo);
+        const uint32_t hb = __builtin_bit_cast(uint16_t, hi), lb = __builtin_bit_cast(uint16_t, lo);
+        const uint32_t hb4 = dpp_u32<0x104>(0u, hb), lb4 = dpp_u32<0x104>(0u, lb);
+        const float vs = ((float)hi + (float)lo) * ((i & 1) ? 16.f : 1.f);
+        const float xs = seg_sum_c<32>(vs);
+        if ((i & 7) < 4) {
+            const int p = 4 * (i >> 3) + (i & 7);
+            s.xp[c][2 * p] = hb | (hb4 << 16);
+            s.xp[c][2 * p + 1] = lb | (lb4 << 16);
+        }
+        if (i == 31) {
+            s.xp[c][32] = __float_as_uint(xs);
+            s.xp[c][33] = __float_as_uint(inv);
+        }
+    }
+    __syncthreads();
+    if (eg >= 0) {
+        dnw_compute(D0, s.xp[0], pr);
+        dnw_load<GSL>(a, eg, cg0 + 2, t, D0);
+        dnw_compute(D1, s.xp[1], pr);
+        dnw_load<GSL>(a, eg, cg0 + 3, t, D1);
+        dnw_compute(D0, s.xp[2], pr);
+        dnw_compute(D1, s.xp[3], pr);
+    }
+    if (working) {
+        // row t + 512 r -> block (t + 512 r) / 16, position t % 16, at this workgroup's place
+#pragma unroll
+        for (int r = 0; r < kRPT; ++r)
+            st_u32(a.cu_part + ((size_t)((t + 512 * r) >> 4) * kNG + g) * kRowsW + (t & 15),
+                   tagged(pr[r], parity));
+    }
+    if (wave == kW - 1) {
+        weights_cu(a, lane, s);
+        if (g == 0 && ok_run && lane < K) {
+            if (a.user_idx) a.user_idx[lane] = s.idx[lane];
+            if (a.user_w) a.user_w[lane] = s.w[lane];
+        }
+    }
+
+    // ---- reduce rows 16 g .. 16 g + 15: thread t < nwork reads source t's 16 ---------
+    // partials (re-reading the stale ones), then per slot and row 16 lanes each
+    // add every 16th source of the slot, and the 16 lanes are summed
+    uint4 q4[4];
+    if (t < nwork) {
+        const uint32_t* p = a.cu_part + ((size_t)g * kNG + t) * kRowsW;
+        bool cur[4] = {false, false, false, false};
+        for (int it = 0;; ++it) {
+            bool all = true;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (!cur[j]) {
+                    q4[j] = ld_coherent16(p + 4 * j);
+                    const uint4 q = q4[j];
+                    cur[j] = ((q.x & q.y & q.z & q.w & 1u) == parity) &&
+                             (((q.x | q.y | q.z | q.w) & 1u) == parity);
+                }
+                all = all && cur[j];
+            }
+            if (all) break;
+            if (it >= a.spin_limit) {
+                flag_error(a.err, 4u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    // stage the sources in LDS (x is no longer used): src[t][16]
+    float* stage = s.x;
+    if (t < nwork) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint4 q = q4[j];
+            *reinterpret_cast<float4*>(&stage[t * 16 + 4 * j]) =
+                float4{__uint_as_float(q.x & ~1u), __uint_as_float(q.y & ~1u),
+                       __uint_as_float(q.z & ~1u), __uint_as_float(q.w & ~1u)};
+        }
+    }
+    __syncthreads();
+    {
+        const int j = t & 15, row = (t >> 4) & 15, k = t >> 8;
+        float sum = 0.f;
+        if (k < K)
+            for (int src = k * wps + j; src < (k + 1) * wps; src += 16) sum += stage[src * 16 + row];
+        sum = seg_sum_c<16>(sum);  // total in lane j = 15
+        if (k < K && j == 15) s.y[k][row] = sum;
+    }
+    __syncthreads();
+
+    // ---- combine in slot order with the residual (Shaders.metal:360-376) -------------
+    if (t < kRowsW) {
+        float acc = res;
+        if (ok_run) {
+#pragma unroll
+            for (int k = 0; k < kMaxKW; ++k)
+                if (k < K && s.idx[k] >= 0) acc = fmaf(s.w[k], s.y[k][t], acc);
+        }
+        a.out[g * kRowsW + t] = acc;
+    }
+    if (t == 0) st_u32(a.cu_seen + g, tag);
+}
+
+template <int GSL>
+void launch_w(const FusedArgs& a, hipStream_t st) {
+    if (a.x_bf16)
+        hipLaunchKernelGGL((moe_decode_cuw_kernel<GSL, false>), dim3(kNG), dim3(kT), 0, st, a);
+    else
+        hipLaunchKernelGGL((moe_decode_cuw_kernel<GSL, true>), dim3(kNG), dim3(kT), 0, st, a);
+}
+
 }  // namespace
 
 bool decode_cu_fits(int h, int E, int K, int I, int gs) {
-    if (h != kH || E > kMaxE || K > kMaxK || (kMaxK % K) != 0) return false;
-    if (gs != 32 && gs != 64 && gs != 128) return false;
-    if (I != 1024 && I != 2048) return false;
-    const int ug = K * I / 2048;
-    return ug == 4 || ug == 8;
+    if (E > kMaxE || K < 1 || gs != 32 && gs != 64 && gs != 128) return false;
+    if (h == kH) {  // moe_decode_cu_kernel
+        if (K > kMaxK || (kMaxK % K) != 0 || (I != 1024 && I != 2048)) return false;
+        const int ug = K * I / 2048;
+        return ug == 4 || ug == 8;
+    }
+    if (h == kHW)  // moe_decode_cuw_kernel
+        return K <= kMaxKW && I % kWRows == 0 && K * (I / kWRows) <= kNG;
+    return false;
 }
 
-uint64_t decode_copy_bytes(int I, int gs) { return DecLayout(kH, I, gs).bytes; }
+uint64_t decode_copy_bytes(int h, int I, int gs) { return DecLayout(h, I, gs).bytes; }
 
-int launch_decode_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int I,
-                       int gs, void* stream) {
-    const DecLayout D(kH, I, gs);
+int launch_decode_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int h,
+                       int I, int gs, void* stream) {
+    const DecLayout D(h, I, gs);
     const uint64_t threads = D.bytes / 16 * (uint64_t)E;
-    hipLaunchKernelGGL(decode_copy_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), layer, expert_bytes, dst, D.bytes, E, I, gs);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (h == kHW)
+        hipLaunchKernelGGL(decode_copy_kernel<kHW>, grid, dim3(256), 0, st, layer, expert_bytes,
+                           dst, D.bytes, E, I, gs);
+    else
+        hipLaunchKernelGGL(decode_copy_kernel<kH>, grid, dim3(256), 0, st, layer, expert_bytes,
+                           dst, D.bytes, E, I, gs);
     return (int)hipGetLastError();
 }
 
 int launch_moe_decode_cu(const FusedArgs& a, void* stream) {
     if (!decode_cu_fits(a.h, a.E, a.K, a.I, a.gs)) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (a.h == kHW) {
+        switch (a.gs) {
+            case 32: launch_w<0>(a, st); break;
+            case 64: launch_w<1>(a, st); break;
+            default: launch_w<2>(a, st); break;
+        }
+        return (int)hipGetLastError();
+    }
     return a.K * a.I == 8192 ? launch_ug<4>(a, st) : launch_ug<8>(a, st);
 }
 

@@ -195,9 +195,9 @@ bool decode_cu_fits(int h, int E, int K, int I, int gs);
 int launch_moe_decode_cu(const FusedArgs& a, void* stream);
 // Bytes of one expert's repacked block (decode_cu.hip) and the launch that
 // builds a layer's repacked blocks from its canonical ones.
-uint64_t decode_copy_bytes(int I, int gs);
-int launch_decode_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int I,
-                       int gs, void* stream);
+uint64_t decode_copy_bytes(int h, int I, int gs);
+int launch_decode_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int h,
+                       int I, int gs, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
 // Writes the PfScaleLayout blocks of E experts (layer image at `layer`) to
 // dst; a non-finite scale or bias raises device error flag 8.

@@ -211,6 +211,11 @@ def test_decode_small(name):
     dict(hidden=2048, num_experts=128, top_k=8, intermediate=1024, group_size=64),
     dict(hidden=2048, num_experts=96, top_k=4, intermediate=2048, group_size=64),
     dict(hidden=2048, num_experts=8, top_k=8, intermediate=1024, group_size=64),
+    # hidden 4096 (the one-workgroup-per-CU kernel for Mixtral-width layers):
+    # K = 1 and 2, 16 to 128 working workgroups per slot, gs 32 and 128
+    dict(hidden=4096, num_experts=16, top_k=1, intermediate=2048, group_size=32),
+    dict(hidden=4096, num_experts=64, top_k=2, intermediate=4096, group_size=128),
+    dict(hidden=4096, num_experts=8, top_k=2, intermediate=16384, group_size=64),
 ])
 def test_decode_ragged_shapes(kw):
     # lane maps with idle lanes (C not a divisor of 64), several chunks per lane,

@@ -840,6 +840,14 @@ constexpr int kRPT = kHW / kT;      // down rows per thread
 constexpr int kWRows = 128;         // act rows per working workgroup
 constexpr int kWChunks = kWRows / 32;
 constexpr int kMaxKW = 2;
+#ifndef M1MOE_W_INFLIGHT
+#define M1MOE_W_INFLIGHT 2
+#endif
+#ifndef M1MOE_W_EARLY
+#define M1MOE_W_EARLY 2
+#endif
+constexpr int kWInFlight = M1MOE_W_INFLIGHT;  // gate/up batches in flight per wave
+constexpr int kWEarlyDown = M1MOE_W_EARLY;    // down chunks requested during the last batches
 
 struct CuwLDS {
     alignas(16) float x[128 * 36];      // staged input, chunk c at 36 c
@@ -1053,20 +1061,23 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
     float pr[kRPT];
 #pragma unroll
     for (int r = 0; r < kRPT; ++r) pr[r] = 0.f;
+    DNChunkW D0, D1;
+    const int cg0 = r0 / 32;
     if (eg >= 0) {
         // batch b: row quad b / 2 of this wave's 16 rows, chunk half b % 2 (lane
         // l: chunk l, then chunk l + 64); two batches in flight
         const int wrow = r0 + 16 * wave;
-        GUBatchW B0, B1;
-        guw_load<GSL>(a, L, eg, wrow, lane, B0);
-        guw_load<GSL>(a, L, eg, wrow, lane + 64, B1);
+        GUBatchW Bq[kWInFlight];
+#pragma unroll
+        for (int bi = 0; bi < kWInFlight; ++bi)
+            guw_load<GSL>(a, L, eg, wrow + 4 * (bi >> 1), lane + 64 * (bi & 1), Bq[bi]);
         const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
         const uint32_t mhi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
         float pg[4], pu[4];
 #pragma unroll
         for (int bi = 0; bi < 8; ++bi) {
             const int q = bi >> 1, ch = bi & 1;
-            GUBatchW& B = ch ? B1 : B0;
+            GUBatchW& B = Bq[bi % kWInFlight];
             const uint32_t* d = s.xq[lane + 64 * ch];
             XChunk2 xc;
 #pragma unroll
@@ -1100,7 +1111,12 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
                 pu[u] = ch ? pu[u] + tu : tu;
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (bi + 2 < 8) guw_load<GSL>(a, L, eg, wrow + 4 * ((bi + 2) >> 1), lane + 64 * ch, B);
+            const int nb = bi + kWInFlight;
+            if (nb < 8) guw_load<GSL>(a, L, eg, wrow + 4 * (nb >> 1), lane + 64 * (nb & 1), B);
+            if (nb == 7) {  // every gate/up byte requested: the first down chunks next
+                if (kWEarlyDown >= 1) dnw_load<GSL>(a, eg, cg0, t, D0);
+                if (kWEarlyDown >= 2) dnw_load<GSL>(a, eg, cg0 + 1, t, D1);
+            }
             if (ch) {
                 const float v8[8] = {pg[0], pu[0], pg[1], pu[1], pg[2], pu[2], pg[3], pu[3]};
                 float gg, uu;
@@ -1110,13 +1126,9 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
             }
         }
     }
-    // the down columns of the first two chunks are requested before the act
-    // rows are complete
-    DNChunkW D0, D1;
-    const int cg0 = r0 / 32;
-    if (eg >= 0) {
-        dnw_load<GSL>(a, eg, cg0, t, D0);
-        dnw_load<GSL>(a, eg, cg0 + 1, t, D1);
+    if (eg >= 0) {  // the down chunks not yet requested
+        if (kWEarlyDown < 1) dnw_load<GSL>(a, eg, cg0, t, D0);
+        if (kWEarlyDown < 2) dnw_load<GSL>(a, eg, cg0 + 1, t, D1);
     }
     __syncthreads();
     if (eg >= 0 && wave < kWChunks / 2) {

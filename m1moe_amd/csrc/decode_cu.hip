@@ -57,6 +57,40 @@
 namespace m1moe {
 namespace {
 
+// Phase stamps of moe_decode_cu_kernel, compiled only into the tracing build
+// (make -C m1moe_amd/csrc trace, -DM1MOE_DECODE_TRACE): s_memrealtime (100
+// MHz) per workgroup into LDS, written at the end of the launch to the buffer
+// that m1moe_trace_decode() set ([workgroup][64 slots]; none set: nothing is
+// written).  Slot numbers are listed by m1moe_amd/csrc/probes/decode_timeline.cpp.
+#ifdef M1MOE_DECODE_TRACE
+__device__ unsigned long long* g_decode_trace;
+__shared__ unsigned long long s_dtr[64];
+#define DTR_BEGIN()                                      \
+    do {                                                 \
+        if (threadIdx.x < 64) s_dtr[threadIdx.x] = 0ull; \
+        __syncthreads();                                 \
+    } while (0)
+#define DTR_WAVE(slot)                                                                   \
+    do {                                                                                 \
+        if ((threadIdx.x & 63) == 0) s_dtr[(slot)] = __builtin_amdgcn_s_memrealtime();  \
+    } while (0)
+#define DTR_WG(slot)                                                          \
+    do {                                                                      \
+        if (threadIdx.x == 0) s_dtr[(slot)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define DTR_END()                                                                          \
+    do {                                                                                   \
+        __syncthreads();                                                                   \
+        if (g_decode_trace && threadIdx.x < 64)                                            \
+            g_decode_trace[(size_t)blockIdx.x * 64 + threadIdx.x] = s_dtr[threadIdx.x];    \
+    } while (0)
+#else
+#define DTR_BEGIN() do {} while (0)
+#define DTR_WAVE(slot) do {} while (0)
+#define DTR_WG(slot) do {} while (0)
+#define DTR_END() do {} while (0)
+#endif
+
 constexpr int kW = 8;               // waves per workgroup
 constexpr int kT = 64 * kW;         // threads per workgroup
 constexpr int kNG = kCuWorkgroups;  // workgroups
@@ -173,8 +207,10 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
 #pragma unroll
         for (int j = 0; j < 4; ++j) s.v[lane + 64 * j] = v[j];
         if (lane == 0) s.ok = ok ? 1 : 0;
+        DTR_WAVE(4);
     }
     __syncthreads();
+    DTR_WG(5);
     // ranks over ep = 2^LEP experts (E rounded up, at least 64; the padding
     // is -inf at indices above every expert)
     const int lep = E <= 64 ? 6 : (E <= 128 ? 7 : 8);
@@ -184,6 +220,7 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
         rank_cu<7>(t, E, K, s);
     else
         rank_cu<8>(t, E, K, s);
+    DTR_WG(7);
     __syncthreads();
 }
 
@@ -217,20 +254,6 @@ __device__ void weights_cu(const FusedArgs& a, int lane, S& s) {
 }
 
 // ---- the repacked copy of an expert block ---------------------------------------------
-
-// Byte offsets within one expert's repacked block (h = 2048):
-//   gsb: [I/4 row quads][h/gs groups][4 rows][gate s | gate b << 16, up s | up b << 16]
-//   dw:  [I/32 column chunks][h rows][4 words]  (the down matrix, chunk-major)
-//   dsb: [I/gs groups][512][4]: entry (t, r) = down s | down b << 16 of row t + 512 r
-struct DecLayout {
-    uint64_t gsb, dw, dsb, bytes;
-    __host__ __device__ DecLayout(int h, int I, int gs) {
-        gsb = 0;
-        dw = (uint64_t)I * (uint64_t)(h / gs) * 8;
-        dsb = dw + (uint64_t)h * (uint64_t)(I / 2);
-        bytes = (dsb + (uint64_t)(I / gs) * (uint64_t)h * 4 + 255) / 256 * 256;
-    }
-};
 
 // One thread per 16 bytes of the repacked block, all experts of a layer
 // (H = hidden width: 2048, or 4096 for moe_decode_cuw_kernel).
@@ -588,6 +611,8 @@ template <int UG, int GSL, bool LO>
 __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     constexpr int NC = UG / 4;
     __shared__ CuLDS s;
+    DTR_BEGIN();
+    DTR_WG(0);
     const int g = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int E = a.E, K = a.K, I = a.I;
     // logit g % E is computed by every workgroup g < E * copies (identical
@@ -652,6 +677,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
         st_u64(a.slots + (size_t)t * kRepStride + le,
                ((unsigned long long)tag << 32) | __float_as_uint(l));
     }
+    DTR_WG(1);
 
     // the gate/up input, chunk c of x for lane c of every wave: prepared once
     // per workgroup by wave 1 while wave 0 awaits the logits
@@ -675,10 +701,12 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
         }
         d[32] = __float_as_uint(c1[0].xs);
         d[33] = __float_as_uint(vinv);
+        DTR_WAVE(2);
     }
 
     route_cu(a, g, t, wave, lane, tag, s);
     const bool ok_run = s.ok != 0;
+    DTR_WG(3);
     XChunk2 xc;
     float inv;
     {
@@ -724,23 +752,28 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     // ---- gate/up + SwiGLU, then the act chunks ----------------------------------------
     // (LO: an f32 input's lo halves take part; a bf16 input is exact in f16)
     if (eg >= 0) gu_compute_cu<UG, LO>(wave, lane, gt, xc, inv, s);
+    DTR_WAVE(8 + wave);
     // the act chunks are prepared (wave 0) while the other waves expand their
     // down nibbles (the down bytes, requested last, are the last to arrive)
     __syncthreads();
     if (wave == 0 && eg >= 0) prep_chunks<UG>(lane, s);
+    if (wave == 0) DTR_WAVE(16);
     DNExpCU<NC> dx;
     if (eg >= 0) dn_expand_cu<NC>(dt, dx);  // (waits for this wave's down loads)
+    DTR_WAVE(40 + wave);
     __syncthreads();
 
     // ---- down partials of all 2048 rows from this workgroup's columns ------------------
     float pr[4] = {0.f, 0.f, 0.f, 0.f};
     if (eg >= 0) dn_compute_cu<NC>(dx, s, pr);
+    DTR_WAVE(24 + wave);
     // row t + 512 r goes to output block (t + 512 r) / 8, position t % 8, at this
     // workgroup's place; eight lanes fill one 32-byte run
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         st_u32(a.cu_part + ((size_t)((t + (kH / 4) * r) >> 3) * kNG + g) * kRows + (t & 7),
                tagged(pr[r], parity));
+    DTR_WG(17);
 
     // the combine weights, off the path to the partial stores (read after the
     // barrier that follows the reduction)
@@ -774,6 +807,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
             __builtin_amdgcn_s_sleep(4);
         }
     }
+    DTR_WAVE(32 + wave);
     // the values without their tag bit (the same in every launch); the
     // sources of one slot are wps consecutive lanes (32 or 64)
     const float yv[4] = {__uint_as_float(q.x & ~1u), __uint_as_float(q.y & ~1u),
@@ -801,7 +835,9 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
         }
         a.out[g * kRows + t] = acc;
     }
+    DTR_WG(56);
     if (t == 0) st_u32(a.cu_seen + g, tag);
+    DTR_END();
 }
 
 template <int UG, int GSL>
@@ -1250,8 +1286,18 @@ void launch_w(const FusedArgs& a, hipStream_t st) {
 
 }  // namespace
 
+#ifdef M1MOE_DECODE_TRACE
+// Tracing build only: sets (or, with NULL, clears) the device buffer that
+// moe_decode_cu_kernel writes its phase stamps to.
+extern "C" int32_t m1moe_trace_decode(void* dev_buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_decode_trace), &dev_buf, sizeof(dev_buf)) == hipSuccess
+               ? 0
+               : M1MOE_ERR_HIP;
+}
+#endif
+
 bool decode_cu_fits(int h, int E, int K, int I, int gs) {
-    if (E > kMaxE || K < 1 || gs != 32 && gs != 64 && gs != 128) return false;
+    if (E > kMaxE || K < 1 || (gs != 32 && gs != 64 && gs != 128)) return false;
     if (h == kH) {  // moe_decode_cu_kernel
         if (K > kMaxK || (kMaxK % K) != 0 || (I != 1024 && I != 2048)) return false;
         const int ug = K * I / 2048;

@@ -400,6 +400,21 @@ struct Layout {
     }
 };
 
+// Byte offsets within one expert's repacked block (h = 2048 or 4096), the copy the
+// decode_cu.hip kernels read instead of the canonical scales and down matrix:
+//   gsb: [I/4 row quads][h/gs groups][4 rows][gate s | gate b << 16, up s | up b << 16]
+//   dw:  [I/32 column chunks][h rows][4 words]  (the down matrix, chunk-major)
+//   dsb: [I/gs groups][512][h/512]: entry (t, r) = down s | down b << 16 of row t + 512 r
+struct DecLayout {
+    uint64_t gsb, dw, dsb, bytes;
+    __host__ __device__ DecLayout(int h, int I, int gs) {
+        gsb = 0;
+        dw = (uint64_t)I * (uint64_t)(h / gs) * 8;
+        dsb = dw + (uint64_t)h * (uint64_t)(I / 2);
+        bytes = (dsb + (uint64_t)(I / gs) * (uint64_t)h * 4 + 255) / 256 * 256;
+    }
+};
+
 __device__ __forceinline__ void flag_error(uint32_t* err, uint32_t code) {
     if (err) atomicOr(err, code);
 }

@@ -121,27 +121,27 @@ int32_t refresh_decode_copy(m1moe_ctx_t ctx, int32_t layer) {
     return M1MOE_OK;
 }
 
-int32_t launch_pfs_copy(m1moe_ctx_t ctx, int32_t layer) {
+int32_t launch_pft_copy(m1moe_ctx_t ctx, int32_t layer) {
     const uint64_t lb = (uint64_t)ctx->g.E * ctx->g.expert_bytes;
-    HIP_TRY((hipError_t)m1moe::launch_pf_scale_copy(
+    HIP_TRY((hipError_t)m1moe::launch_pf_tile_copy(
         ctx->arena + (uint64_t)layer * lb, ctx->g.expert_bytes,
-        ctx->pfs + (uint64_t)layer * ctx->g.E * ctx->pfs_bytes, ctx->g.E, ctx->g.h, ctx->g.I,
+        ctx->pft + (uint64_t)layer * ctx->g.E * ctx->pft_bytes, ctx->g.E, ctx->g.h, ctx->g.I,
         ctx->g.gs, ctx->err, ctx->stream));
-    ctx->pfs_stale[layer] = false;
+    ctx->pft_stale[layer] = false;
     return M1MOE_OK;
 }
 
-// The prefill scale blocks of a layer whose expert blocks were handed out for
+// The prefill copies of a layer whose expert blocks were handed out for
 // writing since they were made.
-int32_t refresh_pfs_copy(m1moe_ctx_t ctx, int32_t layer) {
-    if (!ctx->pfs_stale[layer]) return M1MOE_OK;
+int32_t refresh_pft_copy(m1moe_ctx_t ctx, int32_t layer) {
+    if (!ctx->pft_stale[layer]) return M1MOE_OK;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(ctx->stream, &cs));
     if (cs != hipStreamCaptureStatusNone)
         return fail(M1MOE_ERR_INVALID,
                     "layer %d's expert blocks were handed out for writing since its prefill "
-                    "scales were made; run its prefill once outside stream capture first", layer);
-    return launch_pfs_copy(ctx, layer);
+                    "copy was made; run its prefill once outside stream capture first", layer);
+    return launch_pft_copy(ctx, layer);
 }
 
 int enqueue_decode(m1moe_ctx_t ctx, const m1moe::FusedArgs& a) {
@@ -250,7 +250,7 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
         (rc = check_dev_ptr(d_topk_w, "d_topk_w", true)))
         return rc;
     if ((rc = require_loaded(ctx, layer, true))) return rc;
-    if ((rc = set_device(ctx)) || (rc = refresh_pfs_copy(ctx, layer))) return rc;
+    if ((rc = set_device(ctx)) || (rc = refresh_pft_copy(ctx, layer))) return rc;
     uint8_t* sbase = nullptr;
     if (use_static) {
         const uint64_t need = prefill_scratch_packed(ctx->g, T);
@@ -284,8 +284,8 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
     m1moe::PrefillArgs a{};
     a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
     a.expert_bytes = g.expert_bytes;
-    a.pfs_base = ctx->pfs + (uint64_t)layer * g.E * ctx->pfs_bytes;
-    a.pfs_bytes = ctx->pfs_bytes;
+    a.pft_base = ctx->pft + (uint64_t)layer * g.E * ctx->pft_bytes;
+    a.pft_bytes = ctx->pft_bytes;
     a.x = d_x;
     a.x_bf16 = (x_dtype == M1MOE_BF16);
     a.residual = d_residual;
@@ -389,7 +389,7 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (void* p : ctx->allocs) (void)hipFree(p);
-    void* owned[] = {ctx->arena,   ctx->dec,      ctx->pfs,      ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
+    void* owned[] = {ctx->arena,   ctx->dec,      ctx->pft,      ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
                      ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
                      ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part, ctx->attn_cnt};
@@ -464,10 +464,10 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
                 return cleanup(rc);
         }
     }
-    c->pfs_bytes = m1moe::PfScaleLayout(g.h, g.I, g.gs).bytes;
-    c->pfs_stale.assign(s->num_layers, false);
+    c->pft_bytes = m1moe::PfTileLayout(g.h, g.I, g.gs).bytes;
+    c->pft_stale.assign(s->num_layers, false);
     if ((rc = device_alloc((void**)&c->arena, L * E * g.expert_bytes, "expert arena")) ||
-        (rc = device_alloc((void**)&c->pfs, L * E * c->pfs_bytes, "prefill scale blocks")) ||
+        (rc = device_alloc((void**)&c->pft, L * E * c->pft_bytes, "prefill expert copy")) ||
         (rc = device_alloc((void**)&c->routers, L * E * g.h * 2, "routers")) ||
         (rc = device_alloc((void**)&c->biases, L * E * 4, "logit biases")) ||
         (rc = device_alloc((void**)&c->logits, cap * E * 4, "logits")) ||
@@ -510,7 +510,7 @@ int32_t m1moe_upload_layer_experts(m1moe_ctx_t ctx, int32_t layer, const void* h
             ctx->stream));
         ctx->dec_stale[layer] = false;
     }
-    if ((rc = launch_pfs_copy(ctx, layer))) return rc;
+    if ((rc = launch_pft_copy(ctx, layer))) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     ctx->layer_loaded[layer] = true;
     return M1MOE_OK;
@@ -559,7 +559,7 @@ int32_t m1moe_expert_block(m1moe_ctx_t ctx, int32_t layer, int32_t expert, void*
     if (!dev_ptr) return fail(M1MOE_ERR_INVALID, "null output");
     *dev_ptr = ctx->arena + ((uint64_t)layer * ctx->g.E + (uint64_t)expert) * ctx->g.expert_bytes;
     if (ctx->decode_cu) ctx->dec_stale[layer] = true;  // the caller may write the block
-    ctx->pfs_stale[layer] = true;
+    ctx->pft_stale[layer] = true;
     return M1MOE_OK;
 }
 

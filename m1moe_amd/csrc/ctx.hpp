@@ -56,12 +56,13 @@ struct m1moe_ctx {
     uint8_t* dec = nullptr;
     uint64_t dec_bytes = 0;
     std::vector<bool> dec_stale;
-    // the prefill GEMMs' f16 scale/bias pairs with a power of two per row
-    // (pfs, [L][E][pfs_bytes], PfScaleLayout), made at upload and, like the
-    // decode copy, again after m1moe_expert_block (pfs_stale)
-    uint8_t* pfs = nullptr;
-    uint64_t pfs_bytes = 0;
-    std::vector<bool> pfs_stale;
+    // the prefill GEMMs' copy of every expert block, operand tiles as the
+    // GEMM's LDS images with f16 scale/bias pairs and a power of two per row
+    // (pft, [L][E][pft_bytes], PfTileLayout), made at upload and, like the
+    // decode copy, again after m1moe_expert_block (pft_stale)
+    uint8_t* pft = nullptr;
+    uint64_t pft_bytes = 0;
+    std::vector<bool> pft_stale;
     uint32_t* err = nullptr;         // sticky device error flag
     // prefill scratch, grown on demand to the largest T seen (pf_cap tokens)
     int32_t pf_cap = 0;

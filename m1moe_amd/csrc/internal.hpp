@@ -127,24 +127,39 @@ struct RouterArgs {
     uint32_t* counters;          // [T] zero-initialised, self-resetting
 };
 
-// Per-expert scale block of the prefill GEMMs, made on the device at upload
-// (launch_pf_scale_copy): for gate and up (I rows of h/gs groups) and down (h
-// rows of I/gs groups), one u32 per (row, group) = f16(s * 2^(18 - k)) |
-// f16(b * 2^-k) << 16, then one int8 k per row (gate rows, up rows, down
-// rows).  k, the smallest k >= 0 that keeps s * 2^(18 - k) and every
-// dequantised weight (15|s| + |b|) * 2^-k within f16 range, is undone on the
-// row's accumulator (x 2^k, exact).
-struct PfScaleLayout {
-    uint64_t gate, up, down, kg, ku, kd, bytes;
-    M1MOE_HD PfScaleLayout(int h, int I, int gs) {
-        const uint64_t gh = (uint64_t)(h / gs), gi = (uint64_t)(I / gs);
-        gate = 0;
-        up = (uint64_t)I * gh * 4;
-        down = up + (uint64_t)I * gh * 4;
-        kg = down + (uint64_t)h * gi * 4;
-        ku = kg + (uint64_t)I;
-        kd = ku + (uint64_t)I;
-        bytes = (kd + (uint64_t)h + 255) / 256 * 256;
+// Per-expert prefill copy of an expert block, made on the device at upload
+// (launch_pf_tile_copy): the operand tiles of the prefill GEMMs stored as the
+// LDS images the GEMM copies, one contiguous chunk per (M-tile, 64-column
+// k-block):
+//   gate/up: mg = ceil(I/128) M-tiles x h/64 blocks, rows 0..127 of a tile
+//            gate rows, 128..255 the same up rows;
+//   down:    md = ceil(h/256) M-tiles x I/64 blocks, 256 down rows a tile;
+//   chunk  = A [256 rows][2 units of 16 bytes]: unit kh (the row's packed
+//            columns 32 kh .. 32 kh + 31 of the block) of tile row r at
+//            position kh ^ ((r >> 2) & 1) ^ ((r >> 3) & 1); rows past the
+//            matrix zero
+//          + S [2 groups at gs 32, else 1][256 rows]: u32 f16(s * 2^(20-k))
+//            | f16(b * 2^-k) << 16 of the block's group(s) (at gs 128 the
+//            group the block lies in);
+// then one int8 k per row: gate [mg*128], up [mg*128], down [md*256] (zero
+// past the matrix).  k, the smallest k >= 0 that keeps s * 2^(24 - k) and
+// every dequantised weight (15|s| + |b|) * 2^-k within f16 range, is undone
+// on the row's accumulator (x 2^k, exact).
+struct PfTileLayout {
+    int mg, md, kbg, kbd;        // M-tiles and k-blocks of gate/up and of down
+    uint64_t chunk, gu, dn, kg, ku, kd, bytes;
+    M1MOE_HD PfTileLayout(int h, int I, int gs) {
+        mg = (I + 127) / 128;
+        md = (h + 255) / 256;
+        kbg = h / 64;
+        kbd = I / 64;
+        chunk = 256 * 32 + (gs == 32 ? 2 : 1) * 256 * 4;
+        gu = 0;
+        dn = (uint64_t)mg * kbg * chunk;
+        kg = dn + (uint64_t)md * kbd * chunk;
+        ku = kg + (uint64_t)mg * 128;
+        kd = ku + (uint64_t)mg * 128;
+        bytes = (kd + (uint64_t)md * 256 + 255) / 256 * 256;
     }
 };
 
@@ -152,8 +167,8 @@ struct PfScaleLayout {
 struct PrefillArgs {
     const uint8_t* layer_base;   // first expert block of the layer
     uint64_t expert_bytes;
-    const uint8_t* pfs_base;     // the layer's first scale block (PfScaleLayout)
-    uint64_t pfs_bytes;          // bytes per expert of those blocks
+    const uint8_t* pft_base;     // the layer's first prefill copy (PfTileLayout)
+    uint64_t pft_bytes;          // bytes per expert of those copies
     const void* x;               // [T][h] f32 or bf16
     int32_t x_bf16;
     const float* residual;       // [T][h] or null
@@ -199,10 +214,10 @@ uint64_t decode_copy_bytes(int h, int I, int gs);
 int launch_decode_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int h,
                        int I, int gs, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
-// Writes the PfScaleLayout blocks of E experts (layer image at `layer`) to
+// Writes the PfTileLayout copies of E experts (layer image at `layer`) to
 // dst; a non-finite scale or bias raises device error flag 8.
-int launch_pf_scale_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E,
-                         int h, int I, int gs, uint32_t* err, void* stream);
+int launch_pf_tile_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int h,
+                        int I, int gs, uint32_t* err, void* stream);
 int launch_dequant(const uint8_t* expert_base, const ProjView& p, int32_t gs, float* out,
                    void* stream);
 

@@ -13,27 +13,39 @@
 //                              (largest |x| into [2^13, 2^14): exact for bf16
 //                              inputs, no f16 overflow)
 //   group                      pairs sorted by expert; N-tiles of kPfTN pairs
-//   gemm<2>                    gate and up for a (64 rows x 64 pairs) tile,
+//   gemm<2>                    gate and up for a (rows x 64 pairs) tile,
 //                              epilogue act = silu(g) * u  -> f16 [pair][I]
-//   gemm<1>                    down for a (64 rows x 64 pairs) tile -> f32 y
+//   gemm<1>                    down for a (rows x 64 pairs) tile -> f32 y
 //   combine                    out[t] = residual[t] + sum_k w_tk y[pair(t,k)]
 //                              in slot order (deterministic, no atomics)
 //
 // Dequantisation into MFMA operands.  A lane's A fragment is one packed
-// word (8 nibbles = 8 columns of one weight row).  Each nibble is moved to
-// f16 mantissa bits 6..9, which makes it the exact subnormal n * 2^-18; one
-// v_pk_fma_f16 with (s * 2^(18-k), b * 2^-k) then gives f16((n * s + b) *
-// 2^-k), a single rounding of the exact value (n * s has at most 12
-// significant bits and the FMA is fused).  k is a per-row power of two
-// (0 unless the row has a group scale |s| >= 0.25 or a weight beyond f16
-// range), made at upload with the f16 scale/bias pairs (PfScaleLayout) and
-// undone on the row's f32 accumulator.  The pairs come out in column order
-// (0,4), (1,5), (2,6), (3,7); the B fragments are stored in LDS in the same
-// permuted order (the sum over k does not depend on the order).
+// word (8 nibbles = 8 columns of one weight row, column 2i in the low nibble
+// of byte i).  Masking the word with 0x000F000F leaves columns 0 and 4 as the
+// exact f16 subnormals n * 2^-24, masking with 0x00F000F0 columns 1 and 5 as
+// n * 2^-20, and the same two masks on the word shifted right by 8 give
+// columns 2, 6 and 3, 7.  One v_pk_fma_f16 per pair with (s * 2^(24-k) or
+// s * 2^(20-k), b * 2^-k) then gives f16((n * s + b) * 2^-k), a single
+// rounding of the exact value (n * s has at most 15 significant bits and
+// the FMA is fused).  k is a per-row power of two (the smallest k >= 0 that
+// keeps s * 2^(24-k) and the row's weights within f16 range), made at upload
+// with the f16 (s * 2^(20-k), b * 2^-k) pairs (PfTileLayout) and undone on
+// the row's f32 accumulator.  The columns come out in the order 0, 4, 1, 5,
+// 2, 6, 3, 7; the B operands are stored in that order in memory (every
+// 8-column group of xq and act is permuted by its producer, prep_x and the
+// gate/up epilogue), so both operands agree and no permutation is done in
+// the GEMMs (the sum over k does not depend on the order).
 //
-// MFMA v_mfma_f32_16x16x32_f16: A 16x32 (lane l: row l%16, k 8(l/16)..+7),
-// B 32x16 (lane l: column l%16, the same k), D 16x16 (lane l: column l%16,
-// rows 4(l/16)..+3).
+// The GEMM kernel, pf_mma_kernel: 4 waves, a (128 gate and 128 up rows, or
+// 256 down rows) x 64 pairs tile, v_mfma_f32_32x32x16_f16, 64-column
+// k-blocks copied global -> LDS by the loads themselves (global_load_lds)
+// into a ring of four stages, three blocks ahead: B gathered from the pairs'
+// xq or act rows, A and the scale words from the expert's prefill copy
+// (PfTileLayout, made at upload), stored as the LDS image of a stage.
+//
+// MFMA v_mfma_f32_32x32x16_f16: A 32x16 (lane l: row l%32, k 8(l/32)..+7),
+// B 16x32 (lane l: column l%32, the same k), D 32x32 (lane l: column l%32,
+// element v: row 8(v/4) + 4(l/32) + v%4).
 #include <hip/hip_runtime.h>
 
 #include "device.hpp"
@@ -46,9 +58,14 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
 constexpr int kTN = kPfTN;
 constexpr int kMaxE = 256;
-constexpr uint32_t kNibMask = 0x03C003C0u;  // f16 mantissa bits 6..9 of both halves
+
+// Position i of a permuted 8-column group holds column perm8(i):
+// 0, 4, 1, 5, 2, 6, 3, 7.
+__host__ __device__ constexpr int perm8(int i) { return (i >> 1) | ((i & 1) << 2); }
 
 // ---- x: per-token power-of-two scale, f16 copy ----------------------------------
 
@@ -89,9 +106,10 @@ __global__ __launch_bounds__(256) void prep_x_kernel(PrefillArgs a) {
     for (int it = 0; it < 8; ++it) {
         const int d = (it * 256 + (int)threadIdx.x) * 8;
         if (d < a.h) {
+            // stored in the column order 0, 4, 1, 5, 2, 6, 3, 7 of the A fragments
             f16x8 o;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = (_Float16)(v[it][i] * scale);
+            for (int i = 0; i < 8; ++i) o[i] = (_Float16)(v[it][perm8(i)] * scale);
             *reinterpret_cast<f16x8*>(a.xq + (size_t)t * a.h + d) = o;
         }
     }
@@ -152,90 +170,235 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
 
 // ---- grouped GEMM with fused dequantisation ---------------------------------------
 
-// 8 f16 of one row in column order c0..c7 (four u32 pairs) -> the permuted
-// order (c0,c4), (c1,c5), (c2,c6), (c3,c7) of the A fragments.
-__device__ __forceinline__ uint4 permute8(const uint4& x) {
-    uint4 y;
-    y.x = __builtin_amdgcn_perm(x.z, x.x, 0x05040100u);
-    y.y = __builtin_amdgcn_perm(x.z, x.x, 0x07060302u);
-    y.z = __builtin_amdgcn_perm(x.w, x.y, 0x05040100u);
-    y.w = __builtin_amdgcn_perm(x.w, x.y, 0x07060302u);
-    return y;
-}
-
-// A fragment of one packed word: f16(n*s + b) for its 8 columns, permuted.
-__device__ __forceinline__ f16x8 dequant_word(uint32_t w, f16x2 s2, f16x2 b2) {
-    const f16x2 p0 = __builtin_bit_cast(f16x2, (w << 6) & kNibMask);
-    const f16x2 p1 = __builtin_bit_cast(f16x2, (w << 2) & kNibMask);
-    const f16x2 p2 = __builtin_bit_cast(f16x2, (w >> 2) & kNibMask);
-    const f16x2 p3 = __builtin_bit_cast(f16x2, (w >> 6) & kNibMask);
-    const f16x2 q0 = __builtin_elementwise_fma(p0, s2, b2);
-    const f16x2 q1 = __builtin_elementwise_fma(p1, s2, b2);
-    const f16x2 q2 = __builtin_elementwise_fma(p2, s2, b2);
-    const f16x2 q3 = __builtin_elementwise_fma(p3, s2, b2);
+// A fragment of one packed word: f16((n * s + b) * 2^-k) for its 8 columns in
+// the order 0, 4, 1, 5, 2, 6, 3, 7 (s24 = s * 2^(24-k), s20 = s * 2^(20-k),
+// b2 = b * 2^-k, each in both halves).
+__device__ __forceinline__ f16x8 dequant_word(uint32_t w, f16x2 s24, f16x2 s20, f16x2 b2) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 p0 = __builtin_bit_cast(f16x2, w & 0x000F000Fu);   // columns 0, 4: n * 2^-24
+    const f16x2 p1 = __builtin_bit_cast(f16x2, w & 0x00F000F0u);   // columns 1, 5: n * 2^-20
+    const f16x2 p2 = __builtin_bit_cast(f16x2, w8 & 0x000F000Fu);  // columns 2, 6
+    const f16x2 p3 = __builtin_bit_cast(f16x2, w8 & 0x00F000F0u);  // columns 3, 7
+    const f16x2 q0 = __builtin_elementwise_fma(p0, s24, b2);
+    const f16x2 q1 = __builtin_elementwise_fma(p1, s20, b2);
+    const f16x2 q2 = __builtin_elementwise_fma(p2, s24, b2);
+    const f16x2 q3 = __builtin_elementwise_fma(p3, s20, b2);
     return f16x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
 }
 
-// NMAT = 2: gate and up (K = h, rows = I), B = xq rows of the pairs' tokens,
-//           epilogue act = silu(g) * u.
-// NMAT = 1: down (K = I, rows = h), B = act rows, epilogue y.
-// KB = k per block (64, 128 or 256; K % KB == 0), GSL = log2(group_size / 32).
-// Lane (r = row in the wave's 16, kq = lane / 16) owns the KB/4 contiguous
-// columns kq*KB/4.. of its row in each block (KB/32 packed words, one
-// scale group since KB/4 <= group size); MFMA k-step s uses word s.
-// Blocks are pipelined two deep: the loads of block kb+2 are issued while
-// block kb is multiplied; B tiles go through a double-buffered LDS tile.
-template <int NMAT, int KB, int NW>
-struct PfStage {
-    static constexpr int W = KB / 32;  // packed words per lane per block
-    static constexpr int NB = KB * kTN / (8 * 64 * NW);  // uint4 of the B tile per thread
-    uint32_t aw[NMAT][W];
-    uint32_t sb[NMAT];                 // f16 s * 2^(18-k) | f16 b * 2^-k << 16
-    uint4 b[NB];                       // this thread's share of the B tile
+// The three operands of dequant_word from a PfTileLayout scale word
+// (f16 s * 2^(20-k) | f16 b * 2^-k << 16).
+__device__ __forceinline__ void scale_ops(uint32_t sb, f16x2& s24, f16x2& s20, f16x2& b2) {
+    const uint32_t lo = sb & 0xffffu, hi = sb >> 16;
+    s20 = __builtin_bit_cast(f16x2, lo | (lo << 16));
+    s24 = s20 * (f16x2){(_Float16)16.f, (_Float16)16.f};
+    b2 = __builtin_bit_cast(f16x2, hi | (hi << 16));
+}
+
+// 2^k of a row from its PfTileLayout exponent byte.
+__device__ __forceinline__ float row_scale(uint32_t k) {
+    return __uint_as_float((127u + (k & 0xffu)) << 23);
+}
+
+// ---- pipelined grouped GEMM: operands copied to LDS by the loads themselves -------
+
+// Workgroup: 4 waves, one (TM weight rows x 64 pairs) tile of one expert.
+// NMAT = 2: TM = 128; wave w owns rows 32 w .. 32 w + 31 of gate (row-mat 0)
+//           and of up (row-mat 1), B = xq rows of the pairs' tokens.
+// NMAT = 1: TM = 256; wave w owns rows 64 w .. 64 w + 63 of down (row-mats 0
+//           and 1: its two halves of 32), B = act rows of the pairs.
+// Lane l: c = l % 32 (the A row within a row-mat, the B pair within a
+// 32-pair half), kh = l / 32; in a 64-column k-block the lane owns columns
+// 32 kh .. 32 kh + 31 of its rows (4 packed words) and MFMA step s (0..3)
+// takes word s and the B columns 32 kh + 8 s .. + 7.
+//
+// A stage (one k-block) in LDS, every byte copied from global memory by
+// global_load_lds (no registers, no VALU):
+//   B  [64 pairs][8 units of 16 bytes]   unit u of pair p at position
+//      u ^ (p & 7) ^ ((p >> 3) & 1), gathered from the pairs' xq or act rows
+//   A, S  the (M-tile, k-block) chunk of the expert's prefill copy
+//      (PfTileLayout), copied as it is: it is stored as this LDS image
+// The swizzles put the 8 (or 16) lanes served together by one ds_read_b128
+// on distinct banks.  A wave copies 2 KB of B (lane j of a copy fetching the
+// unit that belongs at its position), 2 KB of A and 256 bytes (512 at group
+// size 32) of S per stage.
+//
+// Pipeline: block kb's copies are issued three blocks ahead into ring slot
+// kb % 4.  Before block kb is multiplied each wave waits until only the
+// copies of the blocks after kb are outstanding (memory loads complete in
+// issue order), then a barrier makes every wave's copies of block kb
+// visible; the slot of block kb - 1, read by every wave before that barrier,
+// is then refilled with block kb + 3.
+constexpr int kMK = 64;                       // k per block
+constexpr int kMB = kTN * kMK * 2;            // 8 KB of B
+constexpr int kMA = 256 * kMK / 2;            // 8 KB of A
+// scale words (two groups per block at gs 32) and a whole stage
+template <int GSL>
+constexpr int mma_sbytes() { return (GSL == 0 ? 2 : 1) * 256 * 4; }
+template <int GSL>
+constexpr int mma_stage() { return kMB + kMA + mma_sbytes<GSL>(); }
+
+// Per-lane sources of the copies and LDS offsets of the reads.
+struct MmaSrc {
+    const uint8_t* b[2];                      // B piece: the unit this lane copies, block 0
+    const uint8_t* a[2];                      // A piece, block 0
+    const uint8_t* sw[2];                     // scale words, block 0 (second only at gs 32)
+    uint32_t chunk;                           // bytes per block of the prefill copy
+    uint32_t boff;                            // B operand of step 0, pairs 0..31
+    uint32_t aoff[2];                         // A unit of row-mat rm
+    uint32_t soff[2];                         // scale word of row-mat rm
+    int wave;
 };
 
-template <int NMAT, int KB, int GSL, int NW>
-__global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_tiles) {
-    constexpr int W = KB / 32;
-    constexpr int TM = 16 * NW;               // weight rows per workgroup
-    constexpr int TPP = 64 * NW / kTN;        // B-staging threads per pair
-    constexpr int NB = PfStage<NMAT, KB, NW>::NB;
-    constexpr int kRow = KB * 2 + 16;  // LDS bytes per pair row (padded)
-    __shared__ __attribute__((aligned(16))) unsigned char s_b[2][kTN * kRow];
+// vmcnt(n) alone (expcnt and lgkmcnt at their maxima, no wait on them).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// global -> LDS copy of 16 (or 4) bytes per lane: lane j's bytes land at LDS
+// byte address lds + 16 j (4 j); lds is the same for the whole wave.  Written
+// as inline assembly: the compiler, which cannot tell the four ring slots
+// apart, would otherwise wait for every copy in flight before each LDS read.
+// The kernel waits for the copies itself (vmcnt, which counts them in issue
+// order with every other load) before the barrier that publishes a slot; the
+// compiler's own vmcnt waits for its loads stay safe, as copies it does not
+// know of only make them wait longer.  M0 is not listed as clobbered (the
+// compiler reserves it and warns): these kernels contain no instruction of
+// the compiler's that reads M0 (no LDS-DMA builtins, indexed lane reads or
+// messages; the generated code sets M0 only in these statements).
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+
+// LDS byte address of a pointer into LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Copies one wave issues per block: 2 of B, 2 of A, 1 or 2 of S.
+template <int GSL>
+constexpr int mma_ops() { return GSL == 0 ? 6 : 5; }
+
+// Block kb's copies into ring slot lds.  Issued for every step, also past the
+// last block (kb is then clamped: the last block is read again into a slot no
+// step reads), so that every wave always has the same number of blocks'
+// copies issued after any block's.
+template <int GSL>
+__device__ __forceinline__ void mma_issue(const MmaSrc& src, int kb, int nblk, uint32_t lds) {
+    kb = min(kb, nblk - 1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        lds_copy16(src.b[i] + (size_t)kb * (kMK * 2), lds + (2 * src.wave + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        lds_copy16(src.a[i] + (size_t)kb * src.chunk, lds + kMB + (2 * src.wave + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < (GSL == 0 ? 2 : 1); ++i)
+        lds_copy4(src.sw[i] + (size_t)kb * src.chunk, lds + kMB + kMA + i * 1024 + src.wave * 256);
+}
+
+template <int GSL>
+__device__ __forceinline__ void mma_compute(const MmaSrc& src, const uint8_t* lds,
+                                            f32x16 (&acc)[2][2]) {
+    uint4 aw[2];
+    f16x2 s24[2], s20[2], b2[2];
+#pragma unroll
+    for (int rm = 0; rm < 2; ++rm) {
+        aw[rm] = *reinterpret_cast<const uint4*>(lds + kMB + src.aoff[rm]);
+        scale_ops(*reinterpret_cast<const uint32_t*>(lds + kMB + kMA + src.soff[rm]), s24[rm],
+                  s20[rm], b2[rm]);
+    }
+    // the B operands of step s + 1 are read while step s is multiplied
+    f16x8 bf[2][2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+        bf[0][cb] = *reinterpret_cast<const f16x8*>(lds + src.boff + cb * (32 * kMK * 2));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        if (s + 1 < 4) {
+            // unit kh * 4 + s + 1 of the same pairs: position (kh * 4 + s + 1) ^
+            // swizzle = position of step 0 ^ (s + 1)
+            const uint32_t o = src.boff ^ ((uint32_t)(s + 1) << 4);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+                bf[(s + 1) & 1][cb] =
+                    *reinterpret_cast<const f16x8*>(lds + o + cb * (32 * kMK * 2));
+        }
+        f16x8 af[2];
+#pragma unroll
+        for (int rm = 0; rm < 2; ++rm) {
+            const uint32_t w = s == 0 ? aw[rm].x : s == 1 ? aw[rm].y : s == 2 ? aw[rm].z : aw[rm].w;
+            af[rm] = dequant_word(w, s24[rm], s20[rm], b2[rm]);
+        }
+#pragma unroll
+        for (int rm = 0; rm < 2; ++rm)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+                acc[rm][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rm], bf[s & 1][cb],
+                                                                     acc[rm][cb], 0, 0, 0);
+    }
+}
+
+// The k loop over a ring of NS slots of mma_stage<GSL>() bytes at LDS address ring.
+template <int GSL, int NS>
+__device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint8_t* ring,
+                                         f32x16 (&acc)[2][2]) {
+    constexpr int ops = mma_ops<GSL>();
+    constexpr int kMStage = mma_stage<GSL>();
+    static_assert((NS - 2) * ops < 64, "outstanding copies beyond the vmcnt field");
+    const uint32_t base = lds_addr(ring);
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i) mma_issue<GSL>(src, i, nblk, base + i * kMStage);
+    int slot = 0;
+    for (int kb = 0; kb < nblk; ++kb) {
+        wait_vm<(NS - 2) * ops>();  // block kb's copies are in (the NS - 2 after it may not be)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int fill = slot == 0 ? NS - 1 : slot - 1;  // the slot of block kb - 1
+        mma_issue<GSL>(src, kb + NS - 1, nblk, base + fill * kMStage);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_compute<GSL>(src, ring + slot * kMStage, acc);
+        slot = slot == NS - 1 ? 0 : slot + 1;
+    }
+    // no copy into LDS may still be in flight when the workgroup ends
+    wait_vm<0>();
+}
+
+#ifndef M1MOE_PF_STAGES
+#define M1MOE_PF_STAGES 4
+#endif
+constexpr int kMStages = M1MOE_PF_STAGES;     // ring slots (4: two workgroups per CU)
+
+template <int NMAT, int GSL>
+__global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_tiles, int nt_max) {
+    constexpr int TM = NMAT == 2 ? 128 : 256;
+    __shared__ __attribute__((aligned(1024))) uint8_t s_ring[kMStages * mma_stage<GSL>()];
     __shared__ int s_tok[kTN];
     __shared__ float s_inv[kTN];
-    // all M-tiles of one N-tile read the same B tile: give them block ids with
-    // the same residue mod 8, i.e. the same XCD (and L2)
-    const int blk = blockIdx.x;
-    const int slot = blk >> 3;
-    const int mt = slot % m_tiles;
-    const int nt = (slot / m_tiles) * 8 + (blk & 7);
-    if (nt >= a.tile_off[a.E]) return;
+    // Block ids: XCD x = id % 8 takes M-tiles x, x + 8, ...; for each, all
+    // N-tiles in order, so the N-tiles of one expert run together on one XCD
+    // and share the expert's A rows through its L2.
+    const int bid = blockIdx.x, j = bid >> 3;
+    const int mt = (j / nt_max) * 8 + (bid & 7), nt = j % nt_max;
+    if (mt >= m_tiles || nt >= a.tile_off[a.E]) return;
     const int e = a.tile_expert[nt];
     const int p0 = a.expert_off[e] + (nt - a.tile_off[e]) * kTN;
     const int np = min(kTN, a.expert_off[e + 1] - p0);
-
     const int K = NMAT == 2 ? a.h : a.I;
+    const int M = NMAT == 2 ? a.I : a.h;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r = lane & 15, kq = lane >> 4;
-    const int row = mt * TM + wave * 16 + r;  // this lane's A row
-    const int nblk = K / KB;
-    const uint32_t groups = (uint32_t)K >> (5 + GSL);
-
-    // expert sub-blocks (planar [gate W|S|B][up W|S|B][down W|S|B])
-    const uint8_t* ex = a.layer_base + (uint64_t)e * a.expert_bytes;
-    const uint8_t* px = a.pfs_base + (uint64_t)e * a.pfs_bytes;
-    const Layout L(a.h, a.I, a.gs);
-    const PfScaleLayout PL(a.h, a.I, a.gs);
-    const uint32_t* wrow[NMAT];
-    const uint32_t* sbrow[NMAT];
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-        const uint64_t wo = NMAT == 2 ? (m == 0 ? L.gate_w : L.up_w) : L.down_w;
-        const uint64_t so = NMAT == 2 ? (m == 0 ? PL.gate : PL.up) : PL.down;
-        wrow[m] = reinterpret_cast<const uint32_t*>(ex + wo) + (size_t)row * (K / 8) + kq * W;
-        sbrow[m] = reinterpret_cast<const uint32_t*>(px + so) + (size_t)row * groups;
-    }
+    const int c = lane & 31, kh = lane >> 5;
 
     if (tid < kTN) {
         const bool ok = tid < np;
@@ -245,151 +408,153 @@ __global__ __launch_bounds__(64 * NW) void pf_gemm_kernel(PrefillArgs a, int m_t
     }
     __syncthreads();
 
-    // B staging: thread -> (pair j = tid / TPP, part q = tid % TPP: KB/TPP elements)
-    const int bj = tid / TPP, bq = tid % TPP;
-    const bool b_ok = bj < np;
-    const _Float16* b_src =
-        (NMAT == 2 ? a.xq + (size_t)s_tok[bj] * a.h : a.act + (size_t)(p0 + (b_ok ? bj : 0)) * a.I) +
-        bq * (KB / TPP);
-    auto load = [&](int kb, PfStage<NMAT, KB, NW>& st) {
-        const uint4* pb = reinterpret_cast<const uint4*>(b_src + kb * KB);
+    // the expert's prefill copy: this M-tile's chunks (block 0) and row exponents
+    const PfTileLayout PT(a.h, a.I, a.gs);
+    const uint8_t* px = a.pft_base + (uint64_t)e * a.pft_bytes;
+    const uint8_t* chunk0 = px + (NMAT == 2 ? PT.gu + (uint64_t)mt * PT.kbg * PT.chunk
+                                            : PT.dn + (uint64_t)mt * PT.kbd * PT.chunk);
+    const int wrow0 = mt * TM + wave * (TM / 4);
+    // the exponents of this lane's accumulator rows, loaded now so that their
+    // latency passes with the first blocks': gate/up 8 bytes per (matrix, q)
+    // (the 8-row group 8 q of the wave's rows), down 4 bytes per (row-mat, q)
+    uint2 kx[2][4];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) st.b[i] = b_ok ? pb[i] : make_uint4(0, 0, 0, 0);
-        const uint32_t g = ((uint32_t)kb * KB + (uint32_t)kq * (KB / 4)) >> (5 + GSL);
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            const uint32_t* pw = wrow[m] + (size_t)kb * (KB / 8);
-            if constexpr (W % 4 == 0) {
-#pragma unroll
-                for (int v = 0; v < W / 4; ++v) {
-                    const uint4 q = *reinterpret_cast<const uint4*>(pw + 4 * v);
-                    st.aw[m][4 * v] = q.x; st.aw[m][4 * v + 1] = q.y;
-                    st.aw[m][4 * v + 2] = q.z; st.aw[m][4 * v + 3] = q.w;
-                }
+        for (int q = 0; q < 4; ++q) {
+            if (NMAT == 2) {
+                kx[m][q] = *reinterpret_cast<const uint2*>(px + (m == 0 ? PT.kg : PT.ku) + wrow0 +
+                                                           8 * q);
             } else {
-                const uint2 q = *reinterpret_cast<const uint2*>(pw);
-                st.aw[m][0] = q.x; st.aw[m][W > 1 ? 1 : 0] = q.y;
+                kx[m][q].x = *reinterpret_cast<const uint32_t*>(px + PT.kd + wrow0 + 32 * m +
+                                                                8 * q + 4 * kh);
+                kx[m][q].y = 0;
             }
-            st.sb[m] = sbrow[m][g];
         }
-    };
-    auto store_b = [&](int buf, const PfStage<NMAT, KB, NW>& st) {
-        uint4* d = reinterpret_cast<uint4*>(&s_b[buf][bj * kRow + bq * (KB / TPP) * 2]);
+    MmaSrc src;
+    src.wave = __builtin_amdgcn_readfirstlane(wave);
+    src.chunk = (uint32_t)PT.chunk;
 #pragma unroll
-        for (int i = 0; i < NB; ++i) d[i] = permute8(st.b[i]);
-    };
-
-    f32x4 acc[NMAT][kTN / 16];
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-        for (int j = 0; j < kTN / 16; ++j) acc[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    auto compute = [&](int buf, const PfStage<NMAT, KB, NW>& st) {
-        f16x2 s2[NMAT], b2[NMAT];
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            const uint32_t lo = st.sb[m] & 0xffffu, hi = st.sb[m] >> 16;
-            s2[m] = __builtin_bit_cast(f16x2, lo | (lo << 16));
-            b2[m] = __builtin_bit_cast(f16x2, hi | (hi << 16));
-        }
-        // two k-steps at a time: their B fragments are read from LDS and their
-        // A fragments unpacked before the 2 * 4 * NMAT MFMAs that use them
-        constexpr int SP = W >= 2 ? 2 : 1;
-#pragma unroll
-        for (int s0 = 0; s0 < W; s0 += SP) {
-            f16x8 bf[SP][kTN / 16];
-#pragma unroll
-            for (int t = 0; t < SP; ++t)
-#pragma unroll
-                for (int j = 0; j < kTN / 16; ++j)
-                    bf[t][j] = *reinterpret_cast<const f16x8*>(
-                        &s_b[buf][(j * 16 + r) * kRow + (kq * W + s0 + t) * 16]);
-            f16x8 af[SP][NMAT];
-#pragma unroll
-            for (int t = 0; t < SP; ++t)
-#pragma unroll
-                for (int m = 0; m < NMAT; ++m) af[t][m] = dequant_word(st.aw[m][s0 + t], s2[m], b2[m]);
-#pragma unroll
-            for (int t = 0; t < SP; ++t)
-#pragma unroll
-                for (int j = 0; j < kTN / 16; ++j)
-#pragma unroll
-                    for (int m = 0; m < NMAT; ++m)
-                        acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][m], bf[t][j], acc[m][j], 0, 0, 0);
-        }
-    };
-
-    PfStage<NMAT, KB, NW> S0, S1;
-    load(0, S0);
-    if (nblk > 1) load(1, S1);
-    store_b(0, S0);
-    __syncthreads();
-    // iteration kb: LDS holds B(kb); S(kb%2) holds A(kb), S((kb+1)%2) holds block kb+1
-    for (int kb = 0; kb < nblk; kb += 2) {
-        compute(0, S0);
-        if (kb + 2 < nblk) load(kb + 2, S0);
-        if (kb + 1 < nblk) store_b(1, S1);
-        __syncthreads();
-        if (kb + 1 >= nblk) break;
-        compute(1, S1);
-        if (kb + 3 < nblk) load(kb + 3, S1);
-        if (kb + 2 < nblk) store_b(0, S0);
-        __syncthreads();
+    for (int i = 0; i < 2; ++i) {
+        const int q = 2 * wave + i;                       // 1 KB piece of the stage
+        // B: pairs 8 q .. 8 q + 7, 128 bytes each
+        const int pair = 8 * q + (lane >> 3);
+        const int u = (lane & 7) ^ (pair & 7) ^ ((pair >> 3) & 1);
+        const int pc = pair < np ? pair : 0;
+        const _Float16* brow = NMAT == 2 ? a.xq + (size_t)s_tok[pc] * a.h
+                                         : a.act + (size_t)(p0 + pc) * a.I;
+        src.b[i] = reinterpret_cast<const uint8_t*>(brow) + u * 16;
+        // A: the chunk's piece q as it is; S: its words of tile rows 64 w + lane
+        src.a[i] = chunk0 + q * 1024 + lane * 16;
+        src.sw[i] = chunk0 + kMA + i * 1024 + wave * 256 + lane * 4;
     }
-    // epilogue: lane holds column (pair) j*16 + r, rows 4*kq..4*kq+3 of the wave's 16;
-    // each row's 2^k comes back on its accumulator
-    const int row0 = mt * TM + wave * 16 + 4 * kq;
-    float rs[NMAT][4];
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-        const uint64_t ko = NMAT == 2 ? (m == 0 ? PL.kg : PL.ku) : PL.kd;
-        const uint32_t k4 = *reinterpret_cast<const uint32_t*>(px + ko + row0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            rs[m][i] = __uint_as_float((uint32_t)(127 + ((k4 >> (8 * i)) & 0xffu)) << 23);
+    {
+        const uint32_t u = (uint32_t)(kh * 4) ^ (uint32_t)(c & 7) ^ (uint32_t)((c >> 3) & 1);
+        src.boff = (uint32_t)c * (kMK * 2) + (u << 4);
     }
 #pragma unroll
-    for (int j = 0; j < kTN / 16; ++j) {
-        const int n = j * 16 + r;
-        if (n >= np) continue;
-        if (NMAT == 2) {
+    for (int rm = 0; rm < 2; ++rm) {
+        // gate/up: weight row perm8 within each 8 (the accumulator rows of a lane
+        // are then 4 consecutive positions of act's permuted groups)
+        const int r = NMAT == 2 ? rm * 128 + 32 * wave + ((c & ~7) | perm8(c & 7))
+                                : 64 * wave + 32 * rm + c;
+        const int ua = kh ^ ((r >> 2) & 1) ^ ((r >> 3) & 1);
+        src.aoff[rm] = (uint32_t)r * 32 + (uint32_t)ua * 16;
+        src.soff[rm] = (GSL == 0 ? (uint32_t)kh * 1024 : 0u) + (uint32_t)r * 4;
+    }
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int rm = 0; rm < 2; ++rm)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[rm][cb][v] = 0.f;
+    mma_loop<GSL, kMStages>(src, K / kMK, s_ring, acc);
+
+    // epilogue: lane holds pair cb * 32 + c and, per row-mat, accumulator rows
+    // 8 q + 4 kh + i (element 4 q + i); each row's 2^k comes back on it
+    if (NMAT == 2) {
+        if (wrow0 >= M) return;
+        float rs[2][4][4];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int col = perm8(4 * kh + i);
+                    rs[m][q][i] =
+                        row_scale((col < 4 ? kx[m][q].x : kx[m][q].y) >> (8 * (col & 3)));
+                }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const int n = cb * 32 + c;
+            if (n >= np) continue;
             const float inv = s_inv[n];
-            _Float16 o[4];
+            _Float16* dst = a.act + (size_t)(p0 + n) * a.I + wrow0 + 4 * kh;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float g = acc[0][j][i] * rs[0][i] * inv;
-                const float u = acc[NMAT - 1][j][i] * rs[NMAT - 1][i] * inv;
-                float v = (g / (1.0f + expf(-g))) * u;  // Shaders.metal:148
-                v = fminf(fmaxf(v, -65504.f), 65504.f);
-                o[i] = (_Float16)v;
+            for (int q = 0; q < 4; ++q) {
+                _Float16 o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float g = acc[0][cb][4 * q + i] * rs[0][q][i] * inv;
+                    const float u = acc[1][cb][4 * q + i] * rs[1][q][i] * inv;
+                    float v = (g / (1.0f + expf(-g))) * u;  // Shaders.metal:148
+                    v = fminf(fmaxf(v, -65504.f), 65504.f);
+                    o[i] = (_Float16)v;
+                }
+                *reinterpret_cast<uint2*>(dst + 8 * q) = __builtin_bit_cast(uint2, o);
             }
-            *reinterpret_cast<uint2*>(a.act + (size_t)(p0 + n) * a.I + row0) =
-                __builtin_bit_cast(uint2, o);
-        } else {
-            const f32x4 y = acc[0][j];
-            *reinterpret_cast<f32x4*>(a.y + (size_t)(p0 + n) * a.h + row0) =
-                f32x4{y[0] * rs[0][0], y[1] * rs[0][1], y[2] * rs[0][2], y[3] * rs[0][3]};
+        }
+    } else {
+#pragma unroll
+        for (int rm = 0; rm < 2; ++rm) {
+            const int rb = wrow0 + 32 * rm;
+            if (rb >= M) continue;
+            float rs[4][4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rs[q][i] = row_scale(kx[rm][q].x >> (8 * i));
+            }
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const int n = cb * 32 + c;
+                if (n >= np) continue;
+                float* dst = a.y + (size_t)(p0 + n) * a.h + rb + 4 * kh;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<f32x4*>(dst + 8 * q) =
+                        f32x4{acc[rm][cb][4 * q] * rs[q][0], acc[rm][cb][4 * q + 1] * rs[q][1],
+                              acc[rm][cb][4 * q + 2] * rs[q][2], acc[rm][cb][4 * q + 3] * rs[q][3]};
+            }
         }
     }
 }
 
-// ---- the scale blocks of the prefill GEMMs (PfScaleLayout), made at upload -----------
+// ---- the prefill copy of the expert blocks (PfTileLayout), made at upload -----------
 
-// One thread per (expert, weight row): the row's power of two k and its
-// groups' f16 (s * 2^(18-k), b * 2^-k) pairs.
-__global__ __launch_bounds__(256) void pf_scale_copy_kernel(const uint8_t* src, uint64_t src_bytes,
-                                                            uint8_t* dst, uint64_t dst_bytes, int E,
-                                                            int h, int I, int gs, uint32_t* err) {
-    const int rows = 2 * I + h;
+// One thread per (expert, row of the padded gate, up and down row ranges): the
+// row's power of two k (0 past the matrix).  A non-finite scale or bias sets
+// error flag 8.
+__global__ __launch_bounds__(256) void pf_row_exp_kernel(const uint8_t* src, uint64_t src_bytes,
+                                                         uint8_t* dst, uint64_t dst_bytes, int E,
+                                                         int h, int I, int gs, uint32_t* err) {
+    const PfTileLayout P(h, I, gs);
+    const int rows = 2 * P.mg * 128 + P.md * 256;
     const uint64_t gid = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= (uint64_t)E * rows) return;
     const int e = (int)(gid / rows), ri = (int)(gid - (uint64_t)e * rows);
-    const int m = ri < I ? 0 : (ri < 2 * I ? 1 : 2);
-    const int row = m == 2 ? ri - 2 * I : ri - m * I;
+    const int m = ri < P.mg * 128 ? 0 : (ri < 2 * P.mg * 128 ? 1 : 2);
+    const int row = m == 2 ? ri - 2 * P.mg * 128 : ri - m * P.mg * 128;
+    uint8_t* d = dst + (uint64_t)e * dst_bytes + (m == 0 ? P.kg : (m == 1 ? P.ku : P.kd)) + row;
+    if (row >= (m == 2 ? h : I)) {
+        *d = 0;
+        return;
+    }
     const int groups = (m == 2 ? I : h) / gs;
     const Layout L(h, I, gs);
-    const PfScaleLayout P(h, I, gs);
     const uint8_t* b = src + (uint64_t)e * src_bytes;
     const uint16_t* sp = reinterpret_cast<const uint16_t*>(
         b + (m == 0 ? L.gate_s : (m == 1 ? L.up_s : L.down_s))) + (size_t)row * groups;
@@ -407,18 +572,74 @@ __global__ __launch_bounds__(256) void pf_scale_copy_kernel(const uint8_t* src, 
     if (!finite) {
         flag_error(err, 8u);
     } else {
-        while (k < 100 && (ldexpf(ms, 18 - k) > 65504.f || ldexpf(mw, -k) > 65504.f)) ++k;
+        while (k < 100 && (ldexpf(ms, 24 - k) > 65504.f || ldexpf(mw, -k) > 65504.f)) ++k;
     }
-    uint8_t* d = dst + (uint64_t)e * dst_bytes;
-    d[(m == 0 ? P.kg : (m == 1 ? P.ku : P.kd)) + row] = (uint8_t)k;
-    uint32_t* o = reinterpret_cast<uint32_t*>(d + (m == 0 ? P.gate : (m == 1 ? P.up : P.down))) +
-                  (size_t)row * groups;
-    for (int g = 0; g < groups; ++g) {
-        const _Float16 s16 = (_Float16)ldexpf(bf16_to_f32(sp[g]), 18 - k);
-        const _Float16 b16 = (_Float16)ldexpf(bf16_to_f32(bp[g]), -k);
-        o[g] = (uint32_t)__builtin_bit_cast(uint16_t, s16) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, b16) << 16);
+    *d = (uint8_t)k;
+}
+
+// One thread per 16 bytes of the chunks of E experts (after pf_row_exp_kernel
+// on the same stream): an A unit (16 packed bytes of one row) or four rows'
+// scale words of one group.
+__global__ __launch_bounds__(256) void pf_tile_copy_kernel(const uint8_t* src, uint64_t src_bytes,
+                                                           uint8_t* dst, uint64_t dst_bytes, int E,
+                                                           int h, int I, int gs) {
+    const PfTileLayout P(h, I, gs);
+    const uint64_t per_chunk = P.chunk / 16;
+    const uint64_t chunks = (uint64_t)P.mg * P.kbg + (uint64_t)P.md * P.kbd;
+    const uint64_t gid = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (uint64_t)E * chunks * per_chunk) return;
+    const uint64_t e = gid / (chunks * per_chunk), uo = gid - e * chunks * per_chunk;
+    const uint64_t ci = uo / per_chunk;
+    const int within = (int)(uo - ci * per_chunk) * 16;
+    const bool gu = ci < (uint64_t)P.mg * P.kbg;
+    const int mt = gu ? (int)(ci / P.kbg) : (int)((ci - (uint64_t)P.mg * P.kbg) / P.kbd);
+    const int kb = gu ? (int)(ci % P.kbg) : (int)((ci - (uint64_t)P.mg * P.kbg) % P.kbd);
+    const Layout L(h, I, gs);
+    const uint8_t* b = src + e * src_bytes;
+    uint8_t* d = dst + e * dst_bytes;
+    // tile row r -> (matrix, row); false past the matrix
+    auto tile_row = [&](int r, int& m, int& row) {
+        m = gu ? r >> 7 : 2;
+        row = gu ? mt * 128 + (r & 127) : mt * 256 + r;
+        return row < (gu ? I : h);
+    };
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (within < 256 * 32) {
+        const int r = within >> 5;
+        const int kh = ((within >> 4) & 1) ^ ((r >> 2) & 1) ^ ((r >> 3) & 1);
+        int m, row;
+        if (tile_row(r, m, row)) {
+            const int K = m == 2 ? I : h;
+            const uint64_t wo = m == 0 ? L.gate_w : (m == 1 ? L.up_w : L.down_w);
+            v = *reinterpret_cast<const uint4*>(b + wo + (uint64_t)row * (K / 2) + kb * 32 +
+                                                kh * 16);
+        }
+    } else {
+        const int so = within - 256 * 32, j = so >> 10, r0 = (so & 1023) >> 2;
+        const int g = gs == 32 ? 2 * kb + j : (gs == 64 ? kb : kb >> 1);
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int m, row;
+            w[i] = 0u;
+            if (!tile_row(r0 + i, m, row)) continue;
+            const int groups = (m == 2 ? I : h) / gs;
+            const int k = d[(m == 0 ? P.kg : (m == 1 ? P.ku : P.kd)) + row];
+            const uint64_t o = ((uint64_t)row * groups + g) * 2;
+            const float sf = bf16_to_f32(*reinterpret_cast<const uint16_t*>(
+                b + (m == 0 ? L.gate_s : (m == 1 ? L.up_s : L.down_s)) + o));
+            const float bf = bf16_to_f32(*reinterpret_cast<const uint16_t*>(
+                b + (m == 0 ? L.gate_b : (m == 1 ? L.up_b : L.down_b)) + o));
+            const _Float16 s16 = (_Float16)ldexpf(sf, 20 - k);
+            const _Float16 b16 = (_Float16)ldexpf(bf, -k);
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, s16) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, b16) << 16);
+        }
+        v = make_uint4(w[0], w[1], w[2], w[3]);
     }
+    *reinterpret_cast<uint4*>(d + (gu ? P.gu : P.dn) +
+                              ((gu ? (uint64_t)mt * P.kbg : (uint64_t)mt * P.kbd) + kb) * P.chunk +
+                              within) = v;
 }
 
 // ---- combine ----------------------------------------------------------------------
@@ -443,62 +664,44 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     *reinterpret_cast<float4*>(a.out + (size_t)t * a.h + d) = acc;
 }
 
-template <int NMAT, int GSL, int NW>
-void launch_gemm_nw(const PrefillArgs& a, hipStream_t st, int groups8, int rows) {
-    const int K = NMAT == 2 ? a.h : a.I;
-    const int m_tiles = rows / (16 * NW);
-    const dim3 grid((unsigned)(8 * groups8 * m_tiles));
-    // Eight-wave gate/up (two matrices: two waves per SIMD at any k-block)
-    // streams 256-wide k-blocks, twice the weight bytes in flight per wave at
-    // the same occupancy.  The down GEMM stays at 128: at 256 its registers
-    // would leave room for one workgroup per CU instead of two.  A lane's 64
-    // columns then still sit in one scale group (group size >= 64).
-    if constexpr (NMAT == 2 && NW == 8 && GSL >= 1) {
-        if (K % 256 == 0) {
-            hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 256, GSL, NW>), grid, dim3(64 * NW), 0, st,
-                               a, m_tiles);
-            return;
-        }
-    }
-    if (K % 128 == 0)
-        hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 128, GSL, NW>), grid, dim3(64 * NW), 0, st, a,
-                           m_tiles);
-    else
-        hipLaunchKernelGGL((pf_gemm_kernel<NMAT, 64, GSL, NW>), grid, dim3(64 * NW), 0, st, a,
-                           m_tiles);
-}
-
-// Eight waves (128 weight rows) per workgroup where the rows allow it: the
-// workgroup's B tile in LDS then feeds twice the rows, halving the B reads.
+// The M-tiles are spread over the 8 XCDs (block id % 8), the N-tiles of each
+// M-tile follow in order.  h and I are multiples of the 64-column k-blocks.
 template <int NMAT, int GSL>
-void launch_gemm(const PrefillArgs& a, hipStream_t st, int groups8, int rows) {
-    if (rows % 128 == 0)
-        launch_gemm_nw<NMAT, GSL, 8>(a, st, groups8, rows);
-    else
-        launch_gemm_nw<NMAT, GSL, 4>(a, st, groups8, rows);
+void launch_one(const PrefillArgs& a, hipStream_t st, int ntiles_max) {
+    const int M = NMAT == 2 ? a.I : a.h;
+    constexpr int TM = NMAT == 2 ? 128 : 256;
+    const int m_tiles = (M + TM - 1) / TM;
+    const int grid = 8 * ((m_tiles + 7) / 8) * ntiles_max;
+    hipLaunchKernelGGL((pf_mma_kernel<NMAT, GSL>), dim3((unsigned)grid), dim3(256), 0, st, a,
+                       m_tiles, ntiles_max);
 }
 
 template <int GSL>
 int launch_gemms(const PrefillArgs& a, hipStream_t st) {
     const int P = a.T * a.K;
     const int ntiles_max = (P + kTN - 1) / kTN + a.E;
-    const int groups8 = (ntiles_max + 7) / 8;
-    launch_gemm<2, GSL>(a, st, groups8, a.I);
+    launch_one<2, GSL>(a, st, ntiles_max);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    launch_gemm<1, GSL>(a, st, groups8, a.h);
+    launch_one<1, GSL>(a, st, ntiles_max);
     return (int)hipGetLastError();
 }
 
 }  // namespace
 
-int launch_pf_scale_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E,
-                         int h, int I, int gs, uint32_t* err, void* stream) {
-    const PfScaleLayout P(h, I, gs);
-    const uint64_t threads = (uint64_t)E * (uint64_t)(2 * I + h);
-    hipLaunchKernelGGL(pf_scale_copy_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
-                       0, static_cast<hipStream_t>(stream), layer, expert_bytes, dst, P.bytes, E,
-                       h, I, gs, err);
+int launch_pf_tile_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* dst, int E, int h,
+                        int I, int gs, uint32_t* err, void* stream) {
+    const PfTileLayout P(h, I, gs);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint64_t rows = (uint64_t)E * (uint64_t)(2 * P.mg * 128 + P.md * 256);
+    hipLaunchKernelGGL(pf_row_exp_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
+                       layer, expert_bytes, dst, P.bytes, E, h, I, gs, err);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    const uint64_t units = (uint64_t)E * ((uint64_t)P.mg * P.kbg + (uint64_t)P.md * P.kbd) *
+                           (P.chunk / 16);
+    hipLaunchKernelGGL(pf_tile_copy_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
+                       st, layer, expert_bytes, dst, P.bytes, E, h, I, gs);
     return (int)hipGetLastError();
 }
 

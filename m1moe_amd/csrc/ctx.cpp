@@ -174,16 +174,16 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
 
 // Sizes in bytes of the nine prefill scratch buffers for T tokens, in the
 // order of PrefillArgs: xq, xinv, pos, sorted_tok, expert_off, tile_off,
-// tile_expert, act, y.
+// tile_desc, act, y.
 void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[9]) {
     const uint64_t t = (uint64_t)T, P = t * (uint64_t)g.K, E = (uint64_t)g.E;
     sz[0] = t * g.h * 2;
     sz[1] = t * 4;
     sz[2] = P * 4;
-    sz[3] = P * 4;
+    sz[3] = P * 8;
     sz[4] = (E + 1) * 4;
     sz[5] = (E + 1) * 4;
-    sz[6] = (P / m1moe::kPfTN + E + 1) * 4;
+    sz[6] = (P / m1moe::kPfTN + E + 1) * 16;
     sz[7] = P * g.I * 2;
     sz[8] = P * g.h * 4;
 }
@@ -205,11 +205,11 @@ int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
     if (int32_t rc = m1moe::refuse_growth_in_capture(ctx->stream, "the prefill scratch")) return rc;
     void** bufs[9] = {(void**)&ctx->pf_xq,   (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
                       (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,
-                      (void**)&ctx->pf_texp, (void**)&ctx->pf_act,  (void**)&ctx->pf_y};
+                      (void**)&ctx->pf_tdesc, (void**)&ctx->pf_act,  (void**)&ctx->pf_y};
     static const char* const names[9] = {
         "prefill x",       "prefill x scales",   "prefill positions",
         "prefill sorted tokens", "prefill expert offsets", "prefill tile offsets",
-        "prefill tile experts",  "prefill act",        "prefill expert outputs"};
+        "prefill tile descriptors", "prefill act",        "prefill expert outputs"};
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     for (void** b : bufs) {
         if (*b) (void)hipFree(*b);
@@ -311,10 +311,10 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
         a.xq = static_cast<_Float16*>(p[0]);
         a.xinv = static_cast<float*>(p[1]);
         a.pos = static_cast<int32_t*>(p[2]);
-        a.sorted_tok = static_cast<int32_t*>(p[3]);
+        a.sorted_tok = static_cast<m1moe::PfPair*>(p[3]);
         a.expert_off = static_cast<int32_t*>(p[4]);
         a.tile_off = static_cast<int32_t*>(p[5]);
-        a.tile_expert = static_cast<int32_t*>(p[6]);
+        a.tile_desc = static_cast<m1moe::PfTile*>(p[6]);
         a.act = static_cast<_Float16*>(p[7]);
         a.y = static_cast<float*>(p[8]);
     } else {
@@ -324,11 +324,12 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
         a.sorted_tok = ctx->pf_sorted;
         a.expert_off = ctx->pf_eoff;
         a.tile_off = ctx->pf_toff;
-        a.tile_expert = ctx->pf_texp;
+        a.tile_desc = ctx->pf_tdesc;
         a.act = ctx->pf_act;
         a.y = ctx->pf_y;
     }
     a.err = ctx->err;
+    a.cus = ctx->cus;
     return launched(m1moe::launch_prefill(a, ctx->stream),
                     use_static ? "moe_prefill_noalloc" : "moe_prefill");
 }
@@ -392,7 +393,7 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     void* owned[] = {ctx->arena,   ctx->dec,      ctx->pft,      ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
                      ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
-                     ctx->pf_toff, ctx->pf_texp,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part, ctx->attn_cnt};
+                     ctx->pf_toff, ctx->pf_tdesc,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part, ctx->attn_cnt};
     for (void* p : owned)
         if (p) (void)hipFree(p);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -455,6 +456,7 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
             return cleanup(fail(M1MOE_ERR_HIP, "hipDeviceGetAttribute(multiprocessor count)"));
+        c->cus = cus;
         c->decode_cu = cus >= m1moe::kCuWorkgroups &&
                        m1moe::decode_cu_fits(g.h, g.E, g.K, g.I, g.gs);
         c->dec_stale.assign(s->num_layers, false);

@@ -26,6 +26,7 @@ struct m1moe_graph {
 
 struct m1moe_ctx {
     int32_t device = 0;
+    int32_t cus = 0;                 // compute units of the device
     m1moe_moe_shape shape{};
     m1moe::Geom g{};
     hipStream_t own_stream = nullptr;
@@ -69,10 +70,10 @@ struct m1moe_ctx {
     _Float16* pf_xq = nullptr;       // [cap][h]
     float* pf_xinv = nullptr;        // [cap]
     int32_t* pf_pos = nullptr;       // [cap*K]
-    int32_t* pf_sorted = nullptr;    // [cap*K]
+    m1moe::PfPair* pf_sorted = nullptr;       // [cap*K]
     int32_t* pf_eoff = nullptr;      // [E+1]
     int32_t* pf_toff = nullptr;      // [E+1]
-    int32_t* pf_texp = nullptr;      // [cap*K/kPfTN + E + 1]
+    m1moe::PfTile* pf_tdesc = nullptr;        // [cap*K/kPfTN + E + 1]
     _Float16* pf_act = nullptr;      // [cap*K][I]
     float* pf_y = nullptr;           // [cap*K][h]
     // this device's static scratch (scratch.hip), for m1moe_moe_prefill_noalloc;

@@ -361,11 +361,6 @@ __device__ __forceinline__ float reduce4_seg(const float (&v)[4], int lane, int 
     return m;
 }
 
-// silu(g) = g / (1 + e^-g) (Shaders.metal:148, fast-math there) on the
-// hardware exp2 and reciprocal.
-__device__ __forceinline__ float silu_fast(float g) {
-    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
-}
 
 // ---- gate/up ---------------------------------------------------------------------
 

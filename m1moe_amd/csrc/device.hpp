@@ -415,6 +415,12 @@ struct DecLayout {
     }
 };
 
+// silu(g) = g / (1 + e^-g) (Shaders.metal:148, fast-math there) on the
+// hardware exp2 and reciprocal.
+__device__ __forceinline__ float silu_fast(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
+
 __device__ __forceinline__ void flag_error(uint32_t* err, uint32_t code) {
     if (err) atomicOr(err, code);
 }

@@ -163,6 +163,16 @@ struct PfTileLayout {
     }
 };
 
+// Prefill grouping results: a sorted (token, slot) pair, and an N-tile of
+// one expert's pairs (np = 0: no tile).
+struct alignas(8) PfPair {
+    int32_t tok;
+    float inv;                   // the token's 2^-e_t
+};
+struct alignas(16) PfTile {
+    int32_t e, p0, np, pad;      // expert, first sorted position, pairs
+};
+
 // Arguments of the prefill kernels (T tokens through one layer).
 struct PrefillArgs {
     const uint8_t* layer_base;   // first expert block of the layer
@@ -180,16 +190,18 @@ struct PrefillArgs {
     _Float16* xq;                // [T][h] x * 2^e_t in f16
     float* xinv;                 // [T] 2^-e_t
     int32_t* pos;                // [T*K] sorted position of pair (t, k)
-    int32_t* sorted_tok;         // [T*K] token of each sorted position
+    PfPair* sorted_tok;          // [T*K] per sorted position
     int32_t* expert_off;         // [E+1] first sorted position of each expert
     int32_t* tile_off;           // [E+1] first N-tile of each expert
-    int32_t* tile_expert;        // [T*K/kPfTN + E] expert of each N-tile
+    PfTile* tile_desc;           // [T*K/kPfTN + E + 1] per N-tile (np = 0 past the last):
+                                 // tiles of more than kPfTN / 2 pairs first
+    int32_t cus;                 // compute units of the device
     _Float16* act;               // [T*K][I] silu(gate)*up per sorted pair
     float* y;                    // [T*K][h] expert outputs per sorted pair
     uint32_t* err;               // sticky device error flag
 };
 
-constexpr int kPfTN = 64;   // prefill GEMM: (token, slot) pairs per workgroup tile
+constexpr int kPfTN = 128;  // prefill GEMM: (token, slot) pairs per workgroup tile
 
 // m1moe_moe_prefill_noalloc: bytes of the per-GPU static scratch (scratch.hip)
 // that holds its prefill buffers.  64 MiB: 779 tokens at hidden 2048,

@@ -48,6 +48,8 @@
 // element v: row 8(v/4) + 4(l/32) + v%4).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "device.hpp"
 #include "internal.hpp"
 
@@ -123,31 +125,35 @@ __global__ __launch_bounds__(256) void prep_x_kernel(PrefillArgs a) {
 // independently of the others, so results do not depend on it).
 __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
     __shared__ int cnt[kMaxE];
-    __shared__ int sc[kMaxE], st[kMaxE];
-    __shared__ int off[kMaxE + 1], toff[kMaxE + 1];
+    __shared__ int sc[kMaxE], st[kMaxE], sb[kMaxE];
+    __shared__ int off[kMaxE + 1], toff[kMaxE + 1], boff[kMaxE + 1];
     const int tid = threadIdx.x;
     const int E = a.E, P = a.T * a.K;
     if (tid < kMaxE) cnt[tid] = 0;
     __syncthreads();
     for (int p = tid; p < P; p += 1024) a.pos[p] = atomicAdd(&cnt[a.idx[p]], 1);
     __syncthreads();
-    // inclusive scans of the pair and N-tile counts
+    // inclusive scans of the pair, N-tile and big-tile (more than kTN / 2
+    // pairs) counts
     if (tid < kMaxE) {
         const int c = tid < E ? cnt[tid] : 0;
         sc[tid] = c;
         st[tid] = (c + kTN - 1) / kTN;
+        sb[tid] = c / kTN + (c % kTN > kTN / 2 ? 1 : 0);
     }
     __syncthreads();
     for (int o = 1; o < kMaxE; o <<= 1) {
-        int vc = 0, vt = 0;
+        int vc = 0, vt = 0, vb = 0;
         if (tid < kMaxE && tid >= o) {
             vc = sc[tid - o];
             vt = st[tid - o];
+            vb = sb[tid - o];
         }
         __syncthreads();
         if (tid < kMaxE) {
             sc[tid] += vc;
             st[tid] += vt;
+            sb[tid] += vb;
         }
         __syncthreads();
     }
@@ -155,16 +161,33 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
         const int o = tid == 0 ? 0 : sc[tid - 1], to = tid == 0 ? 0 : st[tid - 1];
         off[tid] = o;
         toff[tid] = to;
+        boff[tid] = tid == 0 ? 0 : sb[tid - 1];
         a.expert_off[tid] = o;
         a.tile_off[tid] = to;
     }
     __syncthreads();
-    if (tid < E)
-        for (int j = toff[tid]; j < toff[tid + 1]; ++j) a.tile_expert[j] = tid;
+    // one descriptor per N-tile the GEMMs may see ((P + kTN - 1) / kTN + E of
+    // them): expert, first sorted position, pairs; none past the last.  The
+    // big tiles come first (expert order), then each expert's last tile when
+    // it has at most kTN / 2 pairs, so that the GEMMs' queues start the long
+    // work first.
+    const int nt_max = (P + kTN - 1) / kTN + E;
+    for (int j = tid; j < nt_max; j += 1024) a.tile_desc[j] = PfTile{0, 0, 0, 0};
+    __syncthreads();
+    if (tid < E) {
+        const int big = sb[E - 1];
+        for (int j = 0; j < toff[tid + 1] - toff[tid]; ++j) {
+            const int p0 = off[tid] + j * kTN;
+            const int np = min(kTN, off[tid + 1] - p0);
+            const int at = np > kTN / 2 ? boff[tid] + j : big + (toff[tid] - boff[tid]);
+            a.tile_desc[at] = PfTile{tid, p0, np, 0};
+        }
+    }
     for (int p = tid; p < P; p += 1024) {
         const int q = off[a.idx[p]] + a.pos[p];
+        const int t = p / a.K;
         a.pos[p] = q;
-        a.sorted_tok[q] = p / a.K;
+        a.sorted_tok[q] = PfPair{t, a.xinv[t]};
     }
 }
 
@@ -202,52 +225,60 @@ __device__ __forceinline__ float row_scale(uint32_t k) {
 
 // ---- pipelined grouped GEMM: operands copied to LDS by the loads themselves -------
 
-// Workgroup: 4 waves, one (TM weight rows x 64 pairs) tile of one expert.
+// Workgroup: 4 waves, one (TM weight rows x kTN = 128 pairs) tile of one expert.
 // NMAT = 2: TM = 128; wave w owns rows 32 w .. 32 w + 31 of gate (row-mat 0)
 //           and of up (row-mat 1), B = xq rows of the pairs' tokens.
 // NMAT = 1: TM = 256; wave w owns rows 64 w .. 64 w + 63 of down (row-mats 0
 //           and 1: its two halves of 32), B = act rows of the pairs.
-// Lane l: c = l % 32 (the A row within a row-mat, the B pair within a
-// 32-pair half), kh = l / 32; in a 64-column k-block the lane owns columns
+// Lane l: c = l % 32 (the A row within a row-mat, the B pair within each
+// 32-pair quarter), kh = l / 32; in a 64-column k-block the lane owns columns
 // 32 kh .. 32 kh + 31 of its rows (4 packed words) and MFMA step s (0..3)
-// takes word s and the B columns 32 kh + 8 s .. + 7.
+// takes word s and the B columns 32 kh + 8 s .. + 7.  Every dequantised A
+// fragment feeds 4 MFMAs per row-mat (one per quarter); a tile with at most
+// 64 pairs (NQ = 2) copies and multiplies only its first two quarters.
 //
 // A stage (one k-block) in LDS, every byte copied from global memory by
 // global_load_lds (no registers, no VALU):
-//   B  [64 pairs][8 units of 16 bytes]   unit u of pair p at position
-//      u ^ (p & 7) ^ ((p >> 3) & 1), gathered from the pairs' xq or act rows
 //   A, S  the (M-tile, k-block) chunk of the expert's prefill copy
 //      (PfTileLayout), copied as it is: it is stored as this LDS image
+//   B  [128 pairs][8 units of 16 bytes]   unit u of pair p at position
+//      u ^ (p & 7) ^ ((p >> 3) & 1), gathered from the pairs' xq or act rows
 // The swizzles put the 8 (or 16) lanes served together by one ds_read_b128
-// on distinct banks.  A wave copies 2 KB of B (lane j of a copy fetching the
-// unit that belongs at its position), 2 KB of A and 256 bytes (512 at group
-// size 32) of S per stage.
+// on distinct banks.  Per stage a wave copies 2 KB of A, 256 bytes (512 at
+// group size 32) of S and 4 KB (2 KB at NQ = 2) of B, each copy addressed by
+// a wave-uniform base in SGPRs, advanced per block by scalar adds, plus a
+// fixed per-lane offset (lane j of a B copy fetching the unit that belongs
+// at its position).
 //
-// Pipeline: block kb's copies are issued three blocks ahead into ring slot
-// kb % 4.  Before block kb is multiplied each wave waits until only the
-// copies of the blocks after kb are outstanding (memory loads complete in
-// issue order), then a barrier makes every wave's copies of block kb
-// visible; the slot of block kb - 1, read by every wave before that barrier,
-// is then refilled with block kb + 3.
+// Pipeline: three ring slots; block kb's copies are issued two blocks ahead
+// into slot kb % 3.  Before block kb is multiplied each wave waits until only
+// the copies of block kb + 1 are outstanding (memory loads complete in issue
+// order), then a barrier makes every wave's copies of block kb visible; the
+// slot of block kb - 1, read by every wave before that barrier, is then
+// refilled with block kb + 2.
 constexpr int kMK = 64;                       // k per block
-constexpr int kMB = kTN * kMK * 2;            // 8 KB of B
 constexpr int kMA = 256 * kMK / 2;            // 8 KB of A
+constexpr int kMB = kTN * kMK * 2;            // 16 KB of B
 // scale words (two groups per block at gs 32) and a whole stage
 template <int GSL>
 constexpr int mma_sbytes() { return (GSL == 0 ? 2 : 1) * 256 * 4; }
 template <int GSL>
-constexpr int mma_stage() { return kMB + kMA + mma_sbytes<GSL>(); }
+constexpr int mma_stage() { return kMA + mma_sbytes<GSL>() + kMB; }
+constexpr int kMSlots = 3;
 
-// Per-lane sources of the copies and LDS offsets of the reads.
+// Copy sources (per block kb: base + kb * stride, plus the lane's offset) and
+// the lane's LDS read offsets within a stage.
 struct MmaSrc {
-    const uint8_t* b[2];                      // B piece: the unit this lane copies, block 0
-    const uint8_t* a[2];                      // A piece, block 0
-    const uint8_t* sw[2];                     // scale words, block 0 (second only at gs 32)
+    const uint8_t* bbase;                     // first B row (xq or act), block 0
+    const uint8_t* abase;                     // the M-tile's chunk of block 0
     uint32_t chunk;                           // bytes per block of the prefill copy
-    uint32_t boff;                            // B operand of step 0, pairs 0..31
-    uint32_t aoff[2];                         // A unit of row-mat rm
-    uint32_t soff[2];                         // scale word of row-mat rm
-    int wave;
+    uint32_t boff[4];                         // B copy i: the lane's unit of its pair's row
+    uint32_t aoff[2];                         // A copy i
+    uint32_t soff[2];                         // S copy i (second only at gs 32)
+    uint32_t bread[4];                        // B operand of step s, pairs 0..31
+    uint32_t aread[2];                        // A unit of row-mat rm
+    uint32_t sread[2];                        // scale word of row-mat rm
+    uint32_t wave;
 };
 
 // vmcnt(n) alone (expcnt and lgkmcnt at their maxima, no wait on them).
@@ -257,27 +288,28 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// global -> LDS copy of 16 (or 4) bytes per lane: lane j's bytes land at LDS
-// byte address lds + 16 j (4 j); lds is the same for the whole wave.  Written
-// as inline assembly: the compiler, which cannot tell the four ring slots
-// apart, would otherwise wait for every copy in flight before each LDS read.
-// The kernel waits for the copies itself (vmcnt, which counts them in issue
+// global -> LDS copy of 16 (or 4) bytes per lane from sbase + voff (sbase in
+// SGPRs, voff the lane's 32-bit offset): lane j's bytes land at LDS byte
+// address lds + 16 j (4 j); lds is the same for the whole wave.  Written as
+// inline assembly: the compiler, which cannot tell the ring slots apart,
+// would otherwise wait for every copy in flight before each LDS read.  The
+// kernel waits for the copies itself (vmcnt, which counts them in issue
 // order with every other load) before the barrier that publishes a slot; the
 // compiler's own vmcnt waits for its loads stay safe, as copies it does not
 // know of only make them wait longer.  M0 is not listed as clobbered (the
 // compiler reserves it and warns): these kernels contain no instruction of
 // the compiler's that reads M0 (no LDS-DMA builtins, indexed lane reads or
 // messages; the generated code sets M0 only in these statements).
-__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+__device__ __forceinline__ void lds_copy16(uint32_t voff, const uint8_t* sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
-                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "v"(voff), "s"(sbase), "s"(lds)
                  : "memory");
 }
-__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+__device__ __forceinline__ void lds_copy4(uint32_t voff, const uint8_t* sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
                  :
-                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "v"(voff), "s"(sbase), "s"(lds)
                  : "memory");
 }
 
@@ -286,54 +318,54 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// Copies one wave issues per block: 2 of B, 2 of A, 1 or 2 of S.
-template <int GSL>
-constexpr int mma_ops() { return GSL == 0 ? 6 : 5; }
+// Copies one wave issues per block: A 2, S 1 or 2, B 4 (2 at NQ = 2).
+template <int GSL, int NQ>
+constexpr int mma_ops() { return 2 + (GSL == 0 ? 2 : 1) + NQ; }
 
-// Block kb's copies into ring slot lds.  Issued for every step, also past the
-// last block (kb is then clamped: the last block is read again into a slot no
-// step reads), so that every wave always has the same number of blocks'
-// copies issued after any block's.
-template <int GSL>
-__device__ __forceinline__ void mma_issue(const MmaSrc& src, int kb, int nblk, uint32_t lds) {
+// Block kb's copies into ring slot SLOT (ring: LDS address of slot 0).
+// Issued for every step, also past the last block (kb is then clamped: the
+// last block is read again into a slot no step reads), so that every wave
+// always has the same number of copies issued after any block's.
+template <int GSL, int NQ, int SLOT>
+__device__ __forceinline__ void mma_issue(const MmaSrc& src, int kb, int nblk, uint32_t ring) {
     kb = min(kb, nblk - 1);
+    const uint32_t st = ring + SLOT * mma_stage<GSL>();
+    const uint8_t* ab = src.abase + (size_t)kb * src.chunk;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-        lds_copy16(src.b[i] + (size_t)kb * (kMK * 2), lds + (2 * src.wave + i) * 1024);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        lds_copy16(src.a[i] + (size_t)kb * src.chunk, lds + kMB + (2 * src.wave + i) * 1024);
+    for (int i = 0; i < 2; ++i) lds_copy16(src.aoff[i], ab, st + (2 * src.wave + i) * 1024);
 #pragma unroll
     for (int i = 0; i < (GSL == 0 ? 2 : 1); ++i)
-        lds_copy4(src.sw[i] + (size_t)kb * src.chunk, lds + kMB + kMA + i * 1024 + src.wave * 256);
+        lds_copy4(src.soff[i], ab, st + kMA + i * 1024 + src.wave * 256);
+    const uint8_t* bb = src.bbase + (size_t)kb * (kMK * 2);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+        lds_copy16(src.boff[i], bb, st + kMA + mma_sbytes<GSL>() + (NQ * src.wave + i) * 1024);
 }
 
-template <int GSL>
+template <int GSL, int NQ>
 __device__ __forceinline__ void mma_compute(const MmaSrc& src, const uint8_t* lds,
-                                            f32x16 (&acc)[2][2]) {
+                                            f32x16 (&acc)[2][4]) {
+    constexpr int kB = kMA + mma_sbytes<GSL>();   // B's offset in a stage
     uint4 aw[2];
     f16x2 s24[2], s20[2], b2[2];
 #pragma unroll
     for (int rm = 0; rm < 2; ++rm) {
-        aw[rm] = *reinterpret_cast<const uint4*>(lds + kMB + src.aoff[rm]);
-        scale_ops(*reinterpret_cast<const uint32_t*>(lds + kMB + kMA + src.soff[rm]), s24[rm],
+        aw[rm] = *reinterpret_cast<const uint4*>(lds + src.aread[rm]);
+        scale_ops(*reinterpret_cast<const uint32_t*>(lds + kMA + src.sread[rm]), s24[rm],
                   s20[rm], b2[rm]);
     }
     // the B operands of step s + 1 are read while step s is multiplied
-    f16x8 bf[2][2];
+    f16x8 bf[2][NQ];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-        bf[0][cb] = *reinterpret_cast<const f16x8*>(lds + src.boff + cb * (32 * kMK * 2));
+    for (int q = 0; q < NQ; ++q)
+        bf[0][q] = *reinterpret_cast<const f16x8*>(lds + kB + src.bread[0] + q * (32 * kMK * 2));
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         if (s + 1 < 4) {
-            // unit kh * 4 + s + 1 of the same pairs: position (kh * 4 + s + 1) ^
-            // swizzle = position of step 0 ^ (s + 1)
-            const uint32_t o = src.boff ^ ((uint32_t)(s + 1) << 4);
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
-                bf[(s + 1) & 1][cb] =
-                    *reinterpret_cast<const f16x8*>(lds + o + cb * (32 * kMK * 2));
+            for (int q = 0; q < NQ; ++q)
+                bf[(s + 1) & 1][q] = *reinterpret_cast<const f16x8*>(
+                    lds + kB + src.bread[s + 1] + q * (32 * kMK * 2));
         }
         f16x8 af[2];
 #pragma unroll
@@ -344,190 +376,207 @@ __device__ __forceinline__ void mma_compute(const MmaSrc& src, const uint8_t* ld
 #pragma unroll
         for (int rm = 0; rm < 2; ++rm)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
-                acc[rm][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rm], bf[s & 1][cb],
-                                                                     acc[rm][cb], 0, 0, 0);
+            for (int q = 0; q < NQ; ++q)
+                acc[rm][q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rm], bf[s & 1][q],
+                                                                    acc[rm][q], 0, 0, 0);
     }
 }
 
-// The k loop over a ring of NS slots of mma_stage<GSL>() bytes at LDS address ring.
-template <int GSL, int NS>
+// The k loop over the three ring slots of ring (unrolled by 3: every slot's
+// LDS offsets are constants).
+template <int GSL, int NQ>
 __device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint8_t* ring,
-                                         f32x16 (&acc)[2][2]) {
-    constexpr int ops = mma_ops<GSL>();
-    constexpr int kMStage = mma_stage<GSL>();
-    static_assert((NS - 2) * ops < 64, "outstanding copies beyond the vmcnt field");
-    const uint32_t base = lds_addr(ring);
-#pragma unroll
-    for (int i = 0; i < NS - 1; ++i) mma_issue<GSL>(src, i, nblk, base + i * kMStage);
-    int slot = 0;
-    for (int kb = 0; kb < nblk; ++kb) {
-        wait_vm<(NS - 2) * ops>();  // block kb's copies are in (the NS - 2 after it may not be)
+                                         f32x16 (&acc)[2][4]) {
+    constexpr int ops = mma_ops<GSL, NQ>();
+    constexpr int stage = mma_stage<GSL>();
+    const uint32_t rl = lds_addr(ring);
+    mma_issue<GSL, NQ, 0>(src, 0, nblk, rl);
+    mma_issue<GSL, NQ, 1>(src, 1, nblk, rl);
+    auto step = [&](int kb, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        if (kb >= nblk) return;
+        wait_vm<ops>();  // block kb's copies are in (block kb + 1's may not be)
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        const int fill = slot == 0 ? NS - 1 : slot - 1;  // the slot of block kb - 1
-        mma_issue<GSL>(src, kb + NS - 1, nblk, base + fill * kMStage);
+        mma_issue<GSL, NQ, (S + 2) % 3>(src, kb + 2, nblk, rl);
         __builtin_amdgcn_sched_barrier(0);
-        mma_compute<GSL>(src, ring + slot * kMStage, acc);
-        slot = slot == NS - 1 ? 0 : slot + 1;
+        mma_compute<GSL, NQ>(src, ring + S * stage, acc);
+    };
+    for (int kb = 0; kb < nblk; kb += 3) {
+        step(kb, std::integral_constant<int, 0>{});
+        step(kb + 1, std::integral_constant<int, 1>{});
+        step(kb + 2, std::integral_constant<int, 2>{});
     }
     // no copy into LDS may still be in flight when the workgroup ends
     wait_vm<0>();
 }
 
-#ifndef M1MOE_PF_STAGES
-#define M1MOE_PF_STAGES 4
-#endif
-constexpr int kMStages = M1MOE_PF_STAGES;     // ring slots (4: two workgroups per CU)
-
+// Persistent: the workgroups of an XCD take the (N-tile, M-tile) items of
+// their queue in turn (workgroup j of the queue: items j, j + W, ... for W
+// workgroups on the queue).  Queue x (block id % 8, modulo the M-tile count
+// when there are fewer than 8 M-tiles) holds M-tiles x, x + 8, ... of every
+// N-tile, big N-tiles first and, per N-tile, its M-tiles in a row: the long
+// items start first, and the N-tiles of one expert run together on one XCD
+// and share the expert's A rows through its L2.
 template <int NMAT, int GSL>
-__global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_tiles, int nt_max) {
+__global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_tiles) {
     constexpr int TM = NMAT == 2 ? 128 : 256;
-    __shared__ __attribute__((aligned(1024))) uint8_t s_ring[kMStages * mma_stage<GSL>()];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_ring[kMSlots * mma_stage<GSL>()];
     __shared__ int s_tok[kTN];
     __shared__ float s_inv[kTN];
-    // Block ids: XCD x = id % 8 takes M-tiles x, x + 8, ...; for each, all
-    // N-tiles in order, so the N-tiles of one expert run together on one XCD
-    // and share the expert's A rows through its L2.
-    const int bid = blockIdx.x, j = bid >> 3;
-    const int mt = (j / nt_max) * 8 + (bid & 7), nt = j % nt_max;
-    if (mt >= m_tiles || nt >= a.tile_off[a.E]) return;
-    const int e = a.tile_expert[nt];
-    const int p0 = a.expert_off[e] + (nt - a.tile_off[e]) * kTN;
-    const int np = min(kTN, a.expert_off[e + 1] - p0);
     const int K = NMAT == 2 ? a.h : a.I;
     const int M = NMAT == 2 ? a.I : a.h;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c = lane & 31, kh = lane >> 5;
+    const int nq = min(8, m_tiles);
+    const int queue = (int)(blockIdx.x & 7) % nq;
+    const int n_mg = (m_tiles - queue + nq - 1) / nq;
+    const int items = a.tile_off[a.E] * n_mg;
+    const int xcds = (8 - queue + nq - 1) / nq;               // block id residues on this queue
+    const int per_queue = (int)(gridDim.x >> 3) * xcds;       // workgroups taking this queue
+    const int first = (int)(blockIdx.x >> 3) * xcds + (int)(blockIdx.x & 7) / nq;
+    for (int item = first; item < items; item += per_queue) {
+        // every wave is done with the previous item's LDS before the next starts
+        __syncthreads();
+        const int mt = (item % n_mg) * nq + queue;
+        const PfTile desc = a.tile_desc[item / n_mg];
+        const int e = desc.e, p0 = desc.p0, np = desc.np;
 
-    if (tid < kTN) {
-        const bool ok = tid < np;
-        const int tok = (NMAT == 2 && ok) ? a.sorted_tok[p0 + tid] : 0;
-        s_tok[tid] = tok;
-        if (NMAT == 2) s_inv[tid] = ok ? a.xinv[tok] : 0.f;
-    }
-    __syncthreads();
-
-    // the expert's prefill copy: this M-tile's chunks (block 0) and row exponents
-    const PfTileLayout PT(a.h, a.I, a.gs);
-    const uint8_t* px = a.pft_base + (uint64_t)e * a.pft_bytes;
-    const uint8_t* chunk0 = px + (NMAT == 2 ? PT.gu + (uint64_t)mt * PT.kbg * PT.chunk
-                                            : PT.dn + (uint64_t)mt * PT.kbd * PT.chunk);
-    const int wrow0 = mt * TM + wave * (TM / 4);
-    // the exponents of this lane's accumulator rows, loaded now so that their
-    // latency passes with the first blocks': gate/up 8 bytes per (matrix, q)
-    // (the 8-row group 8 q of the wave's rows), down 4 bytes per (row-mat, q)
-    uint2 kx[2][4];
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if (NMAT == 2) {
-                kx[m][q] = *reinterpret_cast<const uint2*>(px + (m == 0 ? PT.kg : PT.ku) + wrow0 +
-                                                           8 * q);
-            } else {
-                kx[m][q].x = *reinterpret_cast<const uint32_t*>(px + PT.kd + wrow0 + 32 * m +
-                                                                8 * q + 4 * kh);
-                kx[m][q].y = 0;
-            }
+        if (NMAT == 2 && tid < kTN) {
+            const PfPair ti = tid < np ? a.sorted_tok[p0 + tid] : PfPair{0, 0.f};
+            s_tok[tid] = ti.tok;
+            s_inv[tid] = ti.inv;
         }
-    MmaSrc src;
-    src.wave = __builtin_amdgcn_readfirstlane(wave);
-    src.chunk = (uint32_t)PT.chunk;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int q = 2 * wave + i;                       // 1 KB piece of the stage
-        // B: pairs 8 q .. 8 q + 7, 128 bytes each
-        const int pair = 8 * q + (lane >> 3);
-        const int u = (lane & 7) ^ (pair & 7) ^ ((pair >> 3) & 1);
-        const int pc = pair < np ? pair : 0;
-        const _Float16* brow = NMAT == 2 ? a.xq + (size_t)s_tok[pc] * a.h
-                                         : a.act + (size_t)(p0 + pc) * a.I;
-        src.b[i] = reinterpret_cast<const uint8_t*>(brow) + u * 16;
-        // A: the chunk's piece q as it is; S: its words of tile rows 64 w + lane
-        src.a[i] = chunk0 + q * 1024 + lane * 16;
-        src.sw[i] = chunk0 + kMA + i * 1024 + wave * 256 + lane * 4;
-    }
-    {
-        const uint32_t u = (uint32_t)(kh * 4) ^ (uint32_t)(c & 7) ^ (uint32_t)((c >> 3) & 1);
-        src.boff = (uint32_t)c * (kMK * 2) + (u << 4);
-    }
-#pragma unroll
-    for (int rm = 0; rm < 2; ++rm) {
-        // gate/up: weight row perm8 within each 8 (the accumulator rows of a lane
-        // are then 4 consecutive positions of act's permuted groups)
-        const int r = NMAT == 2 ? rm * 128 + 32 * wave + ((c & ~7) | perm8(c & 7))
-                                : 64 * wave + 32 * rm + c;
-        const int ua = kh ^ ((r >> 2) & 1) ^ ((r >> 3) & 1);
-        src.aoff[rm] = (uint32_t)r * 32 + (uint32_t)ua * 16;
-        src.soff[rm] = (GSL == 0 ? (uint32_t)kh * 1024 : 0u) + (uint32_t)r * 4;
-    }
+        __syncthreads();
 
-    f32x16 acc[2][2];
-#pragma unroll
-    for (int rm = 0; rm < 2; ++rm)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[rm][cb][v] = 0.f;
-    mma_loop<GSL, kMStages>(src, K / kMK, s_ring, acc);
-
-    // epilogue: lane holds pair cb * 32 + c and, per row-mat, accumulator rows
-    // 8 q + 4 kh + i (element 4 q + i); each row's 2^k comes back on it
-    if (NMAT == 2) {
-        if (wrow0 >= M) return;
-        float rs[2][4][4];
+        // the expert's prefill copy: this M-tile's chunks (block 0) and row exponents
+        const PfTileLayout PT(a.h, a.I, a.gs);
+        const uint8_t* px = a.pft_base + (uint64_t)e * a.pft_bytes;
+        const int wrow0 = mt * TM + wave * (TM / 4);
+        // the exponents of this lane's accumulator rows, loaded now so that their
+        // latency passes with the first blocks': gate/up 8 bytes per (matrix, q)
+        // (the 8-row group 8 q of the wave's rows), down 4 bytes per (row-mat, q)
+        uint2 kx[2][4];
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int col = perm8(4 * kh + i);
-                    rs[m][q][i] =
-                        row_scale((col < 4 ? kx[m][q].x : kx[m][q].y) >> (8 * (col & 3)));
-                }
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const int n = cb * 32 + c;
-            if (n >= np) continue;
-            const float inv = s_inv[n];
-            _Float16* dst = a.act + (size_t)(p0 + n) * a.I + wrow0 + 4 * kh;
-#pragma unroll
             for (int q = 0; q < 4; ++q) {
-                _Float16 o[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float g = acc[0][cb][4 * q + i] * rs[0][q][i] * inv;
-                    const float u = acc[1][cb][4 * q + i] * rs[1][q][i] * inv;
-                    float v = (g / (1.0f + expf(-g))) * u;  // Shaders.metal:148
-                    v = fminf(fmaxf(v, -65504.f), 65504.f);
-                    o[i] = (_Float16)v;
+                if (NMAT == 2) {
+                    kx[m][q] = *reinterpret_cast<const uint2*>(
+                        px + (m == 0 ? PT.kg : PT.ku) + wrow0 + 8 * q);
+                } else {
+                    kx[m][q].x = *reinterpret_cast<const uint32_t*>(px + PT.kd + wrow0 + 32 * m +
+                                                                    8 * q + 4 * kh);
+                    kx[m][q].y = 0;
                 }
-                *reinterpret_cast<uint2*>(dst + 8 * q) = __builtin_bit_cast(uint2, o);
             }
+        const bool full = np > kTN / 2;       // NQ = 4, else 2
+        MmaSrc src;
+        src.wave = __builtin_amdgcn_readfirstlane(wave);
+        src.chunk = (uint32_t)PT.chunk;
+        src.abase = px + (NMAT == 2 ? PT.gu + (uint64_t)mt * PT.kbg * PT.chunk
+                                    : PT.dn + (uint64_t)mt * PT.kbd * PT.chunk);
+        src.bbase = reinterpret_cast<const uint8_t*>(NMAT == 2 ? a.xq : a.act + (size_t)p0 * a.I);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            // A: the chunk's piece 2 w + i as it is; S: its words of tile rows 64 w + lane
+            src.aoff[i] = (uint32_t)((2 * wave + i) * 1024 + lane * 16);
+            src.soff[i] = (uint32_t)(kMA + i * 1024 + wave * 256 + lane * 4);
         }
-    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // B: piece (NQ w + i) holds pairs 8 piece .. + 7, 128 bytes each
+            const int piece = (full ? 4 : 2) * wave + i;
+            const int pair = 8 * piece + (lane >> 3);
+            const int u = (lane & 7) ^ (pair & 7) ^ ((pair >> 3) & 1);
+            const int pc = pair < np ? pair : 0;
+            const uint64_t row = NMAT == 2 ? (uint64_t)s_tok[pc] * a.h : (uint64_t)pc * a.I;
+            src.boff[i] = (uint32_t)(row * 2 + u * 16);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t u =
+                (uint32_t)(kh * 4 + s) ^ (uint32_t)(c & 7) ^ (uint32_t)((c >> 3) & 1);
+            src.bread[s] = (uint32_t)c * (kMK * 2) + (u << 4);
+        }
 #pragma unroll
         for (int rm = 0; rm < 2; ++rm) {
-            const int rb = wrow0 + 32 * rm;
-            if (rb >= M) continue;
-            float rs[4][4];
+            // gate/up: weight row perm8 within each 8 (the accumulator rows of a lane
+            // are then 4 consecutive positions of act's permuted groups)
+            const int r = NMAT == 2 ? rm * 128 + 32 * wave + ((c & ~7) | perm8(c & 7))
+                                    : 64 * wave + 32 * rm + c;
+            const int ua = kh ^ ((r >> 2) & 1) ^ ((r >> 3) & 1);
+            src.aread[rm] = (uint32_t)r * 32 + (uint32_t)ua * 16;
+            src.sread[rm] = (GSL == 0 ? (uint32_t)kh * 1024 : 0u) + (uint32_t)r * 4;
+        }
+
+        f32x16 acc[2][4];
+#pragma unroll
+        for (int rm = 0; rm < 2; ++rm)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[rm][q][v] = 0.f;
+        if (full)
+            mma_loop<GSL, 4>(src, K / kMK, s_ring, acc);
+        else
+            mma_loop<GSL, 2>(src, K / kMK, s_ring, acc);
+
+        // epilogue: lane holds pair q * 32 + c and, per row-mat, accumulator rows
+        // 8 v + 4 kh + i (element 4 v + i); each row's 2^k comes back on it
+        if (NMAT == 2 && wrow0 < M) {
+            float rs[2][4][4];
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int col = perm8(4 * kh + i);
+                        rs[m][v][i] =
+                            row_scale((col < 4 ? kx[m][v].x : kx[m][v].y) >> (8 * (col & 3)));
+                    }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) rs[q][i] = row_scale(kx[rm][q].x >> (8 * i));
-            }
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const int n = cb * 32 + c;
+                const int n = q * 32 + c;
                 if (n >= np) continue;
-                float* dst = a.y + (size_t)(p0 + n) * a.h + rb + 4 * kh;
+                const float inv = s_inv[n];
+                _Float16* dst = a.act + (size_t)(p0 + n) * a.I + wrow0 + 4 * kh;
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *reinterpret_cast<f32x4*>(dst + 8 * q) =
-                        f32x4{acc[rm][cb][4 * q] * rs[q][0], acc[rm][cb][4 * q + 1] * rs[q][1],
-                              acc[rm][cb][4 * q + 2] * rs[q][2], acc[rm][cb][4 * q + 3] * rs[q][3]};
+                for (int v = 0; v < 4; ++v) {
+                    _Float16 o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float g = acc[0][q][4 * v + i] * rs[0][v][i] * inv;
+                        const float u = acc[1][q][4 * v + i] * rs[1][v][i] * inv;
+                        float y = silu_fast(g) * u;  // Shaders.metal:148
+                        y = fminf(fmaxf(y, -65504.f), 65504.f);
+                        o[i] = (_Float16)y;
+                    }
+                    *reinterpret_cast<uint2*>(dst + 8 * v) = __builtin_bit_cast(uint2, o);
+                }
+            }
+        } else if (NMAT == 1) {
+#pragma unroll
+            for (int rm = 0; rm < 2; ++rm) {
+                const int rb = wrow0 + 32 * rm;
+                if (rb >= M) continue;
+                float rs[4][4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) rs[v][i] = row_scale(kx[rm][v].x >> (8 * i));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int n = q * 32 + c;
+                    if (n >= np) continue;
+                    float* dst = a.y + (size_t)(p0 + n) * a.h + rb + 4 * kh;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        *reinterpret_cast<f32x4*>(dst + 8 * v) = f32x4{
+                            acc[rm][q][4 * v] * rs[v][0], acc[rm][q][4 * v + 1] * rs[v][1],
+                            acc[rm][q][4 * v + 2] * rs[v][2], acc[rm][q][4 * v + 3] * rs[v][3]};
+                }
             }
         }
     }
@@ -664,16 +713,18 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     *reinterpret_cast<float4*>(a.out + (size_t)t * a.h + d) = acc;
 }
 
-// The M-tiles are spread over the 8 XCDs (block id % 8), the N-tiles of each
-// M-tile follow in order.  h and I are multiples of the 64-column k-blocks.
+// Two persistent workgroups per compute unit (at most one per item), a
+// multiple of 8 so that every XCD holds the same number.
 template <int NMAT, int GSL>
 void launch_one(const PrefillArgs& a, hipStream_t st, int ntiles_max) {
     const int M = NMAT == 2 ? a.I : a.h;
     constexpr int TM = NMAT == 2 ? 128 : 256;
     const int m_tiles = (M + TM - 1) / TM;
-    const int grid = 8 * ((m_tiles + 7) / 8) * ntiles_max;
+    const long items = (long)ntiles_max * m_tiles;
+    const long cap = 2L * (a.cus > 0 ? a.cus : 256);
+    const int grid = (int)((std::min(items, cap) + 7) / 8 * 8);
     hipLaunchKernelGGL((pf_mma_kernel<NMAT, GSL>), dim3((unsigned)grid), dim3(256), 0, st, a,
-                       m_tiles, ntiles_max);
+                       m_tiles);
 }
 
 template <int GSL>

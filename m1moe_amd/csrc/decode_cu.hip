@@ -57,8 +57,8 @@
 namespace m1moe {
 namespace {
 
-// Phase stamps of moe_decode_cu_kernel, compiled only into the tracing build
-// (make -C m1moe_amd/csrc trace, -DM1MOE_DECODE_TRACE): s_memrealtime (100
+// Phase stamps of the per-CU kernels, compiled only into the tracing build
+// (make -C m1moe_amd/csrc probes, -DM1MOE_DECODE_TRACE): s_memrealtime (100
 // MHz) per workgroup into LDS, written at the end of the launch to the buffer
 // that m1moe_trace_decode() set ([workgroup][64 slots]; none set: nothing is
 // written).  Slot numbers are listed by m1moe_amd/csrc/probes/decode_timeline.cpp.
@@ -984,6 +984,8 @@ __device__ __forceinline__ void dnw_compute(const DNChunkW& d, const uint32_t* x
 template <int GSL, bool LO>
 __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
     __shared__ CuwLDS s;
+    DTR_BEGIN();
+    DTR_WG(0);
     const int g = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int E = a.E, K = a.K, I = a.I;
     const int wps = I / kWRows;               // working workgroups per slot
@@ -1055,6 +1057,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
         st_u64(a.slots + (size_t)t * kRepStride + g,
                ((unsigned long long)tag << 32) | __float_as_uint(l));
     }
+    DTR_WG(1);
     // the gate/up input chunks (lane l of every wave uses chunks l and l + 64),
     // prepared once per workgroup by waves 1 and 2 while wave 0 awaits the logits
     if (wave == 1 || wave == 2) {
@@ -1082,6 +1085,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
 
     route_cu(a, g, t, wave, lane, tag, s);
     const bool ok_run = s.ok != 0;
+    DTR_WG(3);
 
     // ---- working workgroups: gate/up of 128 act rows, then their down columns ------
     const bool working = g < nwork;
@@ -1157,6 +1161,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
             }
         }
     }
+    DTR_WAVE(8 + wave);
     if (eg >= 0) {  // the down chunks not yet requested
         if (kWEarlyDown < 1) dnw_load<GSL>(a, eg, cg0, t, D0);
         if (kWEarlyDown < 2) dnw_load<GSL>(a, eg, cg0 + 1, t, D1);
@@ -1186,6 +1191,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
         }
     }
     __syncthreads();
+    DTR_WG(16);
     if (eg >= 0) {
         dnw_compute(D0, s.xp[0], pr);
         dnw_load<GSL>(a, eg, cg0 + 2, t, D0);
@@ -1194,6 +1200,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
         dnw_compute(D0, s.xp[2], pr);
         dnw_compute(D1, s.xp[3], pr);
     }
+    DTR_WAVE(24 + wave);
     if (working) {
         // row t + 512 r -> block (t + 512 r) / 16, position t % 16, at this workgroup's place
 #pragma unroll
@@ -1201,6 +1208,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
             st_u32(a.cu_part + ((size_t)((t + 512 * r) >> 4) * kNG + g) * kRowsW + (t & 15),
                    tagged(pr[r], parity));
     }
+    DTR_WG(17);
     if (wave == kW - 1) {
         weights_cu(a, lane, s);
         if (g == 0 && ok_run && lane < K) {
@@ -1236,6 +1244,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
             __builtin_amdgcn_s_sleep(2);
         }
     }
+    DTR_WAVE(32 + wave);
     // stage the sources in LDS (x is no longer used): src[t][16]
     float* stage = s.x;
     if (t < nwork) {
@@ -1268,7 +1277,9 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
         }
         a.out[g * kRowsW + t] = acc;
     }
+    DTR_WG(56);
     if (t == 0) st_u32(a.cu_seen + g, tag);
+    DTR_END();
 }
 
 template <int GSL>

@@ -1,4 +1,5 @@
-// decode_timeline — where the time of one moe_decode_cu_kernel launch goes.
+// decode_timeline — where the time of one per-CU MoE decode launch goes
+// (moe_decode_cu_kernel at hidden 2048, moe_decode_cuw_kernel at 4096).
 //
 // Not part of the library.  Built by `make -C m1moe_amd/csrc probes` into
 // m1moe_amd/_probes/decode_timeline, linked against the tracing build of the
@@ -8,14 +9,15 @@
 // into LDS at the phase boundaries below and writes the stamps of each
 // workgroup at its end to the buffer set by m1moe_trace_decode().
 //
-// Workload: the OLMoE-shaped layer (h 2048, 64 experts, top-8, I 1024, 4-bit
-// group 64) with R synthetic replicas, one token per replica, the R launches
+// Workload: cfg0, the OLMoE-shaped layer (h 2048, 64 experts, top-8, I 1024,
+// 4-bit group 64), or cfg2, the Mixtral-shaped one (h 4096, 8 experts, top-2,
+// I 14336), with R synthetic replicas, one token per replica, the R launches
 // captured in one graph as in bench.py.  Prints the launch time of the
 // tracing build with no buffer set, then per phase the spread over all
 // workgroups of 5 traced replays (the graph's last replica), in us from the
 // first workgroup's start.
 //
-// usage: decode_timeline [bf16|f32] [R]
+// usage: decode_timeline [bf16|f32] [R] [cfg0|cfg2]
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -47,8 +49,10 @@ extern "C" int32_t m1moe_trace_decode(void* dev_buf);
 
 int main(int argc, char** argv) {
     const bool f32 = argc > 1 && strcmp(argv[1], "f32") == 0;
-    const int R = argc > 2 ? atoi(argv[2]) : 38;
-    m1moe_moe_shape sh{2048, 64, 8, 1024, 64, R, 0};
+    const bool mixtral = argc > 3 && strcmp(argv[3], "cfg2") == 0;
+    const int R = argc > 2 ? atoi(argv[2]) : (mixtral ? 8 : 38);
+    m1moe_moe_shape sh = mixtral ? m1moe_moe_shape{4096, 8, 2, 14336, 64, R, 0}
+                                 : m1moe_moe_shape{2048, 64, 8, 1024, 64, R, 0};
     m1moe_ctx_t ctx;
     M1CHK(m1moe_create(0, &sh, &ctx));
     uint64_t eb;
@@ -104,8 +108,8 @@ int main(int argc, char** argv) {
     M1CHK(m1moe_event_record(ctx, e1));
     float ms = 0.f;
     M1CHK(m1moe_event_elapsed_ms(e0, e1, &ms));
-    printf("%s input, %d replicas: %.3f us per launch (tracing build, no buffer set)\n",
-           f32 ? "f32" : "bf16", R, ms * 1000.0 / (30.0 * R));
+    printf("%s, %s input, %d replicas: %.3f us per launch (tracing build, no buffer set)\n",
+           mixtral ? "cfg2" : "cfg0", f32 ? "f32" : "bf16", R, ms * 1000.0 / (30.0 * R));
 
     constexpr int G = 256, S = 64, NT = 5;
     unsigned long long* tb;
@@ -122,14 +126,16 @@ int main(int argc, char** argv) {
         unsigned long long t0 = ~0ull;
         for (int w = 0; w < G; ++w)
             if (t[(size_t)w * S]) t0 = std::min(t0, t[(size_t)w * S]);
-        for (int w = 0; w < G; ++w)
+        // (cfg2: the 224 workgroups that multiply; the other 32 only route and reduce)
+        const int gw = mixtral ? sh.top_k * sh.intermediate / 128 : G;
+        for (int w = 0; w < gw; ++w)
             for (int s = 0; s < S; ++s)
                 if (t[(size_t)w * S + s]) acc[s].push_back((double)(t[(size_t)w * S + s] - t0) * 0.01);
     }
     M1CHK(m1moe_trace_decode(nullptr));
-    printf("phase stamps over %d traced replays (all 256 workgroups), us from the first "
-           "workgroup's start\n\n| phase | n | min | p10 | median | p90 | max |\n"
-           "|---|---|---|---|---|---|---|\n", NT);
+    printf("phase stamps over %d traced replays (%s), us from the first workgroup's start\n\n"
+           "| phase | n | min | p10 | median | p90 | max |\n|---|---|---|---|---|---|---|\n",
+           NT, mixtral ? "the 224 working workgroups" : "all 256 workgroups");
     auto stat = [&](const char* name, int s) {
         std::vector<double> v = acc[s];
         if (v.empty()) return;
@@ -140,7 +146,7 @@ int main(int argc, char** argv) {
     char name[96];
     stat("start", 0);
     stat("router logit published (workgroups < E)", 1);
-    stat("x chunks prepared (wave 1)", 2);
+    if (!mixtral) stat("x chunks prepared (wave 1)", 2);
     stat("logits polled (wave 0)", 4);
     stat("rank: logits in LDS", 5);
     stat("rank: top-K written", 7);
@@ -149,7 +155,7 @@ int main(int argc, char** argv) {
         snprintf(name, sizeof name, "gate/up + SwiGLU done, wave %d", w);
         stat(name, 8 + w);
     }
-    stat("act chunks prepared (wave 0)", 16);
+    stat(mixtral ? "act chunks prepared (after barrier)" : "act chunks prepared (wave 0)", 16);
     for (int w = 0; w < 8; ++w) {
         snprintf(name, sizeof name, "down nibbles expanded, wave %d", w);
         stat(name, 40 + w);

@@ -234,8 +234,8 @@ __device__ __forceinline__ float row_scale(uint32_t k) {
 // 32-pair quarter), kh = l / 32; in a 64-column k-block the lane owns columns
 // 32 kh .. 32 kh + 31 of its rows (4 packed words) and MFMA step s (0..3)
 // takes word s and the B columns 32 kh + 8 s .. + 7.  Every dequantised A
-// fragment feeds 4 MFMAs per row-mat (one per quarter); a tile with at most
-// 64 pairs (NQ = 2) copies and multiplies only its first two quarters.
+// fragment feeds one MFMA per quarter of the tile's pairs; a tile copies and
+// multiplies only the NQ = ceil(pairs / 32) quarters it has.
 //
 // A stage (one k-block) in LDS, every byte copied from global memory by
 // global_load_lds (no registers, no VALU):
@@ -245,7 +245,7 @@ __device__ __forceinline__ float row_scale(uint32_t k) {
 //      u ^ (p & 7) ^ ((p >> 3) & 1), gathered from the pairs' xq or act rows
 // The swizzles put the 8 (or 16) lanes served together by one ds_read_b128
 // on distinct banks.  Per stage a wave copies 2 KB of A, 256 bytes (512 at
-// group size 32) of S and 4 KB (2 KB at NQ = 2) of B, each copy addressed by
+// group size 32) of S and NQ KB of B, each copy addressed by
 // a wave-uniform base in SGPRs, advanced per block by scalar adds, plus a
 // fixed per-lane offset (lane j of a B copy fetching the unit that belongs
 // at its position).
@@ -318,7 +318,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// Copies one wave issues per block: A 2, S 1 or 2, B 4 (2 at NQ = 2).
+// Copies one wave issues per block: A 2, S 1 or 2, B NQ.
 template <int GSL, int NQ>
 constexpr int mma_ops() { return 2 + (GSL == 0 ? 2 : 1) + NQ; }
 
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
                     kx[m][q].y = 0;
                 }
             }
-        const bool full = np > kTN / 2;       // NQ = 4, else 2
+        const int nq4 = (np + 31) >> 5;       // NQ, quarters of 32 pairs
         MmaSrc src;
         src.wave = __builtin_amdgcn_readfirstlane(wave);
         src.chunk = (uint32_t)PT.chunk;
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // B: piece (NQ w + i) holds pairs 8 piece .. + 7, 128 bytes each
-            const int piece = (full ? 4 : 2) * wave + i;
+            const int piece = nq4 * wave + i;
             const int pair = 8 * piece + (lane >> 3);
             const int u = (lane & 7) ^ (pair & 7) ^ ((pair >> 3) & 1);
             const int pc = pair < np ? pair : 0;
@@ -517,10 +517,12 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[rm][q][v] = 0.f;
-        if (full)
-            mma_loop<GSL, 4>(src, K / kMK, s_ring, acc);
-        else
-            mma_loop<GSL, 2>(src, K / kMK, s_ring, acc);
+        switch (nq4) {
+            case 1: mma_loop<GSL, 1>(src, K / kMK, s_ring, acc); break;
+            case 2: mma_loop<GSL, 2>(src, K / kMK, s_ring, acc); break;
+            case 3: mma_loop<GSL, 3>(src, K / kMK, s_ring, acc); break;
+            default: mma_loop<GSL, 4>(src, K / kMK, s_ring, acc); break;
+        }
 
         // epilogue: lane holds pair q * 32 + c and, per row-mat, accumulator rows
         // 8 v + 4 kh + i (element 4 v + i); each row's 2^k comes back on it

@@ -204,3 +204,44 @@ public final class HIPDecoder {
     /// InferenceEngine.reset (:159-163).
     public func reset() throws { try hipCheck(m1moe_dec_reset(dec)) }
 }
+
+/// Tokenizer (Tokenizer.swift:17-229) on libm1moe_hip's host code: the same
+/// init(url:), encode(_:addBOS:bos:) and decode(_:skipSpecial:), so the chat
+/// and bench targets switch by changing the type they construct.
+public final class HIPTokenizer {
+    private var tok: m1moe_tokenizer_t?
+
+    public init(url: URL) throws {
+        try hipCheck(m1moe_tokenizer_load(url.path, &tok))
+    }
+
+    deinit { m1moe_tokenizer_free(tok) }
+
+    public func encode(_ text: String, addBOS: Bool = true, bos: UInt32 = 1) -> [UInt32] {
+        let bytes = Array(text.utf8)
+        return bytes.withUnsafeBufferPointer { b -> [UInt32] in
+            let p = UnsafeRawPointer(b.baseAddress)?.assumingMemoryBound(to: CChar.self)
+            var n: UInt64 = 0
+            guard m1moe_tokenizer_encode(tok, p, UInt64(b.count), addBOS ? 1 : 0, bos,
+                                         nil, 0, &n) == 0 else { return [] }
+            var ids = [UInt32](repeating: 0, count: Int(n))
+            let rc = ids.withUnsafeMutableBufferPointer {
+                m1moe_tokenizer_encode(tok, p, UInt64(b.count), addBOS ? 1 : 0, bos,
+                                       $0.baseAddress, n, &n)
+            }
+            return rc == 0 ? ids : []
+        }
+    }
+
+    public func decode(_ ids: [UInt32], skipSpecial: Bool = true) -> String {
+        var len: UInt64 = 0
+        guard m1moe_tokenizer_decode(tok, ids, UInt64(ids.count), skipSpecial ? 1 : 0,
+                                     nil, 0, &len) == 0 else { return "" }
+        var buf = [CChar](repeating: 0, count: Int(len) + 1)
+        guard m1moe_tokenizer_decode(tok, ids, UInt64(ids.count), skipSpecial ? 1 : 0,
+                                     &buf, UInt64(buf.count), &len) == 0 else { return "" }
+        // the bytes are UTF-8 (the library transcodes its ISO-8859-1 fallback)
+        // and may hold NULs, so they are not read as a C string
+        return String(decoding: buf.prefix(Int(len)).map { UInt8(bitPattern: $0) }, as: UTF8.self)
+    }
+}

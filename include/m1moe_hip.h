@@ -400,6 +400,54 @@ int32_t m1moe_store_tensor(m1moe_store_t store, const char* name,
 int32_t m1moe_load_model(m1moe_ctx_t ctx, m1moe_dec_t dec, const char* model_dir,
                          int32_t threads);
 
+/* ---- the converters' 4-bit quantizer (host-only; offline) ---------------
+ * quantize_4bit of scripts/extract_olmoe.py:116-159 (extract_mixtral.py
+ * :93-116 is the same): per row and group of group_size columns, in f32,
+ * lo = min, s = (max - lo) / 15 (1 where that is 0), nibble =
+ * clamp(round-half-even((w - lo) / s), 0, 15); scales = bf16(s), biases =
+ * bf16(lo), nibbles 8 per u32 (column 8w+j in bits 4j..4j+3).  cols must be
+ * a multiple of group_size and of 8 (:130-131); a non-finite weight is
+ * refused (M1MOE_ERR_INVALID).  threads: host threads over rows (<= 0: 1). */
+int32_t m1moe_quantize_4bit(const float* w, int64_t rows, int64_t cols,
+                            int32_t group_size, uint32_t* packed,
+                            uint16_t* scales, uint16_t* biases,
+                            int32_t threads);
+/* One expert block of layer_NN.bin from f32 gate [I, h], up [I, h] and
+ * down [h, I] (the per-expert loop of extract_olmoe.py:322-338):
+ * [gate W|S|B][up W|S|B][down W|S|B].  block_bytes must be expert_bytes. */
+int32_t m1moe_quantize_expert(const m1moe_moe_shape* shape, const float* gate,
+                              const float* up, const float* down, void* block,
+                              uint64_t block_bytes, int32_t threads);
+/* f32_to_bf16 of extract_olmoe.py:104-111: (bits + 0x7FFF + lsb) >> 16. */
+int32_t m1moe_f32_to_bf16(const float* x, uint64_t n, uint16_t* out);
+
+/* ---- BPE tokenizer (host-only) -------------------------------------------
+ * Tokenizer (Sources/M1MoE/Tokenizer.swift) over a HuggingFace
+ * tokenizer.json: byte-level BPE (GPT-2 / OLMoE) or, when
+ * model.byte_fallback is true, SentencePiece BPE (Mistral / Mixtral).
+ * Text crosses the boundary as UTF-8 bytes (not NUL-terminated). */
+typedef struct m1moe_tokenizer* m1moe_tokenizer_t;
+
+/* Tokenizer.init(url:) (:35-62).  M1MOE_ERR_INVALID when the file cannot be
+ * read or lacks model.vocab / model.merges (TokenizerError.invalidFormat). */
+int32_t m1moe_tokenizer_load(const char* path, m1moe_tokenizer_t* out);
+void m1moe_tokenizer_free(m1moe_tokenizer_t tok);
+/* Mode (1 = SentencePiece BPE, 0 = byte-level), vocabulary entries and merge
+ * pairs.  Each output is nullable. */
+int32_t m1moe_tokenizer_info(m1moe_tokenizer_t tok, int32_t* sentencepiece,
+                             uint64_t* vocab_size, uint64_t* merges);
+/* encode(_:addBOS:bos:) (:66-72): bos first when add_bos.  *n_ids gets the
+ * count; ids == NULL only asks for it; a count above cap is an error. */
+int32_t m1moe_tokenizer_encode(m1moe_tokenizer_t tok, const char* text,
+                               uint64_t text_len, int32_t add_bos,
+                               uint32_t bos, uint32_t* ids, uint64_t cap,
+                               uint64_t* n_ids);
+/* decode(_:skipSpecial:) (:76-81): UTF-8 bytes into out (NUL added when
+ * there is room); *out_len gets the length; out == NULL only asks for it. */
+int32_t m1moe_tokenizer_decode(m1moe_tokenizer_t tok, const uint32_t* ids,
+                               uint64_t n, int32_t skip_special, char* out,
+                               uint64_t cap, uint64_t* out_len);
+
 /* ---- seeded synthetic inputs (host-only; bench and test data) ----------
  * Counter-based: value i of tensor `tensor_id` under `seed` is a function of
  * (seed, tensor_id, i) only, so any slice can be generated independently.

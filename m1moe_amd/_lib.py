@@ -135,6 +135,20 @@ _PROTOTYPES = [
      [c_void_p, c_char_p, POINTER(c_void_p), POINTER(c_int32), POINTER(ctypes.c_int64),
       POINTER(c_int32)]),
     ("m1moe_load_model", c_int32, [c_void_p, c_void_p, c_char_p, c_int32]),
+    ("m1moe_quantize_4bit", c_int32,
+     [c_void_p, ctypes.c_int64, ctypes.c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32]),
+    ("m1moe_quantize_expert", c_int32,
+     [POINTER(MoEShape), c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_int32]),
+    ("m1moe_f32_to_bf16", c_int32, [c_void_p, c_uint64, c_void_p]),
+    ("m1moe_tokenizer_load", c_int32, [c_char_p, POINTER(c_void_p)]),
+    ("m1moe_tokenizer_free", None, [c_void_p]),
+    ("m1moe_tokenizer_info", c_int32,
+     [c_void_p, POINTER(c_int32), POINTER(c_uint64), POINTER(c_uint64)]),
+    ("m1moe_tokenizer_encode", c_int32,
+     [c_void_p, c_char_p, c_uint64, c_int32, ctypes.c_uint32, c_void_p, c_uint64,
+      POINTER(c_uint64)]),
+    ("m1moe_tokenizer_decode", c_int32,
+     [c_void_p, c_void_p, c_uint64, c_int32, c_void_p, c_uint64, POINTER(c_uint64)]),
     ("m1moe_synth_normal_bf16", c_int32,
      [c_uint64, c_uint64, c_uint64, c_float, c_int32, c_void_p]),
     ("m1moe_synth_normal_f32", c_int32, [c_uint64, c_uint64, c_uint64, c_float, c_void_p]),

@@ -67,3 +67,39 @@ def make_case(name: str, seed: int = 1234, num_layers: int = 1, router_override=
         routers.append(np.ascontiguousarray(r))
         biases.append(bias)
     return Case(name, shape, seed, ctx, images, routers, biases)
+
+
+# ---- a small byte-level tokenizer.json (chat tests) -----------------------------------------
+
+_BYTE_MERGES = [("Ġ", "t"), ("h", "e"), ("Ġt", "he"), ("i", "n"), ("e", "r"), ("Ġ", "a"),
+                ("o", "u"), ("Ġ", "s"), ("r", "e"), ("o", "n"), ("Ġ", "w"), ("a", "t"),
+                ("e", "n"), ("Ġ", "b"), ("Ġ", "m"), ("in", "g"), ("Ġ", "o"), ("Ġ", "h"),
+                ("l", "l"), ("|", ">"), ("<", "|"), ("Ċ", "<|"), ("u", "s"), ("us", "er")]
+
+
+def write_byte_tokenizer(path, eos_id: int = 299) -> dict:
+    """A GPT-2 style tokenizer.json whose ids fit a 300-entry vocabulary:
+    the 256 byte characters at ids 0..255, one id per merge after them, and
+    "<|endoftext|>" at eos_id.  Merges are "a b" strings (the form the
+    reference reads)."""
+    import json as _json
+
+    own = set(range(33, 127)) | set(range(161, 173)) | set(range(174, 256))
+    chars, extra = [], 0
+    for b in range(256):
+        if b in own:
+            chars.append(chr(b))
+        else:
+            chars.append(chr(256 + extra))
+            extra += 1
+    vocab = {c: i for i, c in enumerate(chars)}
+    for a, b in _BYTE_MERGES:
+        vocab.setdefault(a + b, len(vocab))
+    assert len(vocab) < eos_id
+    vocab["<|endoftext|>"] = eos_id
+    js = {"version": "1.0", "added_tokens": [], "normalizer": None,
+          "model": {"type": "BPE", "dropout": None, "unk_token": None, "byte_fallback": False,
+                    "vocab": vocab, "merges": [f"{a} {b}" for a, b in _BYTE_MERGES]}}
+    with open(path, "w", encoding="utf-8") as f:
+        _json.dump(js, f, ensure_ascii=False)
+    return js

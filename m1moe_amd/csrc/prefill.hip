@@ -125,35 +125,40 @@ __global__ __launch_bounds__(256) void prep_x_kernel(PrefillArgs a) {
 // independently of the others, so results do not depend on it).
 __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
     __shared__ int cnt[kMaxE];
-    __shared__ int sc[kMaxE], st[kMaxE], sb[kMaxE];
-    __shared__ int off[kMaxE + 1], toff[kMaxE + 1], boff[kMaxE + 1];
+    __shared__ int sc[kMaxE], st[kMaxE], sq[4][kMaxE];
+    __shared__ int off[kMaxE + 1], toff[kMaxE + 1], qoff[4][kMaxE + 1];
     const int tid = threadIdx.x;
     const int E = a.E, P = a.T * a.K;
     if (tid < kMaxE) cnt[tid] = 0;
     __syncthreads();
     for (int p = tid; p < P; p += 1024) a.pos[p] = atomicAdd(&cnt[a.idx[p]], 1);
     __syncthreads();
-    // inclusive scans of the pair, N-tile and big-tile (more than kTN / 2
-    // pairs) counts
+    // inclusive scans of the pair and N-tile counts, and of the tiles of
+    // each size class (c + 1 quarters of 32 pairs: every full tile has 4,
+    // an expert's last tile ceil(rest / 32))
     if (tid < kMaxE) {
         const int c = tid < E ? cnt[tid] : 0;
         sc[tid] = c;
         st[tid] = (c + kTN - 1) / kTN;
-        sb[tid] = c / kTN + (c % kTN > kTN / 2 ? 1 : 0);
+        const int r = c % kTN, last = r ? (r + 31) / 32 - 1 : -1;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sq[q][tid] = (q == 3 ? c / kTN : 0) + (last == q ? 1 : 0);
     }
     __syncthreads();
     for (int o = 1; o < kMaxE; o <<= 1) {
-        int vc = 0, vt = 0, vb = 0;
+        int vc = 0, vt = 0, vq[4] = {0, 0, 0, 0};
         if (tid < kMaxE && tid >= o) {
             vc = sc[tid - o];
             vt = st[tid - o];
-            vb = sb[tid - o];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) vq[q] = sq[q][tid - o];
         }
         __syncthreads();
         if (tid < kMaxE) {
             sc[tid] += vc;
             st[tid] += vt;
-            sb[tid] += vb;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sq[q][tid] += vq[q];
         }
         __syncthreads();
     }
@@ -161,25 +166,34 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
         const int o = tid == 0 ? 0 : sc[tid - 1], to = tid == 0 ? 0 : st[tid - 1];
         off[tid] = o;
         toff[tid] = to;
-        boff[tid] = tid == 0 ? 0 : sb[tid - 1];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) qoff[q][tid] = tid == 0 ? 0 : sq[q][tid - 1];
         a.expert_off[tid] = o;
         a.tile_off[tid] = to;
     }
     __syncthreads();
     // one descriptor per N-tile the GEMMs may see ((P + kTN - 1) / kTN + E of
     // them): expert, first sorted position, pairs; none past the last.  The
-    // big tiles come first (expert order), then each expert's last tile when
-    // it has at most kTN / 2 pairs, so that the GEMMs' queues start the long
-    // work first.
+    // tiles are ordered by size class, 4 quarters first, then 3, 2, 1
+    // (experts in order within a class), so that the GEMMs, which deal
+    // their queues out forwards and backwards in turn, give the long work
+    // out first and even out each workgroup's total.
     const int nt_max = (P + kTN - 1) / kTN + E;
     for (int j = tid; j < nt_max; j += 1024) a.tile_desc[j] = PfTile{0, 0, 0, 0};
     __syncthreads();
     if (tid < E) {
-        const int big = sb[E - 1];
+        int base[4];
+        base[3] = 0;
+        base[2] = sq[3][E - 1];
+        base[1] = base[2] + sq[2][E - 1];
+        base[0] = base[1] + sq[1][E - 1];
         for (int j = 0; j < toff[tid + 1] - toff[tid]; ++j) {
             const int p0 = off[tid] + j * kTN;
             const int np = min(kTN, off[tid + 1] - p0);
-            const int at = np > kTN / 2 ? boff[tid] + j : big + (toff[tid] - boff[tid]);
+            const int q = (np + 31) / 32 - 1;
+            // full tiles of the expert first in its class-4 run, its last
+            // tile after them (class 4) or alone in its class
+            const int at = base[q] + qoff[q][tid] + (q == 3 ? j : 0);
             a.tile_desc[at] = PfTile{tid, p0, np, 0};
         }
     }
@@ -250,12 +264,13 @@ __device__ __forceinline__ float row_scale(uint32_t k) {
 // fixed per-lane offset (lane j of a B copy fetching the unit that belongs
 // at its position).
 //
-// Pipeline: three ring slots; block kb's copies are issued two blocks ahead
-// into slot kb % 3.  Before block kb is multiplied each wave waits until only
-// the copies of block kb + 1 are outstanding (memory loads complete in issue
-// order), then a barrier makes every wave's copies of block kb visible; the
-// slot of block kb - 1, read by every wave before that barrier, is then
-// refilled with block kb + 2.
+// Pipeline: NS ring slots (3 for tiles of 3 or 4 quarters, 4 for 2, 5 for
+// 1: the LDS of three full stages); block kb's copies are issued NS - 1
+// blocks ahead into slot kb % NS.  Before block kb is multiplied each wave
+// waits until only the copies of blocks kb + 1 .. kb + NS - 2 are
+// outstanding (memory loads complete in issue order), then a barrier makes
+// every wave's copies of block kb visible; the slot of block kb - 1, read by
+// every wave before that barrier, is then refilled with block kb + NS - 1.
 constexpr int kMK = 64;                       // k per block
 constexpr int kMA = 256 * kMK / 2;            // 8 KB of A
 constexpr int kMB = kTN * kMK * 2;            // 16 KB of B
@@ -265,6 +280,13 @@ constexpr int mma_sbytes() { return (GSL == 0 ? 2 : 1) * 256 * 4; }
 template <int GSL>
 constexpr int mma_stage() { return kMA + mma_sbytes<GSL>() + kMB; }
 constexpr int kMSlots = 3;
+// A tile of NQ quarters uses stages of NQ quarters of B, and as many of them
+// as the LDS of three full stages holds (3, 3, 4, 5 for NQ = 4, 3, 2, 1): a
+// narrow tile keeps more k-blocks of A in flight, which is what bounds it.
+template <int GSL, int NQ>
+constexpr int mma_stage_q() { return kMA + mma_sbytes<GSL>() + NQ * (kMB / 4); }
+template <int GSL, int NQ>
+constexpr int mma_slots() { return kMSlots * mma_stage<GSL>() / mma_stage_q<GSL, NQ>(); }
 
 // Copy sources (per block kb: base + kb * stride, plus the lane's offset) and
 // the lane's LDS read offsets within a stage.
@@ -329,7 +351,7 @@ constexpr int mma_ops() { return 2 + (GSL == 0 ? 2 : 1) + NQ; }
 template <int GSL, int NQ, int SLOT>
 __device__ __forceinline__ void mma_issue(const MmaSrc& src, int kb, int nblk, uint32_t ring) {
     kb = min(kb, nblk - 1);
-    const uint32_t st = ring + SLOT * mma_stage<GSL>();
+    const uint32_t st = ring + SLOT * mma_stage_q<GSL, NQ>();
     const uint8_t* ab = src.abase + (size_t)kb * src.chunk;
 #pragma unroll
     for (int i = 0; i < 2; ++i) lds_copy16(src.aoff[i], ab, st + (2 * src.wave + i) * 1024);
@@ -382,42 +404,59 @@ __device__ __forceinline__ void mma_compute(const MmaSrc& src, const uint8_t* ld
     }
 }
 
-// The k loop over the three ring slots of ring (unrolled by 3: every slot's
-// LDS offsets are constants).
+// Steps I .. NS - 1 of one round of the ring (every slot's LDS offsets are
+// constants).
+template <int I, int NS, class F>
+__device__ __forceinline__ void mma_round(int kb, F& step) {
+    if constexpr (I < NS) {
+        step(kb + I, std::integral_constant<int, I>{});
+        mma_round<I + 1, NS>(kb, step);
+    }
+}
+
+// The k loop over the NS = mma_slots ring slots of ring: blocks 0 .. NS - 2
+// are issued first; step kb waits for block kb (NS - 2 younger blocks may be
+// in flight), passes the barrier after which every wave is done with block
+// kb - 1's slot, issues block kb + NS - 1 into that slot and multiplies
+// block kb.
 template <int GSL, int NQ>
 __device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint8_t* ring,
                                          f32x16 (&acc)[2][4]) {
     constexpr int ops = mma_ops<GSL, NQ>();
-    constexpr int stage = mma_stage<GSL>();
+    constexpr int stage = mma_stage_q<GSL, NQ>();
+    constexpr int NS = mma_slots<GSL, NQ>();
+    static_assert(NS >= 3 && ops * (NS - 2) < 64, "ring depth");
     const uint32_t rl = lds_addr(ring);
-    mma_issue<GSL, NQ, 0>(src, 0, nblk, rl);
-    mma_issue<GSL, NQ, 1>(src, 1, nblk, rl);
+    auto first = [&](int kb, auto slot) {
+        constexpr int S = decltype(slot)::value;
+        if constexpr (S < NS - 1) mma_issue<GSL, NQ, S>(src, kb, nblk, rl);
+    };
+    mma_round<0, NS>(0, first);
     auto step = [&](int kb, auto slot) {
         constexpr int S = decltype(slot)::value;
         if (kb >= nblk) return;
-        wait_vm<ops>();  // block kb's copies are in (block kb + 1's may not be)
+        wait_vm<ops * (NS - 2)>();  // block kb's copies are in (the next NS - 2 may not be)
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        mma_issue<GSL, NQ, (S + 2) % 3>(src, kb + 2, nblk, rl);
+        mma_issue<GSL, NQ, (S + NS - 1) % NS>(src, kb + NS - 1, nblk, rl);
         __builtin_amdgcn_sched_barrier(0);
         mma_compute<GSL, NQ>(src, ring + S * stage, acc);
     };
-    for (int kb = 0; kb < nblk; kb += 3) {
-        step(kb, std::integral_constant<int, 0>{});
-        step(kb + 1, std::integral_constant<int, 1>{});
-        step(kb + 2, std::integral_constant<int, 2>{});
-    }
+    for (int kb = 0; kb < nblk; kb += NS) mma_round<0, NS>(kb, step);
     // no copy into LDS may still be in flight when the workgroup ends
     wait_vm<0>();
 }
 
 // Persistent: the workgroups of an XCD take the (N-tile, M-tile) items of
-// their queue in turn (workgroup j of the queue: items j, j + W, ... for W
-// workgroups on the queue).  Queue x (block id % 8, modulo the M-tile count
-// when there are fewer than 8 M-tiles) holds M-tiles x, x + 8, ... of every
-// N-tile, big N-tiles first and, per N-tile, its M-tiles in a row: the long
-// items start first, and the N-tiles of one expert run together on one XCD
-// and share the expert's A rows through its L2.
+// their queue in rounds of W (W workgroups on the queue), workgroup j taking
+// item j of the even rounds and item W - 1 - j of the odd ones.  Queue x
+// (block id % 8, modulo the M-tile count when there are fewer than 8
+// M-tiles) holds M-tiles x, x + 8, ... of every N-tile, the N-tiles by size
+// class (4 quarters of 32 pairs first, then 3, 2, 1) and, per N-tile, its
+// M-tiles in a row: the long items start first, every workgroup's total
+// work evens out (a large first item is followed by a small second one),
+// and the N-tiles of one expert run together on one XCD and share the
+// expert's A rows through its L2.
 template <int NMAT, int GSL>
 __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_tiles) {
     constexpr int TM = NMAT == 2 ? 128 : 256;
@@ -435,7 +474,12 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
     const int xcds = (8 - queue + nq - 1) / nq;               // block id residues on this queue
     const int per_queue = (int)(gridDim.x >> 3) * xcds;       // workgroups taking this queue
     const int first = (int)(blockIdx.x >> 3) * xcds + (int)(blockIdx.x & 7) / nq;
-    for (int item = first; item < items; item += per_queue) {
+    for (int r = 0;; ++r) {
+        // the queue is dealt out forwards in even rounds and backwards in odd
+        // ones: the workgroups that took the largest items of a round take
+        // the smallest of the next
+        const int item = r * per_queue + ((r & 1) ? per_queue - 1 - first : first);
+        if (item >= items) break;
         // every wave is done with the previous item's LDS before the next starts
         __syncthreads();
         const int mt = (item % n_mg) * nq + queue;

@@ -149,8 +149,10 @@ int enqueue_decode(m1moe_ctx_t ctx, const m1moe::FusedArgs& a) {
                           : m1moe::launch_moe_decode(a, ctx->stream);
 }
 
+// (xq / xinv: the prefill's f16 copy of x, made by the logits kernel, or null)
 int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
-                       int32_t x_dtype, int32_t* uidx, float* uw, float* ulogits) {
+                       int32_t x_dtype, int32_t* uidx, float* uw, float* ulogits,
+                       _Float16* xq = nullptr, float* xinv = nullptr) {
     const m1moe::Geom& g = ctx->g;
     m1moe::RouterArgs r{};
     r.router = ctx->routers + (uint64_t)layer * g.E * g.h;
@@ -169,6 +171,8 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
     r.user_w = uw;
     r.user_logits = ulogits;
     r.counters = ctx->counters;
+    r.xq = xq;
+    r.xinv = xinv;
     return launched(m1moe::launch_router_topk(r, ctx->stream), "router_topk");
 }
 
@@ -278,8 +282,6 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
     } else if ((rc = ensure_prefill_scratch(ctx, T))) {
         return rc;
     }
-    if ((rc = enqueue_router(ctx, layer, T, d_x, x_dtype, d_topk_idx, d_topk_w, nullptr)))
-        return rc;
     const m1moe::Geom& g = ctx->g;
     m1moe::PrefillArgs a{};
     a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
@@ -330,6 +332,9 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
     }
     a.err = ctx->err;
     a.cus = ctx->cus;
+    if ((rc = enqueue_router(ctx, layer, T, d_x, x_dtype, d_topk_idx, d_topk_w, nullptr, a.xq,
+                             a.xinv)))
+        return rc;
     return launched(m1moe::launch_prefill(a, ctx->stream),
                     use_static ? "moe_prefill_noalloc" : "moe_prefill");
 }

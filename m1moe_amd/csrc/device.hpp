@@ -202,6 +202,10 @@ __device__ __forceinline__ float bf16_pick(uint32_t w, uint32_t sel) {
     return __uint_as_float(__builtin_amdgcn_perm(w, w, sel));
 }
 
+// Position i of a permuted 8-column group holds column perm8(i):
+// 0, 4, 1, 5, 2, 6, 3, 7 (the column order of the prefill GEMM's A fragments).
+__host__ __device__ constexpr int perm8(int i) { return (i >> 1) | ((i & 1) << 2); }
+
 // Power-of-two scale that maps max|x| into [2^13, 2^14), so every scaled
 // input is a normal-range f16 with headroom (max f16 is 65504).
 __device__ __forceinline__ void pow2_scale(float maxabs, float& scale, float& inv) {

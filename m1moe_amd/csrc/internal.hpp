@@ -125,6 +125,8 @@ struct RouterArgs {
     float* user_w;
     float* user_logits;
     uint32_t* counters;          // [T] zero-initialised, self-resetting
+    _Float16* xq;                // optional: the prefill's f16 copy of x [T][h] and
+    float* xinv;                 // its per-token 2^-e (PrefillArgs xq / xinv)
 };
 
 // Per-expert prefill copy of an expert block, made on the device at upload

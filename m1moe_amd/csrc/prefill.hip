@@ -65,113 +65,103 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kTN = kPfTN;
 constexpr int kMaxE = 256;
 
-// Position i of a permuted 8-column group holds column perm8(i):
-// 0, 4, 1, 5, 2, 6, 3, 7.
-__host__ __device__ constexpr int perm8(int i) { return (i >> 1) | ((i & 1) << 2); }
-
-// ---- x: per-token power-of-two scale, f16 copy ----------------------------------
-
-// One workgroup per token; h <= 16384 (eight groups of 8 values per thread).
-__global__ __launch_bounds__(256) void prep_x_kernel(PrefillArgs a) {
-    __shared__ float s_max[4];
-    const int t = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float v[8][8];
-    float mx = 0.f;
-#pragma unroll
-    for (int it = 0; it < 8; ++it) {
-        const int d = (it * 256 + (int)threadIdx.x) * 8;
-        if (d < a.h) {
-            if (a.x_bf16) {
-                const uint4 q = *reinterpret_cast<const uint4*>(
-                    static_cast<const uint16_t*>(a.x) + (size_t)t * a.h + d);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[it][i] = bf16x8_at(q, i);
-            } else {
-                const float* xr = static_cast<const float*>(a.x) + (size_t)t * a.h + d;
-                const float4 q0 = *reinterpret_cast<const float4*>(xr);
-                const float4 q1 = *reinterpret_cast<const float4*>(xr + 4);
-                v[it][0] = q0.x; v[it][1] = q0.y; v[it][2] = q0.z; v[it][3] = q0.w;
-                v[it][4] = q1.x; v[it][5] = q1.y; v[it][6] = q1.z; v[it][7] = q1.w;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[it][i]));
-        }
-    }
-    mx = wave_max(mx);
-    if (lane == 0) s_max[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
-    float scale, inv;
-    pow2_scale(mx, scale, inv);
-#pragma unroll
-    for (int it = 0; it < 8; ++it) {
-        const int d = (it * 256 + (int)threadIdx.x) * 8;
-        if (d < a.h) {
-            // stored in the column order 0, 4, 1, 5, 2, 6, 3, 7 of the A fragments
-            f16x8 o;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = (_Float16)(v[it][perm8(i)] * scale);
-            *reinterpret_cast<f16x8*>(a.xq + (size_t)t * a.h + d) = o;
-        }
-    }
-    if (threadIdx.x == 0) a.xinv[t] = inv;
-}
 
 // ---- grouping of (token, slot) pairs by expert ----------------------------------
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+constexpr int kGP = 8;  // pairs per thread per pass of group_kernel
+
 // One workgroup.  Pair p = t*K + k gets the sorted position pos[p]; the order
 // of pairs within an expert is arbitrary (each pair's GEMM column is computed
-// independently of the others, so results do not depend on it).
+// independently of the others, so results do not depend on it).  A thread
+// takes kGP pairs per pass with all their loads in flight; when one pass
+// covers every pair (P <= 1024 kGP) their experts and ranks stay in
+// registers until the positions are written.  One wave computes the prefix
+// sums (4 experts per lane).
 __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
     __shared__ int cnt[kMaxE];
-    __shared__ int sc[kMaxE], st[kMaxE], sq[4][kMaxE];
-    __shared__ int off[kMaxE + 1], toff[kMaxE + 1], qoff[4][kMaxE + 1];
-    const int tid = threadIdx.x;
+    __shared__ int off[kMaxE + 1], toff[kMaxE + 1], qoff[4][kMaxE + 1], qtot[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, P = a.T * a.K;
     if (tid < kMaxE) cnt[tid] = 0;
     __syncthreads();
-    for (int p = tid; p < P; p += 1024) a.pos[p] = atomicAdd(&cnt[a.idx[p]], 1);
-    __syncthreads();
-    // inclusive scans of the pair and N-tile counts, and of the tiles of
-    // each size class (c + 1 quarters of 32 pairs: every full tile has 4,
-    // an expert's last tile ceil(rest / 32))
-    if (tid < kMaxE) {
-        const int c = tid < E ? cnt[tid] : 0;
-        sc[tid] = c;
-        st[tid] = (c + kTN - 1) / kTN;
-        const int r = c % kTN, last = r ? (r + 31) / 32 - 1 : -1;
+    const bool one_pass = P <= 1024 * kGP;
+    int pe[kGP], pr[kGP];
+    for (int base = 0; base < P; base += 1024 * kGP) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sq[q][tid] = (q == 3 ? c / kTN : 0) + (last == q ? 1 : 0);
-    }
-    __syncthreads();
-    for (int o = 1; o < kMaxE; o <<= 1) {
-        int vc = 0, vt = 0, vq[4] = {0, 0, 0, 0};
-        if (tid < kMaxE && tid >= o) {
-            vc = sc[tid - o];
-            vt = st[tid - o];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) vq[q] = sq[q][tid - o];
+        for (int j = 0; j < kGP; ++j) {
+            const int p = base + j * 1024 + tid;
+            pe[j] = p < P ? a.idx[p] : -1;
         }
-        __syncthreads();
-        if (tid < kMaxE) {
-            sc[tid] += vc;
-            st[tid] += vt;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sq[q][tid] += vq[q];
+        for (int j = 0; j < kGP; ++j) pr[j] = pe[j] >= 0 ? atomicAdd(&cnt[pe[j]], 1) : 0;
+        if (!one_pass) {
+#pragma unroll
+            for (int j = 0; j < kGP; ++j) {
+                const int p = base + j * 1024 + tid;
+                if (p < P) a.pos[p] = pr[j];
+            }
         }
-        __syncthreads();
-    }
-    if (tid <= E) {
-        const int o = tid == 0 ? 0 : sc[tid - 1], to = tid == 0 ? 0 : st[tid - 1];
-        off[tid] = o;
-        toff[tid] = to;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) qoff[q][tid] = tid == 0 ? 0 : sq[q][tid - 1];
-        a.expert_off[tid] = o;
-        a.tile_off[tid] = to;
     }
     __syncthreads();
+    // exclusive prefix sums of the pair and N-tile counts, and of the tiles of
+    // each size class (c + 1 quarters of 32 pairs: every full tile has 4, an
+    // expert's last tile ceil(rest / 32)); entry E holds the totals
+    if (wave == 0) {
+        int c[4], tl[4], qq[4][4];
+        int sc = 0, st = 0, sq[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = 4 * lane + j;
+            c[j] = i < E ? cnt[i] : 0;
+            tl[j] = (c[j] + kTN - 1) / kTN;
+            const int r = c[j] % kTN, last = r ? (r + 31) / 32 - 1 : -1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qq[k][j] = (k == 3 ? c[j] / kTN : 0) + (last == k ? 1 : 0);
+            sc += c[j];
+            st += tl[j];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) sq[k] += qq[k][j];
+        }
+        int ec = wave_incl_scan(sc, lane) - sc, et = wave_incl_scan(st, lane) - st, eq[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) eq[k] = wave_incl_scan(sq[k], lane) - sq[k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = 4 * lane + j;
+            if (i <= E) {
+                off[i] = ec;
+                toff[i] = et;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) qoff[k][i] = eq[k];
+                a.expert_off[i] = ec;
+                a.tile_off[i] = et;
+            }
+            ec += c[j];
+            et += tl[j];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) eq[k] += qq[k][j];
+        }
+        if (lane == 63) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qtot[k] = eq[k];
+            if (E == kMaxE) {  // entry E lies past the lanes' 4 x 64 experts
+                off[E] = ec;
+                toff[E] = et;
+                a.expert_off[E] = ec;
+                a.tile_off[E] = et;
+            }
+        }
+    }
     // one descriptor per N-tile the GEMMs may see ((P + kTN - 1) / kTN + E of
     // them): expert, first sorted position, pairs; none past the last.  The
     // tiles are ordered by size class, 4 quarters first, then 3, 2, 1
@@ -184,9 +174,9 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
     if (tid < E) {
         int base[4];
         base[3] = 0;
-        base[2] = sq[3][E - 1];
-        base[1] = base[2] + sq[2][E - 1];
-        base[0] = base[1] + sq[1][E - 1];
+        base[2] = qtot[3];
+        base[1] = base[2] + qtot[2];
+        base[0] = base[1] + qtot[1];
         for (int j = 0; j < toff[tid + 1] - toff[tid]; ++j) {
             const int p0 = off[tid] + j * kTN;
             const int np = min(kTN, off[tid + 1] - p0);
@@ -197,11 +187,24 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
             a.tile_desc[at] = PfTile{tid, p0, np, 0};
         }
     }
-    for (int p = tid; p < P; p += 1024) {
-        const int q = off[a.idx[p]] + a.pos[p];
-        const int t = p / a.K;
-        a.pos[p] = q;
-        a.sorted_tok[q] = PfPair{t, a.xinv[t]};
+    if (one_pass) {
+#pragma unroll
+        for (int j = 0; j < kGP; ++j) {
+            const int p = j * 1024 + tid;
+            if (p < P) {
+                const int q = off[pe[j]] + pr[j];
+                const int t = p / a.K;
+                a.pos[p] = q;
+                a.sorted_tok[q] = PfPair{t, a.xinv[t]};
+            }
+        }
+    } else {
+        for (int p = tid; p < P; p += 1024) {
+            const int q = off[a.idx[p]] + a.pos[p];
+            const int t = p / a.K;
+            a.pos[p] = q;
+            a.sorted_tok[q] = PfPair{t, a.xinv[t]};
+        }
     }
 }
 
@@ -805,11 +808,10 @@ int launch_pf_tile_copy(const uint8_t* layer, uint64_t expert_bytes, uint8_t* ds
 int launch_prefill(const PrefillArgs& a, void* stream) {
     if (a.E > kMaxE || a.h > 16384 || a.h % 64 || a.I % 64) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(prep_x_kernel, dim3((unsigned)a.T), dim3(256), 0, st, a);
+    // (x's f16 copy xq / xinv was made by the router's logits kernel)
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, st, a);
-    if ((e = hipGetLastError()) != hipSuccess) return (int)e;
     int rc;
     switch (a.gs) {
         case 32: rc = launch_gemms<0>(a, st); break;

@@ -7,7 +7,9 @@
 //   router_logits   logits[t][e] = sum_d W[e][d] * x[t][d]: a wave computes
 //                   4 tokens x 4 experts with its lanes across the columns
 //                   (coalesced 128-bit loads, all of a 2048-column row in
-//                   flight at once), a workgroup 4 tokens x 16 experts.
+//                   flight at once), a workgroup 4 tokens x 16 experts.  For
+//                   a prefill it also writes x's f16 copy (prep_token): wave
+//                   w of the workgroups of experts 0-15 takes token t0 + w.
 //                   Every product bf16 * x is exact in f64; each lane sums
 //                   its columns in f64, the lanes are added by a fixed DPP
 //                   tree, then one rounding to f32 (+ the optional logit
@@ -89,10 +91,61 @@ __device__ __forceinline__ void logits_wave(const RouterArgs& a, int t0, int e0,
     }
 }
 
+// The prefill's f16 copy of token t's x row (when a.xq is set): the row times
+// a per-token power of two that maps max|x| into [2^13, 2^14), each 8-column
+// group stored in the column order perm8 of the GEMM's A fragments, and the
+// inverse power in xinv[t].  One wave; h % 64 == 0.
+__device__ void prep_token(const RouterArgs& a, int t, int lane) {
+    if (t >= a.T) return;
+    const int units = a.h / 8;
+    auto load8 = [&](int u, float (&v)[8]) {
+        if (a.x_bf16) {
+            const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) +
+                                                            (size_t)t * a.h + 8 * u);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = bf16x8_at(q, i);
+        } else {
+            const float* xr = static_cast<const float*>(a.x) + (size_t)t * a.h + 8 * u;
+            const float4 q0 = *reinterpret_cast<const float4*>(xr);
+            const float4 q1 = *reinterpret_cast<const float4*>(xr + 4);
+            v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+            v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+        }
+    };
+    float mx = 0.f;
+    for (int u = lane; u < units; u += 64) {
+        float v[8];
+        load8(u, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+    }
+    mx = wave_max(mx);
+    float scale, inv;
+    pow2_scale(mx, scale, inv);
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    for (int u = lane; u < units; u += 64) {
+        float v[8];
+        load8(u, v);
+        h8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (_Float16)(v[perm8(i)] * scale);
+        *reinterpret_cast<h8*>(a.xq + (size_t)t * a.h + 8 * u) = o;
+    }
+    if (lane == 0) a.xinv[t] = inv;
+}
+
+static_assert(kTT == 4, "one wave of the 256-thread workgroup per token");
+
 __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kTT, e0 = blockIdx.y * kTE + wave * kTEw;
-    if (e0 >= a.E) return;
+    // wave w of the workgroups of expert block 0 also makes token t0 + w's
+    // f16 copy for the prefill (its rows are in L2 from the logits)
+    const bool prep = a.xq && blockIdx.y == 0;
+    if (e0 >= a.E) {
+        if (prep) prep_token(a, t0 + wave, lane);
+        return;
+    }
     double acc[kTT][kTEw];
 #pragma unroll
     for (int i = 0; i < kTT; ++i)
@@ -115,6 +168,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
                 if (a.user_logits) a.user_logits[(size_t)t * a.E + e] = l;
             }
         }
+    if (prep) prep_token(a, t0 + wave, lane);
 }
 
 // Orders this wave's LDS accesses before / after the call (lanes exchange

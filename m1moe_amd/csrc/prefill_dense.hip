@@ -8,10 +8,13 @@
 //   embed_rows     the token rows of the bf16 embedding -> f32 [T][h]
 //                  (InferenceEngine.swift:482-488)
 //   rmsnorm_rows   x * rsqrt(mean(x^2) + eps) * w per row (Shaders.metal:96-134)
-//   gemm_kernel    Y[T][N] = X[T][K] W[N][K]^T (+ R) on v_mfma_f32_16x16x4f32:
-//                  bf16 weights widened to f32 in LDS, f32 activations, f32
-//                  accumulation (the arithmetic of matvecBF16, Shaders.metal:
-//                  328-358, in another order)
+//   gemm_bf3       Y[T][N] = X[T][K] W[N][K]^T (+ R): f32 activations split
+//                  exactly into three bf16 parts, each multiplied with the
+//                  bf16 weights on v_mfma_f32_32x32x16_bf16 (exact products,
+//                  f32 accumulation: the arithmetic of matvecBF16,
+//                  Shaders.metal:328-358, in another order); gemm_kernel does
+//                  the same on v_mfma_f32_16x16x4f32 for a K that is not a
+//                  multiple of 64
 //   rope_kv_rows   per token and head: the per-head q/k RMSNorm and RoPE at
 //                  the token's position (InferenceEngine.swift:521-548), k and
 //                  v rows into the caches (:215-220)
@@ -267,6 +270,134 @@ __global__ __launch_bounds__(256) void attn_causal_kernel(PfDenseArgs a) {
 __global__ void advance_pos_kernel(int32_t* pos, int32_t by, int32_t max_seq) {
     *pos = min(*pos + by, max_seq);
 }
+// ---- GEMM on bf16 MFMA with the f32 input split three ways ---------------------------
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+
+// Y[M][N] = X[M][K] W[N][K]^T (+ R), X f32, W bf16.  Each x is split exactly
+// into three bf16 values, hi = x with the low 16 bits cleared, mid = (x - hi)
+// likewise, lo = x - hi - mid (x has 24 significant bits: 8 + 8 + 8), when the
+// X tile is staged in LDS; each part is multiplied with the bf16 weights on
+// v_mfma_f32_32x32x16_bf16, whose products are exact, and accumulated in f32:
+// the arithmetic of the f32 GEMM (exact products, f32 sums) at the bf16 rate.
+// Tile BM tokens x BN weight rows (128 x 128, 64 x 128 or 64 x 64), k-blocks
+// of 64; the next k-block's global loads are issued before the current one
+// is multiplied.  Four waves, each TI x TJ tiles of 32 x 32.  MFMA operands:
+// A = tokens (lane l: row l % 32, k 8 (l / 32) .. + 7), B = weight rows
+// likewise; D element 4 v + i of lane l is token 8 v + 4 (l / 32) + i, weight
+// row l % 32 of the tile.
+constexpr int kBK = 64, kBP = kBK + 8;  // LDS rows padded to 144 bytes
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256, 2) void gemm_bf3_kernel(GemmArgs g) {
+    constexpr int TI = BM == 128 ? 2 : (BN == 128 ? 2 : 1);
+    constexpr int TJ = BM == 128 ? 2 : 1;
+    constexpr int WN = BN / (32 * TJ);              // waves along the weight rows
+    static_assert((BM / (32 * TI)) * WN == 4, "four waves");
+    constexpr int EA = BM * kBK / 256;              // X values staged per thread (32 or 16)
+    constexpr int EW = BN * kBK / 256;              // W values staged per thread (32 or 16)
+    __shared__ __attribute__((aligned(16))) uint16_t sX[3][BM][kBP];
+    __shared__ __attribute__((aligned(16))) uint16_t sW[BN][kBP];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // loaders: X row xr, columns xc .. xc + EA - 1; W row wr, columns wc .. wc + EW - 1
+    const int xr = tid / (kBK / EA), xc = (tid % (kBK / EA)) * EA;
+    const int wr = tid / (kBK / EW), wc = (tid % (kBK / EW)) * EW;
+    const float* xrow = g.A + (size_t)min(m0 + xr, g.M - 1) * g.lda + xc;
+    const uint16_t* wrow = g.W + (size_t)min(n0 + wr, g.N - 1) * g.K + wc;
+    typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+    float4 xv[EA / 4];
+    u32x4v wv[EW / 8];
+    // hi / mid / lo parts of eight values, as bf16 bits packed two per word
+    auto split8 = [&](const float (&v)[8], uint4& h, uint4& m, uint4& l) {
+        uint32_t hb[8], mb[8], lb[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t u = __float_as_uint(v[e]);
+            const float hi = __uint_as_float(u & 0xffff0000u);
+            const float r = v[e] - hi;
+            const float mid = __uint_as_float(__float_as_uint(r) & 0xffff0000u);
+            const float lo = r - mid;
+            hb[e] = __float_as_uint(hi) >> 16;
+            mb[e] = __float_as_uint(mid) >> 16;
+            lb[e] = __float_as_uint(lo) >> 16;
+        }
+        h = make_uint4(hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16);
+        m = make_uint4(mb[0] | mb[1] << 16, mb[2] | mb[3] << 16, mb[4] | mb[5] << 16, mb[6] | mb[7] << 16);
+        l = make_uint4(lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16);
+    };
+    f32x16v acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const int wm = (wave / WN) * 32 * TI, wn = (wave % WN) * 32 * TJ;
+    const int r32 = lane & 31, k8 = (lane >> 5) * 8;
+#pragma unroll
+    for (int i = 0; i < EA / 4; ++i) xv[i] = *reinterpret_cast<const float4*>(xrow + 4 * i);
+#pragma unroll
+    for (int i = 0; i < EW / 8; ++i) wv[i] = *reinterpret_cast<const u32x4v*>(wrow + 8 * i);
+    for (int k0 = 0; k0 < g.K; k0 += kBK) {
+#pragma unroll
+        for (int c = 0; c < EA / 8; ++c) {
+            float v[8];
+            v[0] = xv[2 * c].x, v[1] = xv[2 * c].y, v[2] = xv[2 * c].z, v[3] = xv[2 * c].w;
+            v[4] = xv[2 * c + 1].x, v[5] = xv[2 * c + 1].y, v[6] = xv[2 * c + 1].z, v[7] = xv[2 * c + 1].w;
+            uint4 h, m, l;
+            split8(v, h, m, l);
+            *reinterpret_cast<uint4*>(&sX[0][xr][xc + 8 * c]) = h;
+            *reinterpret_cast<uint4*>(&sX[1][xr][xc + 8 * c]) = m;
+            *reinterpret_cast<uint4*>(&sX[2][xr][xc + 8 * c]) = l;
+        }
+#pragma unroll
+        for (int c = 0; c < EW / 8; ++c) *reinterpret_cast<u32x4v*>(&sW[wr][wc + 8 * c]) = wv[c];
+        __syncthreads();
+        if (k0 + kBK < g.K) {
+            const int k1 = k0 + kBK;
+#pragma unroll
+            for (int i = 0; i < EA / 4; ++i) xv[i] = *reinterpret_cast<const float4*>(xrow + k1 + 4 * i);
+#pragma unroll
+            for (int i = 0; i < EW / 8; ++i) wv[i] = *reinterpret_cast<const u32x4v*>(wrow + k1 + 8 * i);
+        }
+#pragma unroll
+        for (int ks = 0; ks < kBK; ks += 16) {
+            bf16x8 b[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                b[j] = *reinterpret_cast<const bf16x8*>(&sW[wn + 32 * j + r32][ks + k8]);
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sX[p][wm + 32 * i + r32][ks + k8]);
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], acc[i][j], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int n = n0 + wn + 32 * j + r32;
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + wm + 32 * i + 8 * v + 4 * (lane >> 5) + r;
+                    if (m < g.M && n < g.N) {
+                        float y = acc[i][j][4 * v + r];
+                        if (g.R) y += g.R[(size_t)m * g.ldc + n];
+                        g.C[(size_t)m * g.ldc + n] = y;
+                    }
+                }
+        }
+}
 
 }  // namespace
 
@@ -284,8 +415,24 @@ int launch_rmsnorm_rows(const float* x, const uint16_t* w, float* out, int rows,
 
 int launch_gemm(const GemmArgs& g, void* stream) {
     if (g.K % kGK || g.M <= 0 || g.N <= 0 || g.lda % 4) return (int)hipErrorInvalidValue;
-    const dim3 grid((unsigned)((g.N + kGN - 1) / kGN), (unsigned)((g.M + kGM - 1) / kGM));
-    hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), g);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (g.K % kBK) {  // f32 MFMA for a K that is not a multiple of 64
+        const dim3 grid((unsigned)((g.N + kGN - 1) / kGN), (unsigned)((g.M + kGM - 1) / kGM));
+        hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), 0, st, g);
+        return (int)hipGetLastError();
+    }
+    // the largest tile that still gives at least one workgroup per CU
+    const long gm128 = (g.M + 127) / 128, gm64 = (g.M + 63) / 64;
+    const long gn128 = (g.N + 127) / 128, gn64 = (g.N + 63) / 64;
+    if (gn128 * gm128 >= 256)
+        hipLaunchKernelGGL((gemm_bf3_kernel<128, 128>), dim3((unsigned)gn128, (unsigned)gm128),
+                           dim3(256), 0, st, g);
+    else if (gn128 * gm64 >= 256)
+        hipLaunchKernelGGL((gemm_bf3_kernel<64, 128>), dim3((unsigned)gn128, (unsigned)gm64),
+                           dim3(256), 0, st, g);
+    else
+        hipLaunchKernelGGL((gemm_bf3_kernel<64, 64>), dim3((unsigned)gn64, (unsigned)gm64), dim3(256),
+                           0, st, g);
     return (int)hipGetLastError();
 }
 

@@ -82,6 +82,7 @@ struct m1moe_dec {
     // prefill scratch for up to pf_cap tokens (grown on demand)
     int32_t pf_cap = 0;
     float *pf_res = nullptr, *pf_res2 = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr;
+    float* pf_part = nullptr;  // split-K partials of the prefill GEMMs (kGemmPartFloats)
     uint32_t* cnt = nullptr;   // [2 + num_heads]: (unused), lm_head, attention groups
     float* ssq = nullptr;      // o_proj's per-workgroup sums of squares
     float* am_val = nullptr;   // lm_head's per-workgroup best logit
@@ -226,7 +227,7 @@ void m1moe_dec_destroy(m1moe_dec_t dec) {
     (void)hipSetDevice(dec->device);
     for (void* p : dec->allocs) (void)hipFree(p);
     for (void* p : {(void*)dec->pf_res, (void*)dec->pf_res2, (void*)dec->pf_xn, (void*)dec->pf_qkv,
-                    (void*)dec->pf_attn})
+                    (void*)dec->pf_attn, (void*)dec->pf_part})
         if (p) (void)hipFree(p);
     delete dec;
 }
@@ -519,7 +520,7 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
     if (T > dec->pf_cap) {
         if ((rc = refuse_growth_in_capture(ctx->stream, "the decoder prefill scratch"))) return rc;
         HIP_TRY(hipStreamSynchronize(ctx->stream));
-        for (float** b : {&dec->pf_res, &dec->pf_res2, &dec->pf_xn, &dec->pf_qkv, &dec->pf_attn}) {
+        for (float** b : {&dec->pf_res, &dec->pf_res2, &dec->pf_xn, &dec->pf_qkv, &dec->pf_attn, &dec->pf_part}) {
             if (*b) (void)hipFree(*b);
             *b = nullptr;
         }
@@ -529,7 +530,8 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
             (rc = device_alloc((void**)&dec->pf_res2, t * h * 4, "prefill residual 2")) ||
             (rc = device_alloc((void**)&dec->pf_xn, t * h * 4, "prefill normed rows")) ||
             (rc = device_alloc((void**)&dec->pf_qkv, t * N * 4, "prefill q/k/v")) ||
-            (rc = device_alloc((void**)&dec->pf_attn, t * qd * 4, "prefill attention")))
+            (rc = device_alloc((void**)&dec->pf_attn, t * qd * 4, "prefill attention")) ||
+            (rc = device_alloc((void**)&dec->pf_part, kGemmPartFloats * 4, "prefill split-K partials")))
             return rc;
         dec->pf_cap = T;
     }
@@ -570,6 +572,7 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
         g.M = T;
         g.N = n;
         g.K = k;
+        g.part = dec->pf_part;
         return launched(launch_gemm(g, st), what);
     };
     if ((rc = launched(launch_pf_embed(a, st), "prefill embedding"))) return rc;  // :129-131

@@ -339,7 +339,12 @@ struct GemmArgs {
     float* C;
     int32_t ldc;
     int32_t M, N, K;
+    // split-K workspace ([S][M][N] f32 partials, summed in order s = 0 .. S-1)
+    // or null; with it a GEMM whose tiles leave the CUs idle splits its k range
+    float* part;
+    int32_t splits;              // set by launch_gemm
 };
+constexpr int64_t kGemmPartFloats = 512LL * 64 * 64;  // the workspace launch_gemm may use
 
 // The T prompt tokens of a decoder prefill at positions *pos .. *pos + T - 1.
 struct PfDenseArgs {

@@ -336,11 +336,14 @@ __global__ __launch_bounds__(256, 2) void gemm_bf3_kernel(GemmArgs g) {
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
     const int wm = (wave / WN) * 32 * TI, wn = (wave % WN) * 32 * TJ;
     const int r32 = lane & 31, k8 = (lane >> 5) * 8;
+    // this workgroup's k range: split blockIdx.z of gridDim.z, whole k-blocks
+    const int nkb = g.K / kBK, S = (int)gridDim.z, z = (int)blockIdx.z;
+    const int kbeg = (z * nkb / S) * kBK, kend = ((z + 1) * nkb / S) * kBK;
 #pragma unroll
-    for (int i = 0; i < EA / 4; ++i) xv[i] = *reinterpret_cast<const float4*>(xrow + 4 * i);
+    for (int i = 0; i < EA / 4; ++i) xv[i] = *reinterpret_cast<const float4*>(xrow + kbeg + 4 * i);
 #pragma unroll
-    for (int i = 0; i < EW / 8; ++i) wv[i] = *reinterpret_cast<const u32x4v*>(wrow + 8 * i);
-    for (int k0 = 0; k0 < g.K; k0 += kBK) {
+    for (int i = 0; i < EW / 8; ++i) wv[i] = *reinterpret_cast<const u32x4v*>(wrow + kbeg + 8 * i);
+    for (int k0 = kbeg; k0 < kend; k0 += kBK) {
 #pragma unroll
         for (int c = 0; c < EA / 8; ++c) {
             float v[8];
@@ -355,7 +358,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf3_kernel(GemmArgs g) {
 #pragma unroll
         for (int c = 0; c < EW / 8; ++c) *reinterpret_cast<u32x4v*>(&sW[wr][wc + 8 * c]) = wv[c];
         __syncthreads();
-        if (k0 + kBK < g.K) {
+        if (k0 + kBK < kend) {
             const int k1 = k0 + kBK;
 #pragma unroll
             for (int i = 0; i < EA / 4; ++i) xv[i] = *reinterpret_cast<const float4*>(xrow + k1 + 4 * i);
@@ -392,11 +395,35 @@ __global__ __launch_bounds__(256, 2) void gemm_bf3_kernel(GemmArgs g) {
                     const int m = m0 + wm + 32 * i + 8 * v + 4 * (lane >> 5) + r;
                     if (m < g.M && n < g.N) {
                         float y = acc[i][j][4 * v + r];
-                        if (g.R) y += g.R[(size_t)m * g.ldc + n];
-                        g.C[(size_t)m * g.ldc + n] = y;
+                        if (S > 1) {
+                            g.part[((size_t)z * g.M + m) * g.N + n] = y;
+                        } else {
+                            if (g.R) y += g.R[(size_t)m * g.ldc + n];
+                            g.C[(size_t)m * g.ldc + n] = y;
+                        }
                     }
                 }
         }
+}
+
+// C = sum over s = 0 .. S-1 of the split-K partials (in that order) + R; four
+// columns per thread (N, ldc and the C / R addresses are multiples of 4).
+__global__ __launch_bounds__(256) void splitk_sum_kernel(GemmArgs g) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t mn4 = (size_t)g.M * g.N / 4;
+    if (i >= mn4) return;
+    const float4* p = reinterpret_cast<const float4*>(g.part);
+    float4 y = p[i];
+    for (int z = 1; z < g.splits; ++z) {
+        const float4 q = p[(size_t)z * mn4 + i];
+        y.x += q.x, y.y += q.y, y.z += q.z, y.w += q.w;
+    }
+    const size_t m = 4 * i / g.N, n = 4 * i % g.N;
+    if (g.R) {
+        const float4 r = *reinterpret_cast<const float4*>(g.R + m * g.ldc + n);
+        y.x += r.x, y.y += r.y, y.z += r.z, y.w += r.w;
+    }
+    *reinterpret_cast<float4*>(g.C + m * g.ldc + n) = y;
 }
 
 }  // namespace
@@ -430,9 +457,24 @@ int launch_gemm(const GemmArgs& g, void* stream) {
     else if (gn128 * gm64 >= 256)
         hipLaunchKernelGGL((gemm_bf3_kernel<64, 128>), dim3((unsigned)gn128, (unsigned)gm64),
                            dim3(256), 0, st, g);
-    else
-        hipLaunchKernelGGL((gemm_bf3_kernel<64, 64>), dim3((unsigned)gn64, (unsigned)gm64), dim3(256),
-                           0, st, g);
+    else {
+        // Too few 64 x 64 tiles to fill the chip: split the k-blocks over
+        // gridDim.z (at least 4 per split, at most 512 workgroups in all) and
+        // sum the partials in a fixed order, so results do not depend on timing.
+        const long tiles = gn64 * gm64, nkb = g.K / kBK;
+        long S = 512 / tiles < nkb / 4 ? 512 / tiles : nkb / 4;
+        const bool aligned = g.N % 4 == 0 && g.ldc % 4 == 0 && (uintptr_t)g.C % 16 == 0 &&
+                             (uintptr_t)g.R % 16 == 0;
+        if (!g.part || !aligned || S < 2 || S * g.M * g.N > kGemmPartFloats) S = 1;
+        GemmArgs gs = g;
+        gs.splits = (int32_t)S;
+        hipLaunchKernelGGL((gemm_bf3_kernel<64, 64>), dim3((unsigned)gn64, (unsigned)gm64, (unsigned)S),
+                           dim3(256), 0, st, gs);
+        if (S > 1) {
+            const size_t mn4 = (size_t)g.M * g.N / 4;
+            hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)((mn4 + 255) / 256)), dim3(256), 0, st, gs);
+        }
+    }
     return (int)hipGetLastError();
 }
 

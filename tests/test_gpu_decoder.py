@@ -384,6 +384,31 @@ def test_prefill_dense_path_is_tight(Ts):
         p.close()
 
 
+def test_prefill_split_k_gemms_are_tight():
+    """OLMoE widths (h = q = kv = 2048), one layer, MoE block zeroed: a
+    100-token prefill gives each q/k/v/o_proj GEMM 64 tiles of 64 x 64, split
+    over 8 shares of 4 of its 32 k-blocks; a second 170-token prefill gives
+    96 tiles, 5 shares of 6-7 k-blocks.  The partials are summed in a fixed
+    order with the residual; last logits against the oracle's token-by-token
+    run to relative L2 1e-5."""
+    p = Pair(synth.DECODERS["cfg1"], seed=53, max_seq=280, num_layers=1, nthreads=8)
+    try:
+        _zero_experts(p)
+        toks = synth.prompt_tokens(p.wl, 23, 270)
+        off = 0
+        for T in (100, 170):
+            say(f"olmoe-width split-K prefill T={T} at position {off}")
+            g_tok, g_lg = p.dec.prefill(toks[off:off + T], return_logits=True)
+            for t in toks[off:off + T]:
+                w_tok, w_lg = p.orc.step(int(t))
+            off += T
+            rel = rel_l2(g_lg, w_lg)
+            assert rel < 1e-5, f"T={T}: rel L2 {rel:.2e}"
+            assert p.dec.position() == off
+    finally:
+        p.close()
+
+
 def test_prefill_longer_than_one_piece():
     """A 4100-token prompt goes through m1moe_dec_prefill in two pieces (4096
     + 4): last logits against the oracle's token-by-token run to 1e-5 (MoE

@@ -143,10 +143,12 @@ def main() -> int:
                     help="timed steps (default 200; cfg1: 5 jobs, cfg4: 1 job)")
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps (default 20; cfg1/cfg4: 1 job)")
-    ap.add_argument("--config", default="cfg0", choices=["cfg0", "cfg1", "cfg2", "cfg3", "cfg4"],
+    ap.add_argument("--config", default="cfg0",
+                    choices=["cfg0", "cfg1", "cfg2", "cfg3", "cfg4", "quant", "tokenizer"],
                     help="cfg0/cfg2: MoE-layer batch-1 decode; cfg3: 512-token MoE prefill; "
                          "cfg1/cfg4: whole decoder, prompt then greedy steps (a step is one "
-                         "such job)")
+                         "such job); quant / tokenizer: the host rows (converter's 4-bit "
+                         "quantizer over one OLMoE layer, BPE encode), no GPU")
     ap.add_argument("--replicas", type=int, default=0,
                     help="distinct layer replicas (default: >= 1 GiB of selected experts per pass)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
@@ -160,7 +162,8 @@ def main() -> int:
                     help="only run device-to-device copies of BYTES bytes (to scale HBM "
                          "byte counters against a plain copy of known size), then exit")
     args = ap.parse_args()
-    job_defaults = {"cfg1": (5, 1), "cfg4": (1, 1)}.get(args.config, (200, 20))
+    job_defaults = {"cfg1": (5, 1), "cfg4": (1, 1), "quant": (3, 1),
+                    "tokenizer": (3, 1)}.get(args.config, (200, 20))
     if args.steps is None:
         args.steps = job_defaults[0]
     if args.warmup is None:
@@ -179,6 +182,10 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration(m, args.copy_calibration, max(1, args.steps))
 
+    if args.config == "quant":
+        return bench_quant(args, m, synth)
+    if args.config == "tokenizer":
+        return bench_tokenizer(args, m)
     if args.config == "cfg3":
         return bench_prefill(args, m, synth)
     if args.config in ("cfg1", "cfg4"):
@@ -622,6 +629,171 @@ def bench_prefill(args, m, synth) -> int:
     }
     print(json.dumps(line), flush=True)
     ctx.close()
+    return 0
+
+
+def bench_quant(args, m, synth) -> int:
+    """The converters' quantizer (extract_olmoe.py:116-159, quantize_4bit per
+    expert matrix, then the expert block layout) over one OLMoE layer: 64
+    experts of f32 gate [1024, 2048], up [1024, 2048], down [2048, 1024] to the
+    packed layer image, on the host's threads.  A step = one layer.  Eight
+    distinct seeded experts are cycled (the work does not depend on the
+    values).  CPU baseline: the numpy restatement (oracle/quant_oracle.py)
+    on a bounded number of experts, one thread."""
+    from m1moe_amd import quant
+    from oracle import quant_oracle as qo
+
+    shape = synth.CONFIGS["cfg0"].shape(1)
+    h, inter, E = shape.hidden, shape.intermediate, shape.num_experts
+    rng = np.random.default_rng(args.seed)
+    experts = [tuple((rng.standard_normal(s, dtype=np.float32) * 0.02)
+                     for s in ((inter, h), (inter, h), (h, inter))) for _ in range(8)]
+    eb = m.expert_bytes(shape)
+    image = np.empty((E, eb), np.uint8)
+    nt = cpu_threads()
+    f32_bytes = E * 3 * inter * h * 4
+
+    def layer():
+        for e in range(E):
+            image[e] = quant.quantize_expert(shape, *experts[e % 8], threads=nt)
+
+    for _ in range(args.warmup):
+        layer()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        layer()
+    dt = (time.perf_counter() - t0) / args.steps
+    want = qo.expert_block(*experts[0], shape.group_size)
+    exact = bool(np.array_equal(image[0], want) and np.array_equal(image[8], want))
+    log(f"quantizer: {dt * 1e3:.1f} ms per layer, {f32_bytes / dt / 1e9:.2f} GB/s of f32 "
+        f"input on {nt} threads; expert blocks equal to the oracle's: {exact}")
+    cpu = None
+    if args.cpu_seconds > 0:
+        n, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_seconds and n < E:
+            t1 = time.perf_counter()
+            qo.expert_block(*experts[n % 8], shape.group_size)
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        cpu = {"value": round(n / t_cpu / E, 4), "unit": "layers/s", "cores": 1, "kind": "port",
+               "sample": f"{n} of the 64 experts through the numpy restatement "
+                         f"(oracle/quant_oracle.py) on 1 thread ({t_cpu:.1f}s); "
+                         f"host CPU: {cpu_model()}"}
+        log(f"cpu baseline: {cpu['value']} layers/s")
+    print(json.dumps({
+        "metric": "4-bit group-64 quantization of one OLMoE layer's experts (host)",
+        "value": round(1.0 / dt, 3), "unit": "layers/s", "n_gpus": 0, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True,
+        "scaling": "strong", "vs_baseline": None, "dtype": "f32 -> u4 + bf16 scale/bias",
+        "data": "synthetic (seeded N(0, 0.02) expert matrices)",
+        "config": {"workload": "OLMoE layer: 64 experts x (gate, up [1024, 2048], down "
+                               "[2048, 1024]), group 64", "threads": nt},
+        "roofline": None, "host_gbs_of_f32_input": round(f32_bytes / dt / 1e9, 2),
+        "cpu_baseline": cpu, "parity": {"expert_blocks_equal_oracle": exact}}), flush=True)
+    return 0
+
+
+def _bench_corpus(seed: int, lines: int):
+    """Seeded lines of syllable words, English-like words, digits and
+    punctuation, some non-ASCII."""
+    syl = ["ex", "per", "rout", "er", "to", "ken", "mo", "del", "la", "yer", "in", "ter", "ca",
+           "ti", "on", "ma", "tri", "x", "gra", "ph", "é", "ü", "東", "京", "σ", "λ"]
+    rng = np.random.default_rng(seed)
+    words = ["".join(syl[int(j)] for j in rng.integers(0, len(syl), int(rng.integers(1, 5))))
+             for _ in range(3000)] + ["the", "of", "and", "a", "to", "is", "2024", "3.14", "--"]
+    out = []
+    for _ in range(lines):
+        k = int(rng.integers(3, 20))
+        w = [words[int(i)] for i in rng.integers(0, len(words), k)]
+        out.append(" ".join(w) + rng.choice([".", ",", "!", "?", ":", ""]))
+    return out
+
+
+def bench_tokenizer(args, m) -> int:
+    """BPE encode (Tokenizer.swift:34-259) of a seeded synthetic text with
+    vocabularies trained here by the HuggingFace `tokenizers` library: GPT-2
+    byte-level (OLMoE) and SentencePiece with byte fallback (Mixtral), 8000
+    tokens each.  A step = encoding the whole text (4 MiB) with each; one
+    thread, as the reference.  CPU baseline: the pure-Python restatement
+    (oracle/tokenizer_oracle.py) on a bounded prefix."""
+    import tempfile
+
+    import tokenizers
+    from tokenizers import models, pre_tokenizers, trainers
+
+    from m1moe_amd.tokenizer import Tokenizer
+    from oracle.tokenizer_oracle import OracleTokenizer
+
+    corpus = _bench_corpus(args.seed, 20000)
+    text = "\n".join(_bench_corpus(args.seed + 1, 60000))
+    text = text.encode("utf-8")[:4 << 20].decode("utf-8", "ignore")
+    nbytes = len(text.encode("utf-8"))
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        for mode in ("byte_level", "sentencepiece"):
+            if mode == "byte_level":
+                hf = tokenizers.Tokenizer(models.BPE())
+                hf.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False)
+                tr = trainers.BpeTrainer(vocab_size=8000, show_progress=False,
+                                         initial_alphabet=pre_tokenizers.ByteLevel.alphabet(),
+                                         special_tokens=["<|endoftext|>"])
+            else:
+                hf = tokenizers.Tokenizer(models.BPE(byte_fallback=True, unk_token="<unk>"))
+                hf.pre_tokenizer = pre_tokenizers.Metaspace(replacement="\u2581",
+                                                            prepend_scheme="always")
+                specials = ["<unk>", "<s>", "</s>"] + ["<0x%02X>" % b for b in range(256)]
+                tr = trainers.BpeTrainer(vocab_size=8000, special_tokens=specials,
+                                         show_progress=False)
+            hf.train_from_iterator(corpus, tr)
+            js = json.loads(hf.to_str())
+            js["model"]["merges"] = [" ".join(p) if isinstance(p, list) else p
+                                     for p in js["model"]["merges"]]
+            js["model"]["byte_fallback"] = mode == "sentencepiece"
+            path = os.path.join(d, f"{mode}.json")
+            with open(path, "w", encoding="utf-8") as f:
+                json.dump(js, f)
+            tok = Tokenizer(path)
+            for _ in range(args.warmup):
+                ids = tok.encode(text, add_bos=False)
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                ids = tok.encode(text, add_bos=False)
+            dt = (time.perf_counter() - t0) / args.steps
+            orc = OracleTokenizer(path)
+            n, t_cpu, same = 0, 0.0, True
+            pieces = text.split("\n")
+            while n < len(pieces) and (t_cpu < max(args.cpu_seconds, 0.5) / 2):
+                t1 = time.perf_counter()
+                want = orc.encode(pieces[n], add_bos=False)
+                t_cpu += time.perf_counter() - t1
+                same = same and want == tok.encode(pieces[n], add_bos=False)
+                n += 1
+            sample = sum(len(p.encode("utf-8")) + 1 for p in pieces[:n])
+            res[mode] = {"mib_s": nbytes / dt / 2**20, "tokens": len(ids),
+                         "oracle_mib_s": sample / t_cpu / 2**20, "oracle_lines": n,
+                         "oracle_s": t_cpu, "lines_equal_oracle": same}
+            log(f"{mode}: {nbytes / dt / 2**20:.2f} MiB/s ({len(ids)} tokens); oracle "
+                f"{res[mode]['oracle_mib_s']:.3f} MiB/s on {n} lines, equal: {same}")
+            tok.close()
+    bl = res["byte_level"]
+    print(json.dumps({
+        "metric": "BPE encode throughput, byte-level (OLMoE) vocabulary (host, one thread)",
+        "value": round(bl["mib_s"], 3), "unit": "MiB/s", "n_gpus": 0, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(nbytes / bl["mib_s"] / 2**20 * 1e3, 3),
+        "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "u8 text",
+        "data": "synthetic (seeded syllable-word text; vocabularies trained here)",
+        "config": {"workload": "4 MiB of text, 8000-token BPE vocabularies", "bytes": nbytes},
+        "roofline": None,
+        "sentencepiece_mib_s": round(res["sentencepiece"]["mib_s"], 3),
+        "cpu_baseline": {"value": round(bl["oracle_mib_s"], 4), "unit": "MiB/s", "cores": 1,
+                         "kind": "port",
+                         "sample": f"the first {bl['oracle_lines']} lines through the "
+                                   f"pure-Python restatement (oracle/tokenizer_oracle.py), "
+                                   f"{bl['oracle_s']:.1f}s; host CPU: {cpu_model()}"},
+        "cpu_baseline_sentencepiece": round(res["sentencepiece"]["oracle_mib_s"], 4),
+        "parity": {"byte_level_lines_equal_oracle": bl["lines_equal_oracle"],
+                   "sentencepiece_lines_equal_oracle":
+                       res["sentencepiece"]["lines_equal_oracle"]}}), flush=True)
     return 0
 
 

@@ -41,18 +41,43 @@ int64_t quantize_rows(const float* w, int64_t r0, int64_t r1, int64_t cols, int3
         const float* row = w + r * cols;
         for (int64_t g = 0; g < ng; ++g) {
             const float* v = row + g * gs;
-            float lo = v[0], hi = v[0];
-            for (int32_t i = 0; i < gs; ++i) {
-                if (!std::isfinite(v[i])) return r;
-                lo = v[i] < lo ? v[i] : lo;
-                hi = v[i] > hi ? v[i] : hi;
+            // min, max and a finiteness check in eight independent lanes (so
+            // the loop vectorizes): x * 0 is 0 for a finite x and NaN for an
+            // infinite or NaN one, so chk ends 0 or NaN
+            float lo8[8], hi8[8], chk8[8];
+            for (int j = 0; j < 8; ++j) lo8[j] = hi8[j] = v[0], chk8[j] = 0.f;
+            const int32_t g8 = gs - gs % 8;
+            for (int32_t i = 0; i < g8; i += 8)
+                for (int j = 0; j < 8; ++j) {
+                    const float x = v[i + j];
+                    lo8[j] = x < lo8[j] ? x : lo8[j];
+                    hi8[j] = x > hi8[j] ? x : hi8[j];
+                    chk8[j] += x * 0.f;
+                }
+            for (int32_t i = g8; i < gs; ++i) {
+                lo8[0] = v[i] < lo8[0] ? v[i] : lo8[0];
+                hi8[0] = v[i] > hi8[0] ? v[i] : hi8[0];
+                chk8[0] += v[i] * 0.f;
             }
+            float lo = lo8[0], hi = hi8[0], chk = chk8[0];
+            for (int j = 1; j < 8; ++j) {
+                lo = lo8[j] < lo ? lo8[j] : lo;
+                hi = hi8[j] > hi ? hi8[j] : hi;
+                chk += chk8[j];
+            }
+            if (!(chk == 0.f)) return r;
             float s = (hi - lo) / 15.0f;
             if (s == 0.0f) s = 1.0f;
+            uint8_t* qg = q.data() + g * gs;
             for (int32_t i = 0; i < gs; ++i) {
-                // nearbyint rounds half to even in the default rounding mode
-                const float t = std::nearbyint((v[i] - lo) / s);
-                q[(size_t)(g * gs + i)] = (uint8_t)(t < 0.f ? 0.f : t > 15.f ? 15.f : t);
+                // t >= 0; adding and taking away 1.5 * 2^23 rounds it to an
+                // integer half to even (the default rounding mode) for t < 2^22,
+                // as nearbyint; larger values clamp to 15 either way
+                float t = (v[i] - lo) / s;
+                t = (t + 12582912.0f) - 12582912.0f;
+                t = t > 0.f ? t : 0.f;  // (NaN from an overflowed range: 0)
+                t = t < 15.f ? t : 15.f;
+                qg[i] = (uint8_t)(int32_t)t;
             }
             scales[r * ng + g] = bf16_rne(s);
             biases[r * ng + g] = bf16_rne(lo);

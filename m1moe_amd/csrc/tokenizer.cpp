@@ -49,9 +49,20 @@ struct m1moe_tokenizer {
     std::unordered_map<std::string, uint32_t> vocab;
     std::unordered_map<uint32_t, std::string> piece_of;
     std::unordered_map<std::string, int32_t> rank;  // key: a + '\xff' + b
+    // The same merges on interned symbols (every vocab piece, merge part and
+    // merge result has an id): (a, b) -> (rank, id of a + b), so the BPE loop
+    // compares integers; built once after loading.
+    std::unordered_map<std::string, int32_t> sym;
+    std::vector<std::string> sym_str;
+    std::vector<int64_t> sym_vocab;                              // vocab id or -1
+    std::unordered_map<uint64_t, std::pair<int32_t, int32_t>> pair;
+    int32_t byte_sym[256];     // byte-level: the symbol of each byte's table piece
+    int64_t fallback_id[256];  // SentencePiece: the vocab id of "<0xHH>" or -1
 };
 
 namespace {
+
+void build_symbols(m1moe_tokenizer& t);
 
 // ---- UTF-8 -----------------------------------------------------------------
 
@@ -383,77 +394,153 @@ int32_t parse(const std::string& text, m1moe_tokenizer* t) {
         // byte-wise smaller piece so the choice does not depend on hashing
         if (it == t->piece_of.end() || kv.first < it->second) t->piece_of[kv.second] = kv.first;
     }
+    build_symbols(*t);
     return M1MOE_OK;
 }
 
 // ---- BPE (Tokenizer.swift:212-228) ------------------------------------------
 
-void apply_bpe(const m1moe_tokenizer& t, std::vector<std::string>& syms) {
-    std::string key;
+int32_t intern(m1moe_tokenizer& t, const std::string& p) {
+    auto it = t.sym.find(p);
+    if (it != t.sym.end()) return it->second;
+    const int32_t id = (int32_t)t.sym_str.size();
+    t.sym.emplace(p, id);
+    t.sym_str.push_back(p);
+    auto v = t.vocab.find(p);
+    t.sym_vocab.push_back(v == t.vocab.end() ? -1 : (int64_t)v->second);
+    return id;
+}
+
+inline uint64_t pair_key(int32_t a, int32_t b) { return (uint64_t)(uint32_t)a << 32 | (uint32_t)b; }
+
+// The interned form of the loaded vocabulary and merges (see m1moe_tokenizer).
+void build_symbols(m1moe_tokenizer& t) {
+    t.sym.clear();
+    t.sym_str.clear();
+    t.sym_vocab.clear();
+    t.pair.clear();
+    for (const auto& kv : t.vocab) intern(t, kv.first);
+    for (const auto& kv : t.rank) {
+        const size_t cut = kv.first.find('\xff');  // never inside UTF-8
+        const std::string a = kv.first.substr(0, cut), b = kv.first.substr(cut + 1);
+        const int32_t ia = intern(t, a), ib = intern(t, b);
+        t.pair[pair_key(ia, ib)] = {kv.second, intern(t, a + b)};
+    }
+    const ByteTable& bt = byte_table();
+    char hex[8];
+    for (int c = 0; c < 256; ++c) {
+        t.byte_sym[c] = intern(t, bt.enc[c]);
+        std::snprintf(hex, sizeof hex, "<0x%02X>", c);
+        auto it = t.vocab.find(hex);
+        t.fallback_id[c] = it == t.vocab.end() ? -1 : (int64_t)it->second;
+    }
+}
+
+// Tokenizer.swift:212-228: while a pair has a merge, merge the one with the
+// lowest rank (the leftmost of equal ranks) and look again.  Negative ids are
+// scalars that no merge or vocab piece contains.
+void apply_bpe(const m1moe_tokenizer& t, std::vector<int32_t>& syms) {
     while (syms.size() > 1) {
-        int32_t best = INT32_MAX;
+        int32_t best = INT32_MAX, merged = -1;
         size_t at = SIZE_MAX;
         for (size_t i = 0; i + 1 < syms.size(); ++i) {
-            key.assign(syms[i]);
-            key.push_back('\xff');
-            key.append(syms[i + 1]);
-            auto it = t.rank.find(key);
-            if (it != t.rank.end() && it->second < best) best = it->second, at = i;
+            if (syms[i] < 0 || syms[i + 1] < 0) continue;
+            auto it = t.pair.find(pair_key(syms[i], syms[i + 1]));
+            if (it != t.pair.end() && it->second.first < best)
+                best = it->second.first, merged = it->second.second, at = i;
         }
         if (at == SIZE_MAX) break;
-        syms[at] += syms[at + 1];
+        syms[at] = merged;
         syms.erase(syms.begin() + (ptrdiff_t)at + 1);
     }
 }
 
+// Encoding is a function of the word alone, so each call keeps the ids of the
+// words it has seen (bounded; cleared when full).
+struct WordCache {
+    std::unordered_map<std::string, std::vector<uint32_t>> map;
+    const std::vector<uint32_t>* find(const std::string& w) const {
+        auto it = map.find(w);
+        return it == map.end() ? nullptr : &it->second;
+    }
+    void put(const std::string& w, std::vector<uint32_t> ids) {
+        if (map.size() >= (1u << 16)) map.clear();
+        map.emplace(w, std::move(ids));
+    }
+};
+
+// Words start at each space (the space is the word's first symbol, as
+// U+0120); a word's symbols are its bytes' table pieces.  The text is valid
+// UTF-8, so a space byte is always the scalar ' '.
 void encode_byte_level(const m1moe_tokenizer& t, const std::string& text, std::vector<uint32_t>& ids) {
-    const ByteTable& bt = byte_table();
-    std::vector<std::vector<std::string>> words;  // each word as its initial symbols
-    std::vector<std::string> cur;
-    const std::string& space = bt.enc[0x20];
-    bool first = true;
-    for (const std::string& ch : scalars(text)) {
-        const bool is_space = ch.size() == 1 && ch[0] == ' ';
-        if (is_space && !cur.empty()) {
-            words.push_back(std::move(cur));
-            cur.assign(1, space);
-        } else if (first && is_space) {
-            cur.assign(1, space);
-        } else {
-            for (unsigned char c : ch) cur.push_back(bt.enc[c]);
+    WordCache cache;
+    std::vector<int32_t> syms;
+    std::vector<uint32_t> out;
+    auto word = [&](size_t b, size_t e) {
+        const std::string w = text.substr(b, e - b);
+        if (const std::vector<uint32_t>* hit = cache.find(w)) {
+            ids.insert(ids.end(), hit->begin(), hit->end());
+            return;
         }
-        first = false;
-    }
-    if (!cur.empty()) words.push_back(std::move(cur));
-    for (auto& w : words) {
-        apply_bpe(t, w);
-        for (const std::string& s : w) {
-            auto it = t.vocab.find(s);
-            if (it != t.vocab.end()) ids.push_back(it->second);
+        syms.clear();
+        for (size_t i = b; i < e; ++i) syms.push_back(t.byte_sym[(unsigned char)text[i]]);
+        apply_bpe(t, syms);
+        out.clear();
+        for (int32_t id : syms)
+            if (t.sym_vocab[(size_t)id] >= 0) out.push_back((uint32_t)t.sym_vocab[(size_t)id]);
+        ids.insert(ids.end(), out.begin(), out.end());
+        cache.put(w, out);
+    };
+    size_t start = 0;
+    for (size_t i = 1; i < text.size(); ++i)
+        if (text[i] == ' ' && i > start) {
+            word(start, i);
+            start = i;
         }
-    }
+    if (start < text.size()) word(start, text.size());
 }
 
+// Words split at spaces (empty ones skipped), each prefixed with U+2581 and
+// split into scalars; a final symbol outside the vocab becomes its bytes'
+// "<0xHH>" pieces (those present).
 void encode_sentencepiece(const m1moe_tokenizer& t, const std::string& text, std::vector<uint32_t>& ids) {
+    WordCache cache;
+    std::vector<int32_t> syms;
+    std::vector<std::string> unknown;  // the scalars behind negative ids
+    std::vector<uint32_t> out;
     size_t start = 0;
-    char hex[8];
     for (;;) {
         const size_t sp = text.find(' ', start);
-        const std::string word = text.substr(start, sp == std::string::npos ? std::string::npos : sp - start);
-        if (!word.empty()) {
-            std::vector<std::string> syms = scalars(kMeta + word);
-            apply_bpe(t, syms);
-            for (const std::string& s : syms) {
-                auto it = t.vocab.find(s);
-                if (it != t.vocab.end()) {
-                    ids.push_back(it->second);
-                    continue;
+        const size_t end = sp == std::string::npos ? text.size() : sp;
+        if (end > start) {
+            const std::string w = text.substr(start, end - start);
+            if (const std::vector<uint32_t>* hit = cache.find(w)) {
+                ids.insert(ids.end(), hit->begin(), hit->end());
+            } else {
+                syms.clear();
+                unknown.clear();
+                for (std::string& ch : scalars(kMeta + w)) {
+                    auto it = t.sym.find(ch);
+                    if (it != t.sym.end()) {
+                        syms.push_back(it->second);
+                    } else {
+                        unknown.push_back(std::move(ch));
+                        syms.push_back(-(int32_t)unknown.size());
+                    }
                 }
-                for (unsigned char c : s) {  // byte fallback
-                    std::snprintf(hex, sizeof hex, "<0x%02X>", c);
-                    auto jt = t.vocab.find(hex);
-                    if (jt != t.vocab.end()) ids.push_back(jt->second);
+                apply_bpe(t, syms);
+                out.clear();
+                for (int32_t id : syms) {
+                    if (id >= 0 && t.sym_vocab[(size_t)id] >= 0) {
+                        out.push_back((uint32_t)t.sym_vocab[(size_t)id]);
+                        continue;
+                    }
+                    const std::string& p = id >= 0 ? t.sym_str[(size_t)id] : unknown[(size_t)(-id - 1)];
+                    for (unsigned char c : p)  // byte fallback
+                        if (t.fallback_id[c] >= 0) out.push_back((uint32_t)t.fallback_id[c]);
                 }
+                ids.insert(ids.end(), out.begin(), out.end());
+                cache.put(w, out);
             }
         }
         if (sp == std::string::npos) break;

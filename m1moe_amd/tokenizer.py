@@ -50,14 +50,13 @@ class Tokenizer:
     def encode(self, text: str, add_bos: bool = True, bos: int = 1) -> List[int]:
         data = text.encode("utf-8")
         n = ctypes.c_uint64()
-        check(self.lib.m1moe_tokenizer_encode(self.handle, data, len(data), int(add_bos),
-                                              int(bos), None, 0, ctypes.byref(n)),
-              "m1moe_tokenizer_encode")
-        ids = np.empty(max(int(n.value), 1), np.uint32)
+        # at most 4 ids per byte (a SentencePiece word of one unknown byte: the
+        # three bytes of U+2581 and its own, by byte fallback) + the BOS: one call
+        ids = np.empty(4 * len(data) + 8, np.uint32)
         check(self.lib.m1moe_tokenizer_encode(self.handle, data, len(data), int(add_bos),
                                               int(bos), ids.ctypes.data, ids.size,
                                               ctypes.byref(n)), "m1moe_tokenizer_encode")
-        return [int(v) for v in ids[:n.value]]
+        return ids[:n.value].tolist()
 
     def decode(self, ids: Iterable[int], skip_special: bool = True) -> str:
         a = np.ascontiguousarray(list(ids), dtype=np.uint32)

@@ -575,6 +575,37 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
         g.part = dec->pf_part;
         return launched(launch_gemm(g, st), what);
     };
+    // q, k and v: one launch over the three weight segments when the prompt
+    // is short (each alone would leave most CUs idle), three launches else
+    const bool merge_qkv = h % 64 == 0 && (long)((N + 127) / 128) * ((T + 127) / 128) < 256;
+    auto qkv_gemm = [&](int l) -> int32_t {
+        const uint16_t* wq = dec->wq + (size_t)l * qd * h;
+        const uint16_t* wk = dec->wk + (size_t)l * kvd * h;
+        const uint16_t* wv = dec->wv + (size_t)l * kvd * h;
+        if (merge_qkv) {
+            GemmArgs g{};
+            g.A = dec->pf_xn;
+            g.lda = h;
+            g.W = wq;
+            g.W1 = wk;
+            g.W2 = wv;
+            g.n1 = qd;
+            g.n2 = qd + kvd;
+            g.C = dec->pf_qkv;
+            g.ldc = N;
+            g.M = T;
+            g.N = N;
+            g.K = h;
+            g.part = dec->pf_part;
+            return launched(launch_gemm(g, st), "prefill q/k/v");
+        }
+        int32_t r;
+        if ((r = gemm(dec->pf_xn, h, wq, nullptr, dec->pf_qkv, N, qd, h, "prefill q")) ||
+            (r = gemm(dec->pf_xn, h, wk, nullptr, dec->pf_qkv + qd, N, kvd, h, "prefill k")) ||
+            (r = gemm(dec->pf_xn, h, wv, nullptr, dec->pf_qkv + qd + kvd, N, kvd, h, "prefill v")))
+            return r;
+        return M1MOE_OK;
+    };
     if ((rc = launched(launch_pf_embed(a, st), "prefill embedding"))) return rc;  // :129-131
     const uint64_t cache_layer = (uint64_t)dec->sh.max_seq * kvd;
     for (int l = 0; l < dec->L; ++l) {
@@ -582,11 +613,7 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
         if ((rc = launched(launch_rmsnorm_rows(dec->pf_res, dec->in_norm + (size_t)l * h, dec->pf_xn, T, h,
                                                eps, st),
                            "prefill input norm")) ||
-            (rc = gemm(dec->pf_xn, h, dec->wq + (size_t)l * qd * h, nullptr, dec->pf_qkv, N, qd, h, "prefill q")) ||
-            (rc = gemm(dec->pf_xn, h, dec->wk + (size_t)l * kvd * h, nullptr, dec->pf_qkv + qd, N, kvd, h,
-                       "prefill k")) ||
-            (rc = gemm(dec->pf_xn, h, dec->wv + (size_t)l * kvd * h, nullptr, dec->pf_qkv + qd + kvd, N, kvd, h,
-                       "prefill v")))
+            (rc = qkv_gemm(l)))
             return rc;
         // q/k norms, RoPE, KV rows (:194-220); causal attention (:226)
         a.q_norm = qk ? dec->q_norm + (size_t)l * hd : nullptr;

@@ -343,6 +343,12 @@ struct GemmArgs {
     // or null; with it a GEMM whose tiles leave the CUs idle splits its k range
     float* part;
     int32_t splits;              // set by launch_gemm
+    // optional second and third weight segments: rows [n1, n2) are rows
+    // 0 .. of W1, rows [n2, N) rows 0 .. of W2 (q, k and v in one launch);
+    // null W1: every row from W.  Needs K % 64 == 0.
+    const uint16_t* W1;
+    const uint16_t* W2;
+    int32_t n1, n2;
 };
 constexpr int64_t kGemmPartFloats = 512LL * 64 * 64;  // the workspace launch_gemm may use
 

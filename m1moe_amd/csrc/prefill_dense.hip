@@ -305,7 +305,10 @@ __global__ __launch_bounds__(256, 2) void gemm_bf3_kernel(GemmArgs g) {
     const int xr = tid / (kBK / EA), xc = (tid % (kBK / EA)) * EA;
     const int wr = tid / (kBK / EW), wc = (tid % (kBK / EW)) * EW;
     const float* xrow = g.A + (size_t)min(m0 + xr, g.M - 1) * g.lda + xc;
-    const uint16_t* wrow = g.W + (size_t)min(n0 + wr, g.N - 1) * g.K + wc;
+    const int wrow_n = min(n0 + wr, g.N - 1);
+    const uint16_t* wrow = !g.W1 || wrow_n < g.n1 ? g.W + (size_t)wrow_n * g.K + wc
+                           : wrow_n < g.n2        ? g.W1 + (size_t)(wrow_n - g.n1) * g.K + wc
+                                                  : g.W2 + (size_t)(wrow_n - g.n2) * g.K + wc;
     typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
     float4 xv[EA / 4];
     u32x4v wv[EW / 8];
@@ -443,6 +446,8 @@ int launch_rmsnorm_rows(const float* x, const uint16_t* w, float* out, int rows,
 int launch_gemm(const GemmArgs& g, void* stream) {
     if (g.K % kGK || g.M <= 0 || g.N <= 0 || g.lda % 4) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (g.W1 && (g.K % kBK || !g.W2 || g.n1 < 0 || g.n1 > g.n2 || g.n2 > g.N))
+        return (int)hipErrorInvalidValue;
     if (g.K % kBK) {  // f32 MFMA for a K that is not a multiple of 64
         const dim3 grid((unsigned)((g.N + kGN - 1) / kGN), (unsigned)((g.M + kGM - 1) / kGM));
         hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), 0, st, g);

@@ -385,12 +385,13 @@ def test_prefill_dense_path_is_tight(Ts):
 
 
 def test_prefill_split_k_gemms_are_tight():
-    """OLMoE widths (h = q = kv = 2048), one layer, MoE block zeroed: a
-    100-token prefill gives each q/k/v/o_proj GEMM 64 tiles of 64 x 64, split
-    over 8 shares of 4 of its 32 k-blocks; a second 170-token prefill gives
-    96 tiles, 5 shares of 6-7 k-blocks.  The partials are summed in a fixed
-    order with the residual; last logits against the oracle's token-by-token
-    run to relative L2 1e-5."""
+    """OLMoE widths (h = q = kv = 2048), one layer, MoE block zeroed.  A
+    100-token prefill: q, k and v as one launch over three weight segments
+    (192 tiles of 64 x 64, 2 shares of 16 k-blocks), o_proj 64 tiles in 8
+    shares of 4 k-blocks with the residual; a second 170-token prefill:
+    q/k/v 288 tiles unsplit, o_proj 96 tiles in 5 shares of 6-7 k-blocks.
+    Partials summed in a fixed order; last logits against the oracle's
+    token-by-token run to relative L2 1e-5."""
     p = Pair(synth.DECODERS["cfg1"], seed=53, max_seq=280, num_layers=1, nthreads=8)
     try:
         _zero_experts(p)

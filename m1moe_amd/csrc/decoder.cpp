@@ -624,12 +624,22 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
             (rc = launched(launch_pf_attention(a, st), "prefill attention")))
             return rc;
         // o_proj + residual (:227-233), post-attention RMSNorm (:234-236)
-        if ((rc = gemm(dec->pf_attn, qd, dec->wo + (size_t)l * h * qd, dec->pf_res, dec->pf_res2, h, h, qd,
-                       "prefill o_proj")) ||
-            (rc = launched(launch_rmsnorm_rows(dec->pf_res2, dec->post_norm + (size_t)l * h, dec->pf_xn, T, h,
-                                               eps, st),
-                           "prefill post-attention norm")))
-            return rc;
+        // (the norm is made by the GEMM's split-K sum when it has one)
+        GemmArgs o{};
+        o.A = dec->pf_attn;
+        o.lda = qd;
+        o.W = dec->wo + (size_t)l * h * qd;
+        o.R = dec->pf_res;
+        o.C = dec->pf_res2;
+        o.ldc = h;
+        o.M = T;
+        o.N = h;
+        o.K = qd;
+        o.part = dec->pf_part;
+        o.norm_w = dec->post_norm + (size_t)l * h;
+        o.norm_out = dec->pf_xn;
+        o.norm_eps = eps;
+        if ((rc = launched(launch_gemm(o, st), "prefill o_proj + post-attention norm"))) return rc;
         // the MoE block for the T tokens, its output the next residual (:240-266)
         if ((rc = m1moe_moe_prefill(ctx, l, T, dec->pf_xn, M1MOE_F32, dec->pf_res2, dec->pf_res, nullptr,
                                     nullptr)))

@@ -349,6 +349,12 @@ struct GemmArgs {
     const uint16_t* W1;
     const uint16_t* W2;
     int32_t n1, n2;
+    // optional RMSNorm of each output row (ldc == N): norm_out[m] =
+    // C[m] * rsqrt(mean(C[m]^2) + norm_eps) * norm_w (bf16), made by the
+    // split-K sum when there is one, else by a row-norm launch
+    const uint16_t* norm_w;
+    float* norm_out;
+    float norm_eps;
 };
 constexpr int64_t kGemmPartFloats = 512LL * 64 * 64;  // the workspace launch_gemm may use
 

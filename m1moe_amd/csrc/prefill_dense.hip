@@ -429,6 +429,44 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(GemmArgs g) {
     *reinterpret_cast<float4*>(g.C + m * g.ldc + n) = y;
 }
 
+// The same sum for one output row per workgroup (at most kSumNormSplits
+// splits), then that row's RMSNorm with the arithmetic of rmsnorm_rows_kernel
+// (each thread's squares summed in its own column order, four at a time).
+constexpr int kSumNormSplits = 8;
+__global__ __launch_bounds__(256) void splitk_sum_norm_kernel(GemmArgs g) {
+    __shared__ float s_red[4];
+    const size_t m = blockIdx.x, mn4 = (size_t)g.M * g.N / 4;
+    const float4* p = reinterpret_cast<const float4*>(g.part) + m * (g.N / 4);
+    float* c = g.C + m * g.ldc;
+    float acc = 0.f;
+    for (int i = threadIdx.x; i < g.N / 4; i += 256) {
+        float4 v[kSumNormSplits];  // every split's load in flight together
+#pragma unroll
+        for (int z = 0; z < kSumNormSplits; ++z)
+            if (z < g.splits) v[z] = p[(size_t)z * mn4 + i];
+        float4 y = v[0];
+#pragma unroll
+        for (int z = 1; z < kSumNormSplits; ++z)
+            if (z < g.splits) y.x += v[z].x, y.y += v[z].y, y.z += v[z].z, y.w += v[z].w;
+        if (g.R) {
+            const float4 r = *reinterpret_cast<const float4*>(g.R + m * g.ldc + 4 * i);
+            y.x += r.x, y.y += r.y, y.z += r.z, y.w += r.w;
+        }
+        *reinterpret_cast<float4*>(c + 4 * i) = y;
+        acc = fmaf(y.x, y.x, acc);
+        acc = fmaf(y.y, y.y, acc);
+        acc = fmaf(y.z, y.z, acc);
+        acc = fmaf(y.w, y.w, acc);
+    }
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const float ss = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+    const float rms = rsqrtf(ss / (float)g.N + g.norm_eps);
+    float* o = g.norm_out + m * g.ldc;
+    for (int i = threadIdx.x; i < g.N; i += 256) o[i] = c[i] * rms * bf16_to_f32(g.norm_w[i]);
+}
+
 }  // namespace
 
 int launch_pf_embed(const PfDenseArgs& a, void* stream) {
@@ -445,42 +483,50 @@ int launch_rmsnorm_rows(const float* x, const uint16_t* w, float* out, int rows,
 
 int launch_gemm(const GemmArgs& g, void* stream) {
     if (g.K % kGK || g.M <= 0 || g.N <= 0 || g.lda % 4) return (int)hipErrorInvalidValue;
-    hipStream_t st = static_cast<hipStream_t>(stream);
     if (g.W1 && (g.K % kBK || !g.W2 || g.n1 < 0 || g.n1 > g.n2 || g.n2 > g.N))
         return (int)hipErrorInvalidValue;
+    if (g.norm_w && (!g.norm_out || g.ldc != g.N)) return (int)hipErrorInvalidValue;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int splits = 1;
     if (g.K % kBK) {  // f32 MFMA for a K that is not a multiple of 64
         const dim3 grid((unsigned)((g.N + kGN - 1) / kGN), (unsigned)((g.M + kGM - 1) / kGM));
         hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), 0, st, g);
-        return (int)hipGetLastError();
-    }
-    // the largest tile that still gives at least one workgroup per CU
-    const long gm128 = (g.M + 127) / 128, gm64 = (g.M + 63) / 64;
-    const long gn128 = (g.N + 127) / 128, gn64 = (g.N + 63) / 64;
-    if (gn128 * gm128 >= 256)
-        hipLaunchKernelGGL((gemm_bf3_kernel<128, 128>), dim3((unsigned)gn128, (unsigned)gm128),
-                           dim3(256), 0, st, g);
-    else if (gn128 * gm64 >= 256)
-        hipLaunchKernelGGL((gemm_bf3_kernel<64, 128>), dim3((unsigned)gn128, (unsigned)gm64),
-                           dim3(256), 0, st, g);
-    else {
-        // Too few 64 x 64 tiles to fill the chip: split the k-blocks over
-        // gridDim.z (at least 4 per split, at most 512 workgroups in all) and
-        // sum the partials in a fixed order, so results do not depend on timing.
-        const long tiles = gn64 * gm64, nkb = g.K / kBK;
-        long S = 512 / tiles < nkb / 4 ? 512 / tiles : nkb / 4;
-        const bool aligned = g.N % 4 == 0 && g.ldc % 4 == 0 && (uintptr_t)g.C % 16 == 0 &&
-                             (uintptr_t)g.R % 16 == 0;
-        if (!g.part || !aligned || S < 2 || S * g.M * g.N > kGemmPartFloats) S = 1;
-        GemmArgs gs = g;
-        gs.splits = (int32_t)S;
-        hipLaunchKernelGGL((gemm_bf3_kernel<64, 64>), dim3((unsigned)gn64, (unsigned)gm64, (unsigned)S),
-                           dim3(256), 0, st, gs);
-        if (S > 1) {
-            const size_t mn4 = (size_t)g.M * g.N / 4;
-            hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)((mn4 + 255) / 256)), dim3(256), 0, st, gs);
+    } else {
+        // the largest tile that still gives at least one workgroup per CU
+        const long gm128 = (g.M + 127) / 128, gm64 = (g.M + 63) / 64;
+        const long gn128 = (g.N + 127) / 128, gn64 = (g.N + 63) / 64;
+        if (gn128 * gm128 >= 256) {
+            hipLaunchKernelGGL((gemm_bf3_kernel<128, 128>), dim3((unsigned)gn128, (unsigned)gm128),
+                               dim3(256), 0, st, g);
+        } else if (gn128 * gm64 >= 256) {
+            hipLaunchKernelGGL((gemm_bf3_kernel<64, 128>), dim3((unsigned)gn128, (unsigned)gm64),
+                               dim3(256), 0, st, g);
+        } else {
+            // Too few 64 x 64 tiles to fill the chip: split the k-blocks over
+            // gridDim.z (at least 4 per split, at most 512 workgroups in all)
+            // and sum the partials in a fixed order, so results do not depend
+            // on timing.
+            const long tiles = gn64 * gm64, nkb = g.K / kBK;
+            long S = 512 / tiles < nkb / 4 ? 512 / tiles : nkb / 4;
+            const bool aligned = g.N % 4 == 0 && g.ldc % 4 == 0 && (uintptr_t)g.C % 16 == 0 &&
+                                 (uintptr_t)g.R % 16 == 0;
+            if (!g.part || !aligned || S < 2 || S * g.M * g.N > kGemmPartFloats) S = 1;
+            GemmArgs gs = g;
+            gs.splits = splits = (int)S;
+            hipLaunchKernelGGL((gemm_bf3_kernel<64, 64>),
+                               dim3((unsigned)gn64, (unsigned)gm64, (unsigned)S), dim3(256), 0, st, gs);
+            if (S > 1 && S <= kSumNormSplits && g.norm_w) {  // the sum makes the row norm too
+                hipLaunchKernelGGL(splitk_sum_norm_kernel, dim3((unsigned)g.M), dim3(256), 0, st, gs);
+            } else if (S > 1) {
+                const size_t mn4 = (size_t)g.M * g.N / 4;
+                hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)((mn4 + 255) / 256)), dim3(256), 0,
+                                   st, gs);
+            }
         }
     }
-    return (int)hipGetLastError();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !g.norm_w || (splits > 1 && splits <= kSumNormSplits)) return (int)e;
+    return launch_rmsnorm_rows(g.C, g.norm_w, g.norm_out, g.M, g.N, g.norm_eps, stream);
 }
 
 int launch_pf_rope_kv(const PfDenseArgs& a, void* stream) {

@@ -8,8 +8,8 @@
 //                   4 tokens x 4 experts with its lanes across the columns
 //                   (coalesced 128-bit loads, all of a 2048-column row in
 //                   flight at once), a workgroup 4 tokens x 16 experts.  For
-//                   a prefill it also writes x's f16 copy (prep_token): wave
-//                   w of the workgroups of experts 0-15 takes token t0 + w.
+//                   a prefill an extra row of workgroups writes x's f16 copy
+//                   (prep_token): wave w takes token t0 + w.
 //                   Every product bf16 * x is exact in f64; each lane sums
 //                   its columns in f64, the lanes are added by a fixed DPP
 //                   tree, then one rounding to f32 (+ the optional logit
@@ -139,13 +139,13 @@ static_assert(kTT == 4, "one wave of the 256-thread workgroup per token");
 __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kTT, e0 = blockIdx.y * kTE + wave * kTEw;
-    // wave w of the workgroups of expert block 0 also makes token t0 + w's
-    // f16 copy for the prefill (its rows are in L2 from the logits)
-    const bool prep = a.xq && blockIdx.y == 0;
-    if (e0 >= a.E) {
-        if (prep) prep_token(a, t0 + wave, lane);
+    // for a prefill, an extra row of workgroups (the last) makes the f16 copy:
+    // wave w takes token t0 + w, beside the logits of the other rows
+    if (a.xq && blockIdx.y == gridDim.y - 1) {
+        prep_token(a, t0 + wave, lane);
         return;
     }
+    if (e0 >= a.E) return;
     double acc[kTT][kTEw];
 #pragma unroll
     for (int i = 0; i < kTT; ++i)
@@ -168,7 +168,6 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
                 if (a.user_logits) a.user_logits[(size_t)t * a.E + e] = l;
             }
         }
-    if (prep) prep_token(a, t0 + wave, lane);
 }
 
 // Orders this wave's LDS accesses before / after the call (lanes exchange
@@ -264,7 +263,8 @@ int launch_router_topk(const RouterArgs& a, void* stream) {
     if (a.E > kMaxE || a.K > kMaxK || a.h % 64) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(router_logits_kernel,
-                       dim3((unsigned)((a.T + kTT - 1) / kTT), (unsigned)((a.E + kTE - 1) / kTE)),
+                       dim3((unsigned)((a.T + kTT - 1) / kTT),
+                            (unsigned)((a.E + kTE - 1) / kTE + (a.xq ? 1 : 0))),
                        dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;

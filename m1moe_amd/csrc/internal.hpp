@@ -356,7 +356,7 @@ struct GemmArgs {
     float* norm_out;
     float norm_eps;
 };
-constexpr int64_t kGemmPartFloats = 512LL * 64 * 64;  // the workspace launch_gemm may use
+constexpr int64_t kGemmPartFloats = 768LL * 64 * 64;  // the workspace launch_gemm may use
 
 // The T prompt tokens of a decoder prefill at positions *pos .. *pos + T - 1.
 struct PfDenseArgs {

@@ -507,7 +507,7 @@ int launch_gemm(const GemmArgs& g, void* stream) {
             // and sum the partials in a fixed order, so results do not depend
             // on timing.
             const long tiles = gn64 * gm64, nkb = g.K / kBK;
-            long S = 512 / tiles < nkb / 4 ? 512 / tiles : nkb / 4;
+            long S = 768 / tiles < nkb / 4 ? 768 / tiles : nkb / 4;
             const bool aligned = g.N % 4 == 0 && g.ldc % 4 == 0 && (uintptr_t)g.C % 16 == 0 &&
                                  (uintptr_t)g.R % 16 == 0;
             if (!g.part || !aligned || S < 2 || S * g.M * g.N > kGemmPartFloats) S = 1;

@@ -387,17 +387,17 @@ def test_prefill_dense_path_is_tight(Ts):
 def test_prefill_split_k_gemms_are_tight():
     """OLMoE widths (h = q = kv = 2048), one layer, MoE block zeroed.  A
     100-token prefill: q, k and v as one launch over three weight segments
-    (192 tiles of 64 x 64, 2 shares of 16 k-blocks), o_proj 64 tiles in 8
-    shares of 4 k-blocks with the residual; a second 170-token prefill:
-    q/k/v 288 tiles unsplit, o_proj 96 tiles in 5 shares of 6-7 k-blocks.
-    Partials summed in a fixed order; last logits against the oracle's
-    token-by-token run to relative L2 1e-5."""
-    p = Pair(synth.DECODERS["cfg1"], seed=53, max_seq=280, num_layers=1, nthreads=8)
+    (192 tiles of 64 x 64, 4 shares of 8 k-blocks), o_proj 64 tiles in 8
+    shares of 4 k-blocks, summed with the residual and normalised in one
+    kernel; a second 200-token prefill: q/k/v 384 tiles in 2 shares, o_proj
+    128 tiles in 6 shares of 5-6 k-blocks.  Partials summed in a fixed order;
+    last logits against the oracle's token-by-token run to relative L2 1e-5."""
+    p = Pair(synth.DECODERS["cfg1"], seed=53, max_seq=310, num_layers=1, nthreads=8)
     try:
         _zero_experts(p)
-        toks = synth.prompt_tokens(p.wl, 23, 270)
+        toks = synth.prompt_tokens(p.wl, 23, 300)
         off = 0
-        for T in (100, 170):
+        for T in (100, 200):
             say(f"olmoe-width split-K prefill T={T} at position {off}")
             g_tok, g_lg = p.dec.prefill(toks[off:off + T], return_logits=True)
             for t in toks[off:off + T]:

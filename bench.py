@@ -48,16 +48,9 @@ def log(msg: str) -> None:
 
 def decode_kernel_name(shape) -> str:
     """The decode kernel the library selects for this shape on a 256-CU
-    MI355X (ctx.cpp: decode_cu_fits and the CU count)."""
-    K, I, E, gs = shape.top_k, shape.intermediate, shape.num_experts, shape.group_size
-    if E > 256 or gs not in (32, 64, 128):
-        return "moe_decode_kernel"
-    if (shape.hidden == 2048 and K <= 8 and 8 % K == 0 and I in (1024, 2048)
-            and K * I in (8192, 16384)):
-        return "moe_decode_cu_kernel"
-    if shape.hidden == 4096 and K <= 2 and I % 128 == 0 and K * (I // 128) <= 256:
-        return "moe_decode_cuw_kernel"
-    return "moe_decode_kernel"
+    MI355X (m1moe_decode_kernel_for, one per-CU workgroup per CU)."""
+    from m1moe_amd.engine import decode_kernel_for
+    return decode_kernel_for(shape, 256, 1)
 
 
 def cpu_threads() -> int:

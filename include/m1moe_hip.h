@@ -13,11 +13,18 @@
  *    m1moe_last_error() returns a thread-local message for the last failing
  *    call on this thread.
  *  - A context owns all device memory it allocates (expert arena, routers,
- *    scratch, m1moe_alloc buffers) and one HIP stream.  Every compute call is
- *    enqueued asynchronously on that stream; m1moe_sync() waits for it.  A
+ *    scratch, m1moe_alloc buffers).  Every compute call is enqueued
+ *    asynchronously on the context's stream; m1moe_sync() waits for it.  A
  *    context is single-threaded (the reference engine is driven from one
- *    serial queue, Sources/bench/main.swift:58); separate contexts are
- *    independent.
+ *    serial queue, Sources/bench/main.swift:58).
+ *  - All contexts on one device share one library stream, so the library's
+ *    launches on a device never overlap: on a device with at least 256 CUs
+ *    the per-CU decode kernels (hidden 2048 and 4096 shapes, see
+ *    m1moe_decode_kernel_for) run one workgroup on every CU and each
+ *    workgroup waits for every other one, so they need the whole device.
+ *    Work of another stream or process on the same GPU can keep some of
+ *    their workgroups from starting; the waiting ones then give up after
+ *    about a second, and the next m1moe_sync() reports M1MOE_ERR_DEVICE.
  *  - Arguments (shapes, layer/expert ranges, image sizes, dtypes, null
  *    pointers) are validated on the host before anything is enqueued.
  *    Expert indices that arrive in device memory are checked by the kernels;
@@ -95,6 +102,18 @@ int32_t m1moe_expert_bytes(const m1moe_moe_shape* shape, uint64_t* out);
  * (InferenceEngine.swift:84-97). */
 int32_t m1moe_expert_offsets(const m1moe_moe_shape* shape, uint64_t out[9]);
 
+/* The decode kernel a shape runs on a device with `cus` compute units, each
+ * holding `blocks_per_cu` workgroups of the per-CU kernels (1 on an
+ * MI355X): *kernel = 1 (moe_decode_cu_kernel: hidden 2048, K * I 8192 or
+ * 16384) or 2 (moe_decode_cuw_kernel: hidden 4096, K <= 2) when all 256 of
+ * the per-CU kernel's workgroups fit on the device at once — these need the
+ * whole device (conventions above) — else 0 (moe_decode_kernel, which only
+ * waits for lower workgroup ids and shares the device safely).  m1moe_create
+ * makes the same choice from the device's CU count and occupancy.  No
+ * counterpart in the reference (one Metal path); host only. */
+int32_t m1moe_decode_kernel_for(const m1moe_moe_shape* shape, int32_t cus,
+                                int32_t blocks_per_cu, int32_t* kernel);
+
 /* ---- context (replaces MetalContext, MetalContext.swift:69-185) -------- */
 
 /* Creates a context on HIP device `device`: allocates the resident expert
@@ -111,7 +130,8 @@ void m1moe_destroy(m1moe_ctx_t ctx);
 /* Copies one layer_NN.bin image (num_experts expert blocks, exactly
  * num_experts * expert_bytes bytes) from host memory into the arena.  The
  * reference zero-fills a missing or short expert read
- * (InferenceEngine.swift:274-279); here a wrong size is an error. */
+ * (InferenceEngine.swift:274-279); here a wrong size is an error, and so is
+ * a non-finite group scale or bias (the layer then stays unloaded). */
 int32_t m1moe_upload_layer_experts(m1moe_ctx_t ctx, int32_t layer,
                                    const void* host_image, uint64_t bytes);
 
@@ -128,7 +148,14 @@ int32_t m1moe_set_logit_bias(m1moe_ctx_t ctx, int32_t layer,
                              const float* host_bias, int32_t count);
 
 /* Device pointer to the first byte of (layer, expert)'s block, for callers
- * that fill the arena on the device. */
+ * that fill the arena on the device.  The decode and prefill kernels also
+ * read repacked copies of each layer's blocks; this call marks the layer's
+ * copies stale and the next decode or prefill of the layer rebuilds them
+ * from the arena (refused during graph capture).  So every write through
+ * the pointer must be complete, in order on the context stream (or
+ * synchronised), before the next decode or prefill of the layer, and a
+ * later write needs this call again first: a write after the rebuild is
+ * seen by the arena's gate/up rows but not by the copies. */
 int32_t m1moe_expert_block(m1moe_ctx_t ctx, int32_t layer, int32_t expert,
                            void** dev_ptr);
 
@@ -145,7 +172,10 @@ int32_t m1moe_copy_d2d(m1moe_ctx_t ctx, void* dev_dst, const void* dev_src,
                        uint64_t bytes);
 
 /* Replaces the context stream with a caller-owned hipStream_t (passed as
- * void*); NULL restores the context's own stream. */
+ * void*); NULL restores the library stream of the device.  Refused
+ * (M1MOE_ERR_INVALID) while another context is live on the same device, and
+ * m1moe_create on a device refuses a second context while the first runs on
+ * a caller stream: launches on one device stay on one stream. */
 int32_t m1moe_set_stream(m1moe_ctx_t ctx, void* hip_stream);
 int32_t m1moe_get_stream(m1moe_ctx_t ctx, void** hip_stream);
 
@@ -162,7 +192,12 @@ int32_t m1moe_event_elapsed_ms(m1moe_event_t start, m1moe_event_t end,
 void m1moe_event_destroy(m1moe_event_t ev);
 
 /* Captures every call enqueued on the context stream between begin and end
- * into a HIP graph (no device work runs during capture). */
+ * into a HIP graph (no device work runs during capture).  A graph is
+ * launched on the context it was captured on; its launch is refused
+ * (M1MOE_ERR_INVALID) once a call has reallocated a scratch buffer of the
+ * context since the capture (a prefill, decoder prefill or attention call
+ * larger than any before), since the graph holds the freed addresses:
+ * capture it again. */
 int32_t m1moe_graph_begin(m1moe_ctx_t ctx);
 int32_t m1moe_graph_end(m1moe_ctx_t ctx, m1moe_graph_t* out);
 int32_t m1moe_graph_launch(m1moe_ctx_t ctx, m1moe_graph_t graph);

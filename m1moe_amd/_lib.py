@@ -81,6 +81,7 @@ _PROTOTYPES = [
     ("m1moe_check_shape", c_int32, [POINTER(MoEShape)]),
     ("m1moe_expert_bytes", c_int32, [POINTER(MoEShape), POINTER(c_uint64)]),
     ("m1moe_expert_offsets", c_int32, [POINTER(MoEShape), POINTER(c_uint64)]),
+    ("m1moe_decode_kernel_for", c_int32, [POINTER(MoEShape), c_int32, c_int32, POINTER(c_int32)]),
     ("m1moe_create", c_int32, [c_int32, POINTER(MoEShape), POINTER(c_void_p)]),
     ("m1moe_destroy", None, [c_void_p]),
     ("m1moe_upload_layer_experts", c_int32, [c_void_p, c_int32, c_void_p, c_uint64]),

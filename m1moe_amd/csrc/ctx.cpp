@@ -12,6 +12,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <new>
 #include <set>
 #include <string>
@@ -67,6 +69,58 @@ namespace {
 using namespace m1moe;
 
 constexpr int32_t kSpinLimit = 1 << 20;  // bounded waits in the decode kernel (~1 s)
+
+// The one library stream of each device, shared by every context on it, so
+// that no two launches of the library overlap on a device (the per-CU decode
+// kernels wait for all 256 of their workgroups, which must be resident
+// together; the reference drives its engine from one serial queue,
+// MetalContext.swift:73-77, Sources/bench/main.swift:58).  A caller stream
+// (m1moe_set_stream) is accepted only while its context is the device's only
+// one, and no second context is created on the device until it is unset.
+struct DeviceShare {
+    hipStream_t stream = nullptr;
+    int users = 0;
+    m1moe_ctx_t on_caller_stream = nullptr;
+};
+std::mutex g_share_mu;
+std::map<int32_t, DeviceShare> g_share;
+
+int32_t share_join(m1moe_ctx_t c) {
+    std::lock_guard<std::mutex> lk(g_share_mu);
+    DeviceShare& d = g_share[c->device];
+    if (d.users > 0 && d.on_caller_stream)
+        return fail(M1MOE_ERR_INVALID,
+                    "device %d's other context enqueues on a caller stream (m1moe_set_stream); "
+                    "set it back to NULL before creating another context on the device (all "
+                    "contexts on one device share one stream)", c->device);
+    if (!d.stream) {
+        hipError_t e = hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            d.stream = nullptr;
+            if (d.users == 0) g_share.erase(c->device);
+            return fail(M1MOE_ERR_HIP, "hipStreamCreate failed: %s", hipGetErrorString(e));
+        }
+    }
+    ++d.users;
+    c->registered = true;
+    c->lib_stream = d.stream;
+    c->stream = d.stream;
+    return M1MOE_OK;
+}
+
+void share_leave(m1moe_ctx_t c) {
+    if (!c->registered) return;
+    std::lock_guard<std::mutex> lk(g_share_mu);
+    auto it = g_share.find(c->device);
+    if (it == g_share.end()) return;
+    DeviceShare& d = it->second;
+    if (d.on_caller_stream == c) d.on_caller_stream = nullptr;
+    if (--d.users == 0) {
+        if (d.stream) (void)hipStreamDestroy(d.stream);
+        g_share.erase(it);
+    }
+    c->registered = false;
+}
 
 m1moe::FusedArgs fused_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32_t x_dtype,
                             const float* residual, float* out) {
@@ -215,6 +269,7 @@ int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
         "prefill sorted tokens", "prefill expert offsets", "prefill tile offsets",
         "prefill tile descriptors", "prefill act",        "prefill expert outputs"};
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->pf_cap > 0) ++ctx->scratch_gen;  // earlier graphs hold the old buffers
     for (void** b : bufs) {
         if (*b) (void)hipFree(*b);
         *b = nullptr;
@@ -390,10 +445,26 @@ int32_t m1moe_expert_offsets(const m1moe_moe_shape* s, uint64_t out[9]) {
     return M1MOE_OK;
 }
 
+int32_t m1moe_decode_kernel_for(const m1moe_moe_shape* s, int32_t cus, int32_t blocks_per_cu,
+                                int32_t* kernel) {
+    int32_t rc = m1moe_check_shape(s);
+    if (rc) return rc;
+    if (!kernel) return fail(M1MOE_ERR_INVALID, "null output");
+    if (cus < 0 || blocks_per_cu < 0)
+        return fail(M1MOE_ERR_INVALID, "cus=%d and blocks_per_cu=%d must be >= 0", cus,
+                    blocks_per_cu);
+    const bool fits = m1moe::decode_cu_fits(s->hidden, s->num_experts, s->top_k,
+                                            s->intermediate, s->group_size);
+    *kernel = m1moe::decode_kernel_choice(fits, s->hidden, cus, blocks_per_cu);
+    return M1MOE_OK;
+}
+
 void m1moe_destroy(m1moe_ctx_t ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->lib_stream && ctx->lib_stream != ctx->stream)
+        (void)hipStreamSynchronize(ctx->lib_stream);
     for (void* p : ctx->allocs) (void)hipFree(p);
     void* owned[] = {ctx->arena,   ctx->dec,      ctx->pft,      ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
@@ -401,7 +472,7 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
                      ctx->pf_toff, ctx->pf_tdesc,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part, ctx->attn_cnt};
     for (void* p : owned)
         if (p) (void)hipFree(p);
-    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    share_leave(ctx);
     delete ctx;
 }
 
@@ -429,12 +500,10 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         return code;
     };
     if (hipSetDevice(device) != hipSuccess) return cleanup(fail(M1MOE_ERR_HIP, "hipSetDevice"));
-    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess)
-        return cleanup(fail(M1MOE_ERR_HIP, "hipStreamCreate failed"));
+    if ((rc = share_join(c))) return cleanup(rc);
     if (int e = m1moe::static_scratch_attach(device, &c->static_scratch))
         return cleanup(fail(M1MOE_ERR_HIP, "static scratch address of device %d: %s", device,
                             hipGetErrorString((hipError_t)e)));
-    c->stream = c->own_stream;
     const uint64_t cap = m1moe::kPrefillCap;
     {
         // hand-off state of the fused decode kernel: kLogitRep replicas of
@@ -462,8 +531,13 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
             return cleanup(fail(M1MOE_ERR_HIP, "hipDeviceGetAttribute(multiprocessor count)"));
         c->cus = cus;
-        c->decode_cu = cus >= m1moe::kCuWorkgroups &&
-                       m1moe::decode_cu_fits(g.h, g.E, g.K, g.I, g.gs);
+        // the per-CU kernels only when all of their workgroups fit on the
+        // device at once (CUs x workgroups per CU, from the occupancy query)
+        const bool fits = m1moe::decode_cu_fits(g.h, g.E, g.K, g.I, g.gs);
+        int blocks = 0;
+        if (fits && m1moe::decode_cu_blocks_per_cu(g.h, g.K, g.I, g.gs, &blocks) != 0)
+            blocks = 0;
+        c->decode_cu = m1moe::decode_kernel_choice(fits, g.h, cus, blocks) != 0;
         c->dec_stale.assign(s->num_layers, false);
         if (c->decode_cu) {
             c->dec_bytes = m1moe::decode_copy_bytes(g.h, g.I, g.gs);
@@ -519,6 +593,18 @@ int32_t m1moe_upload_layer_experts(m1moe_ctx_t ctx, int32_t layer, const void* h
     }
     if ((rc = launch_pft_copy(ctx, layer))) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    // the prefill copy kernel flags a non-finite group scale or bias (bit 8):
+    // report it here, take the bit back, and leave the layer unloaded
+    uint32_t flag = 0;
+    HIP_TRY(hipMemcpy(&flag, ctx->err, 4, hipMemcpyDeviceToHost));
+    if (flag & 8u) {
+        const uint32_t rest = flag & ~8u;
+        HIP_TRY(hipMemcpy(ctx->err, &rest, 4, hipMemcpyHostToDevice));
+        ctx->layer_loaded[layer] = false;
+        return fail(M1MOE_ERR_INVALID,
+                    "layer %d image has a non-finite group scale or bias; the layer is not "
+                    "loaded", layer);
+    }
     ctx->layer_loaded[layer] = true;
     return M1MOE_OK;
 }
@@ -619,7 +705,14 @@ int32_t m1moe_copy_d2d(m1moe_ctx_t ctx, void* d, const void* s, uint64_t n) {
 int32_t m1moe_set_stream(m1moe_ctx_t ctx, void* hip_stream) {
     int32_t rc;
     if ((rc = check_ctx(ctx))) return rc;
-    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    std::lock_guard<std::mutex> lk(g_share_mu);
+    DeviceShare& d = g_share[ctx->device];
+    if (hip_stream && d.users > 1)
+        return fail(M1MOE_ERR_INVALID,
+                    "%d contexts share device %d and its one stream; a caller stream is accepted "
+                    "only while a context is the device's only one", d.users, ctx->device);
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->lib_stream;
+    d.on_caller_stream = hip_stream ? ctx : nullptr;
     return M1MOE_OK;
 }
 
@@ -725,6 +818,8 @@ int32_t m1moe_graph_end(m1moe_ctx_t ctx, m1moe_graph_t* out) {
         delete gr;
         return fail(M1MOE_ERR_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
     }
+    gr->owner = ctx;
+    gr->scratch_gen = ctx->scratch_gen;
     *out = gr;
     return M1MOE_OK;
 }
@@ -733,6 +828,12 @@ int32_t m1moe_graph_launch(m1moe_ctx_t ctx, m1moe_graph_t graph) {
     int32_t rc;
     if ((rc = check_ctx(ctx))) return rc;
     if (!graph) return fail(M1MOE_ERR_INVALID, "null graph");
+    if (graph->owner != ctx)
+        return fail(M1MOE_ERR_INVALID, "the graph was captured on another context");
+    if (graph->scratch_gen != ctx->scratch_gen)
+        return fail(M1MOE_ERR_INVALID,
+                    "a scratch buffer was reallocated (a call with a larger size) since the "
+                    "graph was captured, so it holds freed addresses; capture it again");
     HIP_TRY(hipGraphLaunch(graph->exec, ctx->stream));
     return M1MOE_OK;
 }

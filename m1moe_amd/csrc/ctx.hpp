@@ -22,6 +22,8 @@ struct m1moe_event {
 struct m1moe_graph {
     hipGraph_t graph;
     hipGraphExec_t exec;
+    m1moe_ctx_t owner;       // the context whose stream was captured
+    uint64_t scratch_gen;    // owner->scratch_gen when the capture ended
 };
 
 struct m1moe_ctx {
@@ -29,8 +31,17 @@ struct m1moe_ctx {
     int32_t cus = 0;                 // compute units of the device
     m1moe_moe_shape shape{};
     m1moe::Geom g{};
-    hipStream_t own_stream = nullptr;
+    // every context on a device enqueues on the device's one library stream
+    // (lib_stream, shared and reference-counted across the process), or on a
+    // caller stream set by m1moe_set_stream while it is the device's only
+    // context: the per-CU decode kernels need all their workgroups resident
+    // at once, so no two launches of the library may overlap on one device
+    hipStream_t lib_stream = nullptr;
     hipStream_t stream = nullptr;
+    bool registered = false;         // counted in the device's stream share
+    // bumped whenever a scratch buffer is reallocated: a graph captured
+    // before then holds the freed addresses and is refused at launch
+    uint64_t scratch_gen = 0;
     uint8_t* arena = nullptr;        // [L][E] expert blocks
     uint16_t* routers = nullptr;     // [L][E][h] bf16
     float* biases = nullptr;         // [L][E]

@@ -57,11 +57,11 @@
 namespace m1moe {
 namespace {
 
-// Phase stamps of the per-CU kernels, compiled only into the tracing build
-// (make -C m1moe_amd/csrc probes, -DM1MOE_DECODE_TRACE): s_memrealtime (100
-// MHz) per workgroup into LDS, written at the end of the launch to the buffer
-// that m1moe_trace_decode() set ([workgroup][64 slots]; none set: nothing is
-// written).  Slot numbers are listed by m1moe_amd/csrc/probes/decode_timeline.cpp.
+// Phase stamps of the per-CU kernels, compiled only when M1MOE_DECODE_TRACE
+// is defined (never in libm1moe_hip.so): s_memrealtime (100 MHz) per
+// workgroup into LDS, written at the end of the launch to the buffer that
+// m1moe_trace_decode() set ([workgroup][64 slots]; none set: nothing is
+// written).  The slot numbers are the arguments of the DTR_* calls below.
 #ifdef M1MOE_DECODE_TRACE
 __device__ unsigned long long* g_decode_trace;
 __shared__ unsigned long long s_dtr[64];
@@ -871,14 +871,8 @@ constexpr int kRPT = kHW / kT;      // down rows per thread
 constexpr int kWRows = 128;         // act rows per working workgroup
 constexpr int kWChunks = kWRows / 32;
 constexpr int kMaxKW = 2;
-#ifndef M1MOE_W_INFLIGHT
-#define M1MOE_W_INFLIGHT 2
-#endif
-#ifndef M1MOE_W_EARLY
-#define M1MOE_W_EARLY 2
-#endif
-constexpr int kWInFlight = M1MOE_W_INFLIGHT;  // gate/up batches in flight per wave
-constexpr int kWEarlyDown = M1MOE_W_EARLY;    // down chunks requested during the last batches
+constexpr int kWInFlight = 2;   // gate/up batches in flight per wave
+constexpr int kWEarlyDown = 2;  // down chunks requested during the last batches
 
 struct CuwLDS {
     alignas(16) float x[128 * 36];      // staged input, chunk c at 36 c
@@ -1312,6 +1306,39 @@ bool decode_cu_fits(int h, int E, int K, int I, int gs) {
     if (h == kHW)  // moe_decode_cuw_kernel
         return K <= kMaxKW && I % kWRows == 0 && K * (I / kWRows) <= kNG;
     return false;
+}
+
+namespace {
+template <class F>
+int occupancy_min(F f0, F f1, int* blocks) {
+    int b0 = 0, b1 = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b0, f0, kT, 0);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, f1, kT, 0);
+    *blocks = e == hipSuccess ? min(b0, b1) : 0;
+    return (int)e;
+}
+template <int UG, int GSL>
+int occupancy_ug(int* blocks) {
+    return occupancy_min(moe_decode_cu_kernel<UG, GSL, false>, moe_decode_cu_kernel<UG, GSL, true>,
+                         blocks);
+}
+template <int UG>
+int occupancy_gs(int gs, int* blocks) {
+    return gs == 32 ? occupancy_ug<UG, 0>(blocks)
+                    : (gs == 64 ? occupancy_ug<UG, 1>(blocks) : occupancy_ug<UG, 2>(blocks));
+}
+}  // namespace
+
+int decode_cu_blocks_per_cu(int h, int K, int I, int gs, int* blocks) {
+    *blocks = 0;
+    if (h == kHW) {
+        switch (gs) {
+            case 32: return occupancy_min(moe_decode_cuw_kernel<0, false>, moe_decode_cuw_kernel<0, true>, blocks);
+            case 64: return occupancy_min(moe_decode_cuw_kernel<1, false>, moe_decode_cuw_kernel<1, true>, blocks);
+            default: return occupancy_min(moe_decode_cuw_kernel<2, false>, moe_decode_cuw_kernel<2, true>, blocks);
+        }
+    }
+    return K * I == 8192 ? occupancy_gs<4>(gs, blocks) : occupancy_gs<8>(gs, blocks);
 }
 
 uint64_t decode_copy_bytes(int h, int I, int gs) { return DecLayout(h, I, gs).bytes; }

@@ -33,6 +33,7 @@ int32_t ensure_attn_scratch(m1moe_ctx_t ctx, uint64_t floats) {
     }
     if (floats <= ctx->attn_part_floats) return M1MOE_OK;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->attn_part) ++ctx->scratch_gen;  // earlier graphs hold the old buffer
     if (ctx->attn_part) HIP_TRY(hipFree(ctx->attn_part));
     ctx->attn_part = nullptr;
     ctx->attn_part_floats = 0;
@@ -520,6 +521,7 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
     if (T > dec->pf_cap) {
         if ((rc = refuse_growth_in_capture(ctx->stream, "the decoder prefill scratch"))) return rc;
         HIP_TRY(hipStreamSynchronize(ctx->stream));
+        if (dec->pf_cap > 0) ++ctx->scratch_gen;  // earlier graphs hold the old buffers
         for (float** b : {&dec->pf_res, &dec->pf_res2, &dec->pf_xn, &dec->pf_qkv, &dec->pf_attn, &dec->pf_part}) {
             if (*b) (void)hipFree(*b);
             *b = nullptr;

@@ -207,7 +207,10 @@ __device__ __forceinline__ float bf16_pick(uint32_t w, uint32_t sel) {
 __host__ __device__ constexpr int perm8(int i) { return (i >> 1) | ((i & 1) << 2); }
 
 // Power-of-two scale that maps max|x| into [2^13, 2^14), so every scaled
-// input is a normal-range f16 with headroom (max f16 is 65504).
+// input is a normal-range f16 with headroom (max f16 is 65504).  The scale
+// is at most 2^126 so both factors stay finite, normal f32 values: a max|x|
+// below 2^-112 is scaled by 2^126 only (its chunk then sits below 2^14 with
+// fewer f16 bits; finite f32 inputs never need the lower bound).
 __device__ __forceinline__ void pow2_scale(float maxabs, float& scale, float& inv) {
     if (!(maxabs > 0.f) || !(maxabs < 3.0e38f)) {
         scale = 1.f;
@@ -216,8 +219,9 @@ __device__ __forceinline__ void pow2_scale(float maxabs, float& scale, float& in
     }
     int e;
     frexpf(maxabs, &e);  // maxabs = m * 2^e, m in [0.5, 1)
-    scale = ldexpf(1.f, 14 - e);
-    inv = ldexpf(1.f, e - 14);
+    const int k = min(max(14 - e, -126), 126);
+    scale = ldexpf(1.f, k);
+    inv = ldexpf(1.f, -k);
 }
 
 // ---- cross-lane reductions on DPP (full-rate VALU lane moves) ---------------

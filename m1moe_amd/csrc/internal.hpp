@@ -222,6 +222,18 @@ int launch_moe_decode(const FusedArgs& a, void* stream);
 // launcher (all kCuWorkgroups workgroups must be resident together).
 bool decode_cu_fits(int h, int E, int K, int I, int gs);
 int launch_moe_decode_cu(const FusedArgs& a, void* stream);
+// Workgroups of the per-CU kernel of this shape one CU of the current device
+// holds (the occupancy query; the smaller of the bf16 and f32 input
+// variants).  Returns a hipError_t as int.
+int decode_cu_blocks_per_cu(int h, int K, int I, int gs, int* blocks);
+// The decode kernel of a shape (fits: decode_cu_fits) on a device of `cus`
+// CUs holding `blocks` per-CU workgroups each: 1 = moe_decode_cu_kernel
+// (hidden 2048), 2 = moe_decode_cuw_kernel (hidden 4096), when all
+// kCuWorkgroups workgroups fit at once; else 0 = moe_decode_kernel.
+inline int decode_kernel_choice(bool fits, int h, int cus, int blocks) {
+    if (!fits || (int64_t)cus * blocks < kCuWorkgroups) return 0;
+    return h == 2048 ? 1 : 2;
+}
 // Bytes of one expert's repacked block (decode_cu.hip) and the launch that
 // builds a layer's repacked blocks from its canonical ones.
 uint64_t decode_copy_bytes(int h, int I, int gs);

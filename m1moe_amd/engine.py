@@ -105,6 +105,20 @@ def expert_offsets(shape: MoEShape) -> list:
     return [int(v) for v in out]
 
 
+DECODE_KERNELS = ("moe_decode_kernel", "moe_decode_cu_kernel", "moe_decode_cuw_kernel")
+
+
+def decode_kernel_for(shape: MoEShape, cus: int = 256, blocks_per_cu: int = 1) -> str:
+    """Name of the decode kernel the library runs for `shape` on a device of
+    `cus` CUs each holding `blocks_per_cu` per-CU workgroups
+    (m1moe_decode_kernel_for; host only)."""
+    k = ctypes.c_int32(-1)
+    lib = _lib.load()
+    check(lib.m1moe_decode_kernel_for(ctypes.byref(shape), int(cus), int(blocks_per_cu),
+                                      ctypes.byref(k)), "m1moe_decode_kernel_for")
+    return DECODE_KERNELS[k.value]
+
+
 def check_shape(shape: MoEShape) -> None:
     check(_lib.load().m1moe_check_shape(ctypes.byref(shape)), "m1moe_check_shape")
 

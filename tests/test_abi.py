@@ -198,3 +198,33 @@ def test_modelspec_loads_reference_config_format(tmp_path):
     sh = spec.shape()
     assert (sh.hidden, sh.num_experts, sh.top_k, sh.intermediate, sh.group_size,
             sh.num_layers, sh.norm_topk_prob) == (2048, 64, 8, 1024, 64, 16, 0)
+
+
+@pytest.mark.parametrize("shape,cus,blocks,want", [
+    (make_shape(2048, 64, 8, 1024, 64), 256, 1, "moe_decode_cu_kernel"),
+    (make_shape(2048, 64, 8, 1024, 64), 255, 1, "moe_decode_kernel"),   # one workgroup unplaced
+    (make_shape(2048, 64, 8, 1024, 64), 128, 2, "moe_decode_cu_kernel"),
+    (make_shape(2048, 64, 8, 1024, 64), 256, 0, "moe_decode_kernel"),   # does not fit a CU
+    (make_shape(2048, 64, 8, 1024, 64), 32, 1, "moe_decode_kernel"),    # a 32-CU partition
+    (make_shape(4096, 8, 2, 14336, 64, norm_topk_prob=True), 256, 1, "moe_decode_cuw_kernel"),
+    (make_shape(4096, 8, 2, 14336, 64, norm_topk_prob=True), 240, 1, "moe_decode_kernel"),
+    (make_shape(128, 8, 2, 64, 64), 256, 1, "moe_decode_kernel"),       # shape outside both
+    (make_shape(2048, 64, 8, 1024, 128), 256, 1, "moe_decode_cu_kernel"),
+])
+def test_decode_kernel_choice(shape, cus, blocks, want):
+    """The per-CU decode kernels wait for all 256 of their workgroups, so the
+    library picks them only when the device holds all 256 at once."""
+    from m1moe_amd.engine import decode_kernel_for
+    assert decode_kernel_for(shape, cus, blocks) == want
+
+
+def test_decode_kernel_choice_rejects_bad_arguments():
+    lib = _lib.load()
+    k = ctypes.c_int32()
+    s = make_shape(2048, 64, 8, 1024, 64)
+    assert lib.m1moe_decode_kernel_for(ctypes.byref(s), -1, 1, ctypes.byref(k)) == \
+        _lib.M1MOE_ERR_INVALID
+    assert lib.m1moe_decode_kernel_for(ctypes.byref(s), 256, 1, None) == _lib.M1MOE_ERR_INVALID
+    bad = make_shape(100, 8, 2, 64, 64)
+    assert lib.m1moe_decode_kernel_for(ctypes.byref(bad), 256, 1, ctypes.byref(k)) == \
+        _lib.M1MOE_ERR_INVALID

@@ -212,7 +212,7 @@ def test_prefill_takes_large_scales():
         c.close()
 
 
-def test_prefill_reports_a_non_finite_scale():
+def test_prefill_upload_refuses_a_non_finite_scale():
     c = make_case("tiny", seed=9)
     try:
         s = c.shape
@@ -220,11 +220,15 @@ def test_prefill_reports_a_non_finite_scale():
         img = c.images[0].copy()
         _set_groups(img, 3 * c.ctx.expert_bytes + offs[1], 7, s.hidden // s.group_size, 1, 1,
                     0x7F80)  # +inf
-        say("upload with an infinite gate scale (expect a device error)")
-        c.ctx.upload_layer_experts(0, img)
+        say("upload with an infinite gate scale (expect the upload to refuse it)")
         with pytest.raises(m.M1MoEError, match="non-finite"):
-            c.ctx.sync()
-        c.ctx.sync()  # the flag was cleared
+            c.ctx.upload_layer_experts(0, img)
+        c.ctx.sync()  # nothing left for the next sync
+        # the layer stays unloaded until a good image arrives
+        with pytest.raises(m.M1MoEError, match="never uploaded"):
+            MoEBlock(c.ctx).prefill(0, 1, c.ctx.alloc(2 * s.hidden), "bf16", None,
+                                    c.ctx.alloc(4 * s.hidden))
+        c.ctx.upload_layer_experts(0, c.images[0])
     finally:
         c.close()
 

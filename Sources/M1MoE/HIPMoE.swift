@@ -128,9 +128,19 @@ public final class HIPDecoder {
     private let moe: HIPMoE
     private var dec: m1moe_dec_t?
     private var dTok: UnsafeMutableRawPointer?
+    private var dLogits: UnsafeMutableRawPointer?
+    private var logits: [Float]
+
+    /// InferenceEngine.seqPos (InferenceEngine.swift:25): the next position,
+    /// read from the device (m1moe_dec_position waits for the context stream).
+    public var seqPos: Int {
+        var p: Int32 = 0
+        return m1moe_dec_position(dec, &p) == 0 ? Int(p) : -1
+    }
 
     public init(moe: HIPMoE, weights: WeightStore) throws {
         self.moe = moe
+        self.logits = [Float](repeating: 0, count: moe.spec.vocabSize)
         let spec = moe.spec
         let att = spec.attention
         var shape = m1moe_dec_shape(
@@ -164,20 +174,70 @@ public final class HIPDecoder {
             }
         }
         try hipCheck(m1moe_alloc(moe.ctx, 16, &dTok))
+        try hipCheck(m1moe_alloc(moe.ctx, UInt64(4 * V), &dLogits))
     }
 
     deinit { m1moe_dec_destroy(dec) }   // before the HIPMoE's context, which `moe` keeps alive
 
-    /// InferenceEngine.forward(token:) at temperature 0: one call and one
-    /// 4-byte read-back.
-    public func forward(token: UInt32) throws -> UInt32 {
+    /// InferenceEngine.forward(token:temperature:topP:) (InferenceEngine.swift:
+    /// 125-156).  At temperature <= 0 the greedy token is the step's own
+    /// device-side argmax: one call and one 4-byte read-back.  Otherwise the
+    /// step's f32 logits are read back and sampled on the host as the
+    /// reference does (sampleToken below).
+    @discardableResult
+    public func forward(token: UInt32, temperature: Float = 0, topP: Float = 1) throws -> UInt32 {
         var t = Int32(bitPattern: token)
         let p = dTok!.assumingMemoryBound(to: Int32.self)
+        let sampled = temperature > 0
         try hipCheck(m1moe_copy_h2d(moe.ctx, dTok, &t, 4))
-        try hipCheck(m1moe_dec_step(dec, p, p, nil))
-        try hipCheck(m1moe_copy_d2h(moe.ctx, &t, dTok, 4))
+        try hipCheck(m1moe_dec_step(dec, p, p,
+                                    sampled ? dLogits!.assumingMemoryBound(to: Float.self) : nil))
+        if sampled {
+            try logits.withUnsafeMutableBytes {
+                try hipCheck(m1moe_copy_d2h(moe.ctx, $0.baseAddress, dLogits, UInt64($0.count)))
+            }
+        } else {
+            try hipCheck(m1moe_copy_d2h(moe.ctx, &t, dTok, 4))
+        }
         try hipCheck(m1moe_sync(moe.ctx))   // reports a token outside the vocabulary or a full cache
-        return UInt32(bitPattern: t)
+        if !sampled { return UInt32(bitPattern: t) }
+        return logits.withUnsafeBufferPointer {
+            HIPDecoder.sampleToken(logits: $0.baseAddress!, count: $0.count,
+                                   temperature: temperature, topP: topP)
+        }
+    }
+
+    /// sampleToken (InferenceEngine.swift:550-575) on the host, in the same
+    /// f32 order: exp((l - max) / T) with a sequential sum, the nucleus in
+    /// descending probability until its running sum reaches topP, then a
+    /// uniform draw walked down the nucleus.  Equal probabilities keep the
+    /// lower index first (the reference's sort leaves their order open).
+    static func sampleToken(logits: UnsafePointer<Float>, count: Int,
+                            temperature: Float, topP: Float) -> UInt32 {
+        if temperature <= 0 {
+            var best = 0; var bestV = logits[0]
+            for i in 1 ..< count where logits[i] > bestV { bestV = logits[i]; best = i }
+            return UInt32(best)
+        }
+        var probs = [Float](repeating: 0, count: count)
+        var mx = logits[0]
+        for i in 1 ..< count where logits[i] > mx { mx = logits[i] }
+        var sum: Float = 0
+        for i in 0 ..< count { probs[i] = expf((logits[i] - mx) / temperature); sum += probs[i] }
+        let inv = 1.0 / sum
+        for i in 0 ..< count { probs[i] *= inv }
+        let order = probs.indices.sorted {
+            probs[$0] > probs[$1] || (probs[$0] == probs[$1] && $0 < $1)
+        }
+        var cumul: Float = 0
+        var nucleus: [Int] = []
+        for idx in order {
+            nucleus.append(idx); cumul += probs[idx]
+            if cumul >= topP { break }
+        }
+        var r = Float.random(in: 0 ..< cumul)
+        for idx in nucleus { r -= probs[idx]; if r <= 0 { return UInt32(idx) } }
+        return UInt32(nucleus.last!)
     }
 
     /// The bench loop (Sources/bench/main.swift:136-163) with no host round

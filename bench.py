@@ -390,6 +390,7 @@ def bench_decoder(args, m, synth) -> int:
                                    wl.rope_theta, wl.rms_eps, tensors, images, routers)
         dec.reset()
         worst, n, t_cpu, tok_ok = 0.0, 0, 0.0, True
+        orc.set_scalar(True)  # the lane-by-lane matvec restatement, as the cfg0 baseline
         while n < P and (n == 0 or t_cpu < args.cpu_seconds):
             g_tok, g_lg = dec.forward(int(prompt[n]), return_logits=True)
             t1 = time.perf_counter()
@@ -400,6 +401,7 @@ def bench_decoder(args, m, synth) -> int:
             top2 = np.sort(w_lg.astype(np.float64))[-2:]
             tok_ok &= g_tok == w_tok or bool(top2[1] - top2[0] < 1e-2)
             n += 1
+        orc.set_scalar(False)
         parity = {"steps_checked": n, "logits_rel_l2_max": worst, "greedy_tokens_agree": tok_ok}
         log(f"parity over {n} steps: logits rel L2 max {worst:.2e}, tokens agree {tok_ok}")
         if worst > 1e-2 or not tok_ok:

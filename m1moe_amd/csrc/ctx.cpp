@@ -259,6 +259,7 @@ uint64_t prefill_scratch_packed(const m1moe::Geom& g, int32_t T) {
 // capture, and a graph captured before a call with a larger T must be
 // captured again.
 int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
+    ctx->capture_uses_scratch = true;
     if (T <= ctx->pf_cap) return M1MOE_OK;
     if (int32_t rc = m1moe::refuse_growth_in_capture(ctx->stream, "the prefill scratch")) return rc;
     void** bufs[9] = {(void**)&ctx->pf_xq,   (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
@@ -798,6 +799,7 @@ int32_t m1moe_graph_begin(m1moe_ctx_t ctx) {
     int32_t rc;
     if ((rc = check_ctx(ctx)) || (rc = set_device(ctx))) return rc;
     HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capture_uses_scratch = false;
     return M1MOE_OK;
 }
 
@@ -820,6 +822,7 @@ int32_t m1moe_graph_end(m1moe_ctx_t ctx, m1moe_graph_t* out) {
     }
     gr->owner = ctx;
     gr->scratch_gen = ctx->scratch_gen;
+    gr->uses_scratch = ctx->capture_uses_scratch;
     *out = gr;
     return M1MOE_OK;
 }
@@ -830,7 +833,7 @@ int32_t m1moe_graph_launch(m1moe_ctx_t ctx, m1moe_graph_t graph) {
     if (!graph) return fail(M1MOE_ERR_INVALID, "null graph");
     if (graph->owner != ctx)
         return fail(M1MOE_ERR_INVALID, "the graph was captured on another context");
-    if (graph->scratch_gen != ctx->scratch_gen)
+    if (graph->uses_scratch && graph->scratch_gen != ctx->scratch_gen)
         return fail(M1MOE_ERR_INVALID,
                     "a scratch buffer was reallocated (a call with a larger size) since the "
                     "graph was captured, so it holds freed addresses; capture it again");

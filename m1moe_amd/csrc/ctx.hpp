@@ -24,6 +24,7 @@ struct m1moe_graph {
     hipGraphExec_t exec;
     m1moe_ctx_t owner;       // the context whose stream was captured
     uint64_t scratch_gen;    // owner->scratch_gen when the capture ended
+    bool uses_scratch;       // a captured call used the context's growable scratch
 };
 
 struct m1moe_ctx {
@@ -42,6 +43,9 @@ struct m1moe_ctx {
     // bumped whenever a scratch buffer is reallocated: a graph captured
     // before then holds the freed addresses and is refused at launch
     uint64_t scratch_gen = 0;
+    // set by every call that uses the growable scratch (prefill, decoder
+    // prefill, attention), cleared when a capture begins
+    bool capture_uses_scratch = false;
     uint8_t* arena = nullptr;        // [L][E] expert blocks
     uint16_t* routers = nullptr;     // [L][E][h] bf16
     float* biases = nullptr;         // [L][E]

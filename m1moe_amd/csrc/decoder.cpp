@@ -24,6 +24,7 @@ int32_t check_f32_vec(const void* p, const char* what) { return check_dev_ptr(p,
 constexpr int kAttnCounters = 1024;  // >= num_heads (num_heads * 64 <= 65536)
 
 int32_t ensure_attn_scratch(m1moe_ctx_t ctx, uint64_t floats) {
+    ctx->capture_uses_scratch = true;
     if (!ctx->attn_cnt || floats > ctx->attn_part_floats)
         if (int32_t rc = refuse_growth_in_capture(ctx->stream, "the attention scratch")) return rc;
     if (!ctx->attn_cnt) {
@@ -516,6 +517,7 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
     int32_t rc;
     m1moe_ctx_t ctx = dec->moe;
     if ((rc = set_device(ctx))) return rc;
+    ctx->capture_uses_scratch = true;
     const int32_t h = dec->h, qd = dec->qd, kvd = dec->kvd, hd = dec->sh.head_dim;
     const int32_t N = qd + 2 * kvd;
     if (T > dec->pf_cap) {

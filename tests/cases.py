@@ -1,6 +1,7 @@
 """Shared set-up of seeded MoE-layer cases for the GPU parity tests."""
 from __future__ import annotations
 
+import os
 import sys
 from dataclasses import dataclass, field
 
@@ -19,10 +20,21 @@ def rel_l2(got, want) -> float:
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-300))
 
 
+_PROGRESS = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpurun_out")
+
+
 def say(msg: str) -> None:
-    """Names the case before a GPU step (flushed, in case the step never returns)."""
+    """Names the case before a GPU step (flushed, in case the step never
+    returns); also appended to gpurun_out/test_progress.log when that folder
+    exists, so a long test shows progress while pytest holds its output."""
     print(f"[case] {msg}", flush=True)
     sys.stdout.flush()
+    if os.path.isdir(_PROGRESS):
+        try:
+            with open(os.path.join(_PROGRESS, "test_progress.log"), "a") as f:
+                f.write(f"[case] {msg}\n")
+        except OSError:
+            pass
 
 
 @dataclass

@@ -699,3 +699,64 @@ def test_decoder_rejects_missing_weights_and_bad_shapes():
         dec.close()
     finally:
         ctx.close()
+
+
+@pytest.mark.timeout(1200)
+def test_decoder_mixtral_32_layers_2048_prompt_64_greedy():
+    """cfg4 at full depth and length (Sources/bench/main.swift:133-185): 32
+    Mixtral-width layers, a 2048-token prompt in one batch, then 64 greedy
+    steps.  The oracle would take hours here, so the batched prefill (f16
+    MFMA operands) is held against the same prompt fed token by token
+    through the decode step, which the tests above pin to the oracle at
+    ~1e-7: the last position's logits within 1e-2 relative L2 (the greedy
+    tokens may differ only inside that margin).  Every logit is finite, and
+    a second prefill-then-generate run is bit-identical."""
+    wl = synth.DECODERS["cfg4"]
+    L, P, G, seed = wl.num_layers, 2048, 64, 404
+    shape = wl.moe.shape(L)
+    say(f"cfg4 full depth: {L} layers, prompt {P}, {G} greedy steps")
+    ctx = m.HIPContext(shape)
+    dec = None
+    try:
+        dec = Decoder(ctx, wl.dec_shape(P + G + 1))
+        dec.upload_all(lambda which, l: synth.dense_weight(wl, seed, which, l))
+        for l in range(L):
+            ctx.upload_layer_experts(l, synth.layer_image(shape, seed, l))
+            ctx.upload_router(l, synth.router(shape, seed, l))
+        say("  weights uploaded")
+        prompt = synth.prompt_tokens(wl, seed, P)
+        runs = []
+        for run in range(2):
+            dec.reset()
+            tok, lg = dec.prefill(prompt, return_logits=True)
+            toks, lgs = [tok], [lg]
+            for _ in range(G):
+                tok, lg = dec.forward(tok, return_logits=True)
+                toks.append(tok)
+                lgs.append(lg)
+            assert all(np.isfinite(x).all() for x in lgs), f"run {run}: non-finite logits"
+            assert dec.position() == P + G
+            runs.append((toks, lgs))
+            say(f"  run {run}: prefill + {G} greedy steps, tokens {toks[:6]}...")
+        assert runs[0][0] == runs[1][0]
+        for a, b in zip(runs[0][1], runs[1][1]):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        # the same prompt through the decode step, token by token
+        seq = ctx.to_device(np.concatenate([prompt, np.zeros(1, np.int32)]).astype(np.int32))
+        lgbuf = ctx.alloc(4 * wl.vocab)
+        dec.reset()
+        for i in range(P):
+            dec.step_seq(seq, P, P + 1, lgbuf if i == P - 1 else None)
+            if i % 512 == 511:
+                ctx.sync()
+                say(f"  token by token: {i + 1}/{P}")
+        ctx.sync()
+        step_tok = int(seq.download(np.int32)[P])
+        step_lg = lgbuf.download(np.float32)
+        rel = check_step(runs[0][0][0], runs[0][1][0], step_tok, step_lg,
+                         "batched prefill vs token-by-token decode at position 2047")
+        say(f"  last-position logits rel L2 (batched prefill vs decode steps): {rel:.3e}")
+    finally:
+        if dec is not None:
+            dec.close()
+        ctx.close()

@@ -140,6 +140,7 @@ m1moe::FusedArgs fused_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32
     a.cu_seen = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_cu_seen);
     a.cu_cnt = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_cu_cnt);
     a.cu_part = reinterpret_cast<uint32_t*>(ctx->sync + ctx->sync_cu_part);
+    a.xl = reinterpret_cast<unsigned long long*>(ctx->sync + ctx->sync_xl);
     a.dec_base = ctx->dec ? ctx->dec + (uint64_t)layer * g.E * ctx->dec_bytes : nullptr;
     a.dec_bytes = ctx->dec_bytes;
     a.err = ctx->err;
@@ -524,8 +525,10 @@ int32_t m1moe_create(int32_t device, const m1moe_moe_shape* s, m1moe_ctx_t* out)
         c->sync_cu_part =
             c->sync_cu_cnt + (uint64_t)m1moe::kCuRep * m1moe::kCuParts * m1moe::kCntStride * 4;
         // per-CU kernels: [256 row blocks][256 sources][8 or 16 rows] f32 partials
-        c->sync_bytes = c->sync_cu_part + (uint64_t)m1moe::kCuWorkgroups *
-                                              m1moe::kCuWorkgroups * (g.h > 2048 ? 16 : 8) * 4;
+        c->sync_xl = c->sync_cu_part + (uint64_t)m1moe::kCuWorkgroups *
+                                           m1moe::kCuWorkgroups * (g.h > 2048 ? 16 : 8) * 4;
+        // per-CU kernels: XCD-local logit slots, [8][kRepStride] u64
+        c->sync_bytes = c->sync_xl + (uint64_t)8 * m1moe::kRepStride * 8;
     }
     {
         int cus = 0;

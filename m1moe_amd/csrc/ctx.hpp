@@ -59,9 +59,9 @@ struct m1moe_ctx {
     uint32_t* counters = nullptr;    // [cap]
     float* act = nullptr;            // [K][I]
     uint8_t* sync = nullptr;         // decode hand-off state: slots | gu_cnt | seen |
-                                     // cu_seen | cu_cnt | cu_part
+                                     // cu_seen | cu_cnt | cu_part | xl
     uint64_t sync_bytes = 0, sync_gu_cnt = 0, sync_seen = 0;
-    uint64_t sync_cu_seen = 0, sync_cu_cnt = 0, sync_cu_part = 0;
+    uint64_t sync_cu_seen = 0, sync_cu_cnt = 0, sync_cu_part = 0, sync_xl = 0;
     // decode launches use the one-workgroup-per-CU kernel (decode_cu.hip):
     // the shape fits it and the device has the CUs to hold all its
     // workgroups at once.  That kernel reads a repacked copy of every expert

@@ -11,9 +11,9 @@
 // hidden width 2048 with K * I = 8192 or 16384 (OLMoE: K = 8, I = 1024).
 //
 // Every workgroup g does the same four things:
-//   1. router: g < E * copies computes logit g % E (exact bf16*x products
-//      summed in f64, rounded once) and publishes it (several copies of each
-//      logit, so a slow producer does not hold every workgroup); every
+//   1. router: every XCD computes all E logits (exact bf16*x products
+//      summed in f64, rounded once; workgroup j of an XCD takes experts
+//      j + 32 i) and hands them to its own workgroups through its L2; every
 //      workgroup polls the logits and ranks them (descending, ties to the
 //      lower index);
 //   2. gate/up: 8 * UG consecutive act rows of one slot (UG rows per wave,
@@ -36,8 +36,10 @@
 // lane instead of sixteen 4-byte ones), the down scales/biases group-major.
 // The gate/up weights are read from the canonical arena.
 //
-// Hand-off.  Published logits are (launch number, value) pairs in kLogitRep
-// replicas.  Partial sums carry the parity of the launch number in their
+// Hand-off.  Published logits are (launch number, value) pairs: in the
+// XCD's local slots (plain stores, read with non-temporal loads through the
+// XCD's L2) and in one global replica per XCD (sc1), read only when the local
+// slots stay incomplete (workgroups not placed on the XCDs in turn).  Partial sums carry the parity of the launch number in their
 // lowest mantissa bit: the reader checks every value it loads, reads the
 // stale ones again until all are current, and clears the bit (the value used
 // is the same in every launch: a relative change below 2^-23), so no counter
@@ -99,7 +101,32 @@ constexpr int kRows = kH / kNG;     // output rows per workgroup
 constexpr int kMaxE = 256;
 constexpr int kMaxK = 8;
 constexpr int kChunkWords = 34;     // prepared act chunk: 16 hi pairs, 16 lo pairs, sum, 2^-e
-constexpr int kLogitCopies = 1;     // workgroups computing each router logit
+constexpr int kMaxLoc = 8;          // router logits per workgroup (E <= 256, 32 per XCD)
+constexpr int kLocalPolls = 64;     // XCD-local logit polls before the global replicas are read
+
+// The XCD (and L2) the calling workgroup runs on.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 7u;
+}
+
+// XCD-local hand-off words: a plain store lands in the XCD's L2 (the CU's L1
+// writes through), and a non-temporal load reads that L2 without the CU's
+// L1, so workgroups of one XCD see each other's stores in ~0.25 us (an sc1
+// store and load pair, which goes through memory and works between XCDs,
+// takes ~0.6 us).  Other XCDs cannot rely on seeing such a store.
+__device__ __forceinline__ void st_l2_u64(unsigned long long* p, unsigned long long v) {
+    asm volatile("global_store_dwordx2 %0, %1, off" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ unsigned long long ld_l2_u64(const unsigned long long* p) {
+    unsigned long long v;
+    asm volatile("global_load_dwordx2 %0, %1, off nt\n\ts_waitcnt vmcnt(0)"
+                 : "=v"(v)
+                 : "v"(p)
+                 : "memory");
+    return v;
+}
 
 static_assert(kRows == 8 && kT * 4 == kH, "one x quad and four down rows per thread");
 
@@ -109,7 +136,7 @@ struct CuLDS {
     alignas(16) uint32_t xp[2][36]; // this workgroup's prepared act chunks
     alignas(16) uint32_t xq[64][36];// gate/up input chunk of each lane: 16 hi pairs, 16 lo
                                     // pairs, sum, 2^-e (prepared once per workgroup)
-    double lp[kW];                  // wave partials of this workgroup's logit
+    double lp[kMaxLoc][kW];         // wave partials of this workgroup's logits
     float act[64];                  // this workgroup's act rows
     float y[kMaxK][kRows];          // per slot: reduced down outputs of rows 8g .. 8g+7
     int idx[kMaxK];                 // expert of each slot (-1: none)
@@ -145,6 +172,50 @@ __device__ __forceinline__ void rank_cu(int t, int E, int K, S& s) {
     if (i < E && q == P - 1 && (int)cnt < K) s.idx[(int)cnt] = i;
 }
 
+// Router logits (InferenceEngine.swift:490-500) computed on every XCD: the
+// workgroup with local index j = g / 8 (one per workgroup of an XCD when the
+// workgroups are placed on the XCDs in turn) takes experts j + 32 i < E, each
+// the exact products of its bf16 router row and x summed in f64 (NX
+// consecutive columns per thread, a fixed wave tree, the waves in order) and
+// rounded once, plus the optional bias.  Stage 1 (before the barrier that
+// follows): the wave partials into lp.  Stage 2: published as (launch tag,
+// value) to the XCD's local slots (plain stores) and to the XCD's global
+// replica (sc1 stores).
+template <int NX, class RW>
+__device__ __forceinline__ void logits_partial(int nloc, int wave, int lane, const RW (&rw)[kMaxLoc],
+                                               const float (&xv)[NX], double (*lp)[kW]) {
+#pragma unroll
+    for (int i = 0; i < kMaxLoc; ++i) {
+        if (i < nloc) {
+            const uint32_t* r = reinterpret_cast<const uint32_t*>(&rw[i]);
+            double acc = 0.0;
+#pragma unroll
+            for (int k = 0; k < NX / 2; ++k) {
+                acc += (double)__uint_as_float(r[k] << 16) * (double)xv[2 * k];
+                acc += (double)__uint_as_float(r[k] & 0xffff0000u) * (double)xv[2 * k + 1];
+            }
+            acc = wave_sum_f64_last(acc);
+            if (lane == 63) lp[i][wave] = acc;
+        }
+    }
+}
+
+__device__ __forceinline__ void logits_publish(const FusedArgs& a, int t, int jl, int nloc,
+                                               uint32_t tag, const double (*lp)[kW]) {
+    if (t < nloc) {
+        const int e = jl + 32 * t;
+        double sum = lp[t][0];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) sum += lp[t][w];
+        float l = (float)sum;
+        if (a.bias) l = l + a.bias[e];
+        const unsigned long long u = ((unsigned long long)tag << 32) | __float_as_uint(l);
+        const uint32_t x = xcc_id();
+        st_l2_u64(a.xl + (size_t)x * kRepStride + e, u);
+        st_u64(a.slots + (size_t)x * kRepStride + e, u);
+    }
+}
+
 // Obtains the routing: the given one, or the published logits (wave 0 polls
 // replica g % kLogitRep) ranked by all threads: expert i's rank is the
 // number of experts ahead of it (larger logit, or equal logit and lower
@@ -170,7 +241,11 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
         return;
     }
     if (wave == 0) {
-        const unsigned long long* rep = a.slots + (size_t)(g % kLogitRep) * kRepStride;
+        // this XCD's own slots first (its workgroups compute every logit, see
+        // publish_logits); after kLocalPolls rounds, for workgroups placed on
+        // the XCDs other than in turn, the global replicas, one per XCD,
+        // rotating over them (every logit is in at least one)
+        const unsigned long long* loc = a.xl + (size_t)xcc_id() * kRepStride;
         const int nj = (E + 63) >> 6;  // logits per lane (wave-uniform)
         float v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         bool have[4];
@@ -178,11 +253,16 @@ __device__ void route_cu(const FusedArgs& a, int g, int t, int wave, int lane, u
         for (int j = 0; j < 4; ++j) have[j] = (lane + 64 * j >= E);
         bool ok = true;
         for (int it = 0;; ++it) {
-            // every missing logit of the lane is requested before any is examined
+            const bool local = it < kLocalPolls;
             unsigned long long u[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                u[j] = (j < nj && !have[j]) ? ld_u64(rep + lane + 64 * j) : 0ull;
+            for (int j = 0; j < 4; ++j) {
+                const int e = lane + 64 * j;
+                u[j] = 0ull;
+                if (j < nj && !have[j])
+                    u[j] = local ? ld_l2_u64(loc + e)
+                                 : ld_u64(a.slots + (size_t)((it + e) & 7) * kRepStride + e);
+            }
             bool all = true;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -610,12 +690,9 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     DTR_WG(0);
     const int g = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int E = a.E, K = a.K, I = a.I;
-    // logit g % E is computed by every workgroup g < E * copies (identical
-    // values, written to the same words): the pollers wait for the first
-    // copy of each logit, not for the slowest producer
-    const int copies = min(kLogitCopies, kNG / E);
-    const bool producer = !a.given_idx && g < E * copies;
-    const int le = g % E;
+    // router logits jl + 32 i < E, computed on every XCD (logits_partial)
+    const int jl = g >> 3;
+    const int nloc = (a.given_idx || jl >= E) ? 0 : (E - jl + 31) / 32;
 
     // ---- input, launch number, router row --------------------------------------
     if (t == 0) s.tag = ld_u32(a.cu_seen + g) + 1u;
@@ -638,8 +715,11 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
         xv[3] = q.w;
         if (normed) nw = *reinterpret_cast<const uint2*>(a.x_norm_w + 4 * t);
     }
-    uint2 rw = make_uint2(0u, 0u);
-    if (producer) rw = *reinterpret_cast<const uint2*>(a.router + (size_t)le * kH + 4 * t);
+    uint2 rw[kMaxLoc];
+#pragma unroll
+    for (int i = 0; i < kMaxLoc; ++i)
+        rw[i] = i < nloc ? *reinterpret_cast<const uint2*>(a.router + (size_t)(jl + 32 * i) * kH + 4 * t)
+                         : make_uint2(0u, 0u);
     if (normed && wave == 0) {
         const float r = input_rms(a, lane);
         if (lane == 0) s.rms = r;
@@ -653,25 +733,10 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
         xv[3] = xv[3] * rms * __uint_as_float(nw.y & 0xffff0000u);
     }
     *reinterpret_cast<float4*>(&s.x[(t >> 3) * 36 + (t & 7) * 4]) = float4{xv[0], xv[1], xv[2], xv[3]};
-    if (producer) {  // InferenceEngine.swift:490-500, exact products summed in f64
-        double acc = (double)__uint_as_float(rw.x << 16) * (double)xv[0];
-        acc += (double)__uint_as_float(rw.x & 0xffff0000u) * (double)xv[1];
-        acc += (double)__uint_as_float(rw.y << 16) * (double)xv[2];
-        acc += (double)__uint_as_float(rw.y & 0xffff0000u) * (double)xv[3];
-        acc = wave_sum_f64_last(acc);
-        if (lane == 63) s.lp[wave] = acc;
-    }
+    logits_partial<4>(nloc, wave, lane, rw, xv, s.lp);
     __syncthreads();
     const uint32_t tag = s.tag, parity = tag & 1u;
-    if (producer && t < kLogitRep) {
-        double sum = s.lp[0];
-#pragma unroll
-        for (int w = 1; w < kW; ++w) sum += s.lp[w];
-        float l = (float)sum;
-        if (a.bias) l = l + a.bias[le];
-        st_u64(a.slots + (size_t)t * kRepStride + le,
-               ((unsigned long long)tag << 32) | __float_as_uint(l));
-    }
+    logits_publish(a, t, jl, nloc, tag, s.lp);
     DTR_WG(1);
 
     // the gate/up input, chunk c of x for lane c of every wave: prepared once
@@ -879,7 +944,7 @@ struct CuwLDS {
     alignas(16) float v[kMaxE];         // logits
     alignas(16) uint32_t xq[128][36];   // prepared gate/up input chunks (hi, lo, sum, 2^-e)
     alignas(16) uint32_t xp[kWChunks][36];  // this workgroup's prepared act chunks
-    double lp[kW];
+    double lp[kMaxLoc][kW];
     float act[kWRows];
     float y[kMaxKW][kRowsW];
     int idx[kMaxK];
@@ -984,7 +1049,8 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
     const int E = a.E, K = a.K, I = a.I;
     const int wps = I / kWRows;               // working workgroups per slot
     const int nwork = K * wps;
-    const bool producer = !a.given_idx && g < E;
+    const int jl = g >> 3;  // router logits jl + 32 i < E (logits_partial)
+    const int nloc = (a.given_idx || jl >= E) ? 0 : (E - jl + 31) / 32;
 
     // ---- input, launch number, router row --------------------------------------------
     if (t == 0) s.tag = ld_u32(a.cu_seen + g) + 1u;
@@ -1008,8 +1074,11 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
         xv[4] = q1.x; xv[5] = q1.y; xv[6] = q1.z; xv[7] = q1.w;
         if (normed) nw = *reinterpret_cast<const uint4*>(a.x_norm_w + 8 * t);
     }
-    uint4 rw = make_uint4(0u, 0u, 0u, 0u);
-    if (producer) rw = *reinterpret_cast<const uint4*>(a.router + (size_t)g * kHW + 8 * t);
+    uint4 rw[kMaxLoc];
+#pragma unroll
+    for (int i = 0; i < kMaxLoc; ++i)
+        rw[i] = i < nloc ? *reinterpret_cast<const uint4*>(a.router + (size_t)(jl + 32 * i) * kHW + 8 * t)
+                         : make_uint4(0u, 0u, 0u, 0u);
     if (normed && wave == 0) {
         const float r = input_rms(a, lane);
         if (lane == 0) s.rms = r;
@@ -1029,28 +1098,10 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
         *reinterpret_cast<float4*>(dx) = float4{xv[0], xv[1], xv[2], xv[3]};
         *reinterpret_cast<float4*>(dx + 4) = float4{xv[4], xv[5], xv[6], xv[7]};
     }
-    if (producer) {  // InferenceEngine.swift:490-500, exact products summed in f64
-        const uint32_t rr[4] = {rw.x, rw.y, rw.z, rw.w};
-        double acc = 0.0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc += (double)__uint_as_float(rr[i] << 16) * (double)xv[2 * i];
-            acc += (double)__uint_as_float(rr[i] & 0xffff0000u) * (double)xv[2 * i + 1];
-        }
-        acc = wave_sum_f64_last(acc);
-        if (lane == 63) s.lp[wave] = acc;
-    }
+    logits_partial<8>(nloc, wave, lane, rw, xv, s.lp);
     __syncthreads();
     const uint32_t tag = s.tag, parity = tag & 1u;
-    if (producer && t < kLogitRep) {
-        double sum = s.lp[0];
-#pragma unroll
-        for (int w = 1; w < kW; ++w) sum += s.lp[w];
-        float l = (float)sum;
-        if (a.bias) l = l + a.bias[g];
-        st_u64(a.slots + (size_t)t * kRepStride + g,
-               ((unsigned long long)tag << 32) | __float_as_uint(l));
-    }
+    logits_publish(a, t, jl, nloc, tag, s.lp);
     DTR_WG(1);
     // the gate/up input chunks (lane l of every wave uses chunks l and l + 64),
     // prepared once per workgroup by waves 1 and 2 while wave 0 awaits the logits

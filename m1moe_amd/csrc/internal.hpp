@@ -64,6 +64,7 @@ struct FusedArgs {
     // every workgroup counts its own launches in seen[wg], so all workgroups
     // agree on the launch number ("tag") without communicating.
     unsigned long long* slots;   // [kLogitRep][kRepStride] logits tagged with the launch number
+    unsigned long long* xl;      // [8 XCDs][kRepStride] the same, XCD-local (decode_cu.hip)
     float* act;                  // [K][I] silu(gate) * up
     uint32_t* gu_cnt;            // [kNRep][n_cnt] monotonic counters of finished gate/up
                                  // tiles, kCntStride apart

@@ -924,8 +924,9 @@ int launch_ug(const FusedArgs& a, hipStream_t st) {
 // The same one-launch, one-workgroup-per-CU scheme for hidden width 4096 and
 // top-K <= 2: working workgroup g < K * I / 128 owns 128 consecutive act rows
 // of one slot (4 chunks of 32; wave w: rows 16 w .. 16 w + 15), streams their
-// gate/up rows in batches of 4 rows x one 32-column chunk per lane (two
-// batches in flight), then its down columns chunk by chunk (rows t + 512 r, r
+// gate/up rows in batches of 4 rows x one 32-column chunk per lane (one
+// batch in flight while the previous one is multiplied), then its down
+// columns chunk by chunk (rows t + 512 r, r
 // < 8, per thread), and stores 4096 partial sums.  Every workgroup (working
 // or not) then reduces output rows 16 g .. 16 g + 15 over the working
 // workgroups of each slot, in a fixed order, and combines the slots.
@@ -936,7 +937,8 @@ constexpr int kRPT = kHW / kT;      // down rows per thread
 constexpr int kWRows = 128;         // act rows per working workgroup
 constexpr int kWChunks = kWRows / 32;
 constexpr int kMaxKW = 2;
-constexpr int kWInFlight = 2;   // gate/up batches in flight per wave
+constexpr int kWInFlight = 1;   // gate/up batches in flight per wave (two: 43.9 against
+                                // 43.3 us per cfg2 layer-token, more queueing in the memory system)
 constexpr int kWEarlyDown = 2;  // down chunks requested during the last batches
 
 struct CuwLDS {
@@ -1145,7 +1147,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cuw_kernel(FusedArgs a) {
     const int cg0 = r0 / 32;
     if (eg >= 0) {
         // batch b: row quad b / 2 of this wave's 16 rows, chunk half b % 2 (lane
-        // l: chunk l, then chunk l + 64); two batches in flight
+        // l: chunk l, then chunk l + 64); kWInFlight batches in flight
         const int wrow = r0 + 16 * wave;
         GUBatchW Bq[kWInFlight];
 #pragma unroll

@@ -256,8 +256,8 @@ int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T,
  * scratch is a fixed 64 MiB static device array per GPU (looked up by
  * m1moe_create, held until the process ends) instead of the context's
  * buffers that m1moe_moe_prefill grows; a T whose scratch would not fit is
- * rejected with M1MOE_ERR_INVALID naming the largest T that fits (779
- * tokens at hidden 2048, 8 x 1024 experts; 682 at hidden 4096,
+ * rejected with M1MOE_ERR_INVALID naming the largest T that fits (776
+ * tokens at hidden 2048, 8 x 1024 experts; 676 at hidden 4096,
  * 2 x 14336).  Every call on one GPU shares that array, so calls that overlap
  * on one GPU (two streams, or two contexts on one device) race. */
 int32_t m1moe_moe_prefill_noalloc(m1moe_ctx_t ctx, int32_t layer, int32_t T,

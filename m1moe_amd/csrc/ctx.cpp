@@ -231,10 +231,10 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
     return launched(m1moe::launch_router_topk(r, ctx->stream), "router_topk");
 }
 
-// Sizes in bytes of the nine prefill scratch buffers for T tokens, in the
+// Sizes in bytes of the kPfBufs prefill scratch buffers for T tokens, in the
 // order of PrefillArgs: xq, xinv, pos, sorted_tok, expert_off, tile_off,
-// tile_desc, act, y.
-void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[9]) {
+// tile_desc, act, y, act_exp, pair_scale, act_flag.
+void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[m1moe::kPfBufs]) {
     const uint64_t t = (uint64_t)T, P = t * (uint64_t)g.K, E = (uint64_t)g.E;
     sz[0] = t * g.h * 2;
     sz[1] = t * 4;
@@ -245,11 +245,14 @@ void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[9]) {
     sz[6] = (P / m1moe::kPfTN + E + 1) * 16;
     sz[7] = P * g.I * 2;
     sz[8] = P * g.h * 4;
+    sz[9] = P * (g.I / 32);
+    sz[10] = P * 4;
+    sz[11] = 4;
 }
 
-// Bytes of the nine buffers carved from one block, each 256-byte aligned.
+// Bytes of the kPfBufs buffers carved from one block, each 256-byte aligned.
 uint64_t prefill_scratch_packed(const m1moe::Geom& g, int32_t T) {
-    uint64_t sz[9], total = 0;
+    uint64_t sz[m1moe::kPfBufs], total = 0;
     prefill_scratch_sizes(g, T, sz);
     for (uint64_t b : sz) total += (b + 255) / 256 * 256;
     return total;
@@ -263,13 +266,16 @@ int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
     ctx->capture_uses_scratch = true;
     if (T <= ctx->pf_cap) return M1MOE_OK;
     if (int32_t rc = m1moe::refuse_growth_in_capture(ctx->stream, "the prefill scratch")) return rc;
-    void** bufs[9] = {(void**)&ctx->pf_xq,   (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
-                      (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,
-                      (void**)&ctx->pf_tdesc, (void**)&ctx->pf_act,  (void**)&ctx->pf_y};
-    static const char* const names[9] = {
+    void** bufs[m1moe::kPfBufs] = {
+        (void**)&ctx->pf_xq,    (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
+        (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,
+        (void**)&ctx->pf_tdesc, (void**)&ctx->pf_act,  (void**)&ctx->pf_y,
+        (void**)&ctx->pf_aexp,  (void**)&ctx->pf_pscale, (void**)&ctx->pf_aflag};
+    static const char* const names[m1moe::kPfBufs] = {
         "prefill x",       "prefill x scales",   "prefill positions",
         "prefill sorted tokens", "prefill expert offsets", "prefill tile offsets",
-        "prefill tile descriptors", "prefill act",        "prefill expert outputs"};
+        "prefill tile descriptors", "prefill act",        "prefill expert outputs",
+        "prefill act exponents", "prefill pair scales", "prefill act flag"};
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     if (ctx->pf_cap > 0) ++ctx->scratch_gen;  // earlier graphs hold the old buffers
     for (void** b : bufs) {
@@ -277,9 +283,9 @@ int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
         *b = nullptr;
     }
     ctx->pf_cap = 0;
-    uint64_t sz[9];
+    uint64_t sz[m1moe::kPfBufs];
     prefill_scratch_sizes(ctx->g, T, sz);
-    for (int i = 0; i < 9; ++i)
+    for (int i = 0; i < m1moe::kPfBufs; ++i)
         if (int32_t rc = device_alloc(bufs[i], sz[i], names[i])) return rc;
     ctx->pf_cap = T;
     return M1MOE_OK;
@@ -358,12 +364,12 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
     a.I = g.I;
     a.gs = g.gs;
     if (sbase) {
-        // carve the nine buffers, 256-byte aligned; every one is written
+        // carve the kPfBufs buffers, 256-byte aligned; every one is written
         // before it is read, so nothing left by an earlier call is used
-        uint64_t sz[9];
-        void* p[9];
+        uint64_t sz[m1moe::kPfBufs];
+        void* p[m1moe::kPfBufs];
         prefill_scratch_sizes(g, T, sz);
-        for (int i = 0; i < 9; ++i) {
+        for (int i = 0; i < m1moe::kPfBufs; ++i) {
             p[i] = sbase;
             sbase += (sz[i] + 255) / 256 * 256;
         }
@@ -376,6 +382,9 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
         a.tile_desc = static_cast<m1moe::PfTile*>(p[6]);
         a.act = static_cast<_Float16*>(p[7]);
         a.y = static_cast<float*>(p[8]);
+        a.act_exp = static_cast<uint8_t*>(p[9]);
+        a.pair_scale = static_cast<float*>(p[10]);
+        a.act_flag = static_cast<uint32_t*>(p[11]);
     } else {
         a.xq = ctx->pf_xq;
         a.xinv = ctx->pf_xinv;
@@ -386,6 +395,9 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
         a.tile_desc = ctx->pf_tdesc;
         a.act = ctx->pf_act;
         a.y = ctx->pf_y;
+        a.act_exp = ctx->pf_aexp;
+        a.pair_scale = ctx->pf_pscale;
+        a.act_flag = ctx->pf_aflag;
     }
     a.err = ctx->err;
     a.cus = ctx->cus;
@@ -471,7 +483,8 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
     void* owned[] = {ctx->arena,   ctx->dec,      ctx->pft,      ctx->routers,  ctx->biases,  ctx->logits,  ctx->topk_idx,
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
                      ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
-                     ctx->pf_toff, ctx->pf_tdesc,  ctx->pf_act,  ctx->pf_y,     ctx->attn_part, ctx->attn_cnt};
+                     ctx->pf_toff, ctx->pf_tdesc,  ctx->pf_act,  ctx->pf_y,     ctx->pf_aexp,
+                     ctx->pf_pscale, ctx->pf_aflag, ctx->attn_part, ctx->attn_cnt};
     for (void* p : owned)
         if (p) (void)hipFree(p);
     share_leave(ctx);
@@ -753,6 +766,10 @@ int32_t m1moe_sync(m1moe_ctx_t ctx) {
             return fail(M1MOE_ERR_DEVICE,
                         "a decoder step read a token id outside the vocabulary; token 0 was "
                         "embedded (device flag 0x%x)", flag);
+        if (flag & 64u)
+            return fail(M1MOE_ERR_DEVICE,
+                        "a prefill's SwiGLU product was outside the f16 range (|act| > 65504) or "
+                        "not finite; it was clamped to +-65504 (device flag 0x%x)", flag);
         if (flag & 32u)
             return fail(M1MOE_ERR_DEVICE,
                         "a decoder step ran with the KV cache full (position == max_seq); "

@@ -21,16 +21,17 @@ namespace {
 
 int32_t check_f32_vec(const void* p, const char* what) { return check_dev_ptr(p, what, false); }
 
-constexpr int kAttnCounters = 1024;  // >= num_heads (num_heads * 64 <= 65536)
+constexpr int kAttnCounters = 1024;  // >= num_heads (num_heads * 64 <= 65536); then the
+                                     // synchronous merge's launch number and finish count
 
 int32_t ensure_attn_scratch(m1moe_ctx_t ctx, uint64_t floats) {
     ctx->capture_uses_scratch = true;
     if (!ctx->attn_cnt || floats > ctx->attn_part_floats)
         if (int32_t rc = refuse_growth_in_capture(ctx->stream, "the attention scratch")) return rc;
     if (!ctx->attn_cnt) {
-        int32_t rc = device_alloc((void**)&ctx->attn_cnt, kAttnCounters * 4, "attention counters");
+        int32_t rc = device_alloc((void**)&ctx->attn_cnt, (kAttnCounters + 2) * 4, "attention counters");
         if (rc) return rc;
-        HIP_TRY(hipMemset(ctx->attn_cnt, 0, kAttnCounters * 4));
+        HIP_TRY(hipMemset(ctx->attn_cnt, 0, (kAttnCounters + 2) * 4));
     }
     if (floats <= ctx->attn_part_floats) return M1MOE_OK;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -85,8 +86,10 @@ struct m1moe_dec {
     int32_t pf_cap = 0;
     float *pf_res = nullptr, *pf_res2 = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr;
     float* pf_part = nullptr;  // split-K partials of the prefill GEMMs (kGemmPartFloats)
-    uint32_t* cnt = nullptr;   // [2 + num_heads]: (unused), lm_head, attention groups
+    uint32_t* cnt = nullptr;   // [4 + num_heads]: (unused), lm_head, attention groups,
+                               // the attention's launch number and finish count
     float* ssq = nullptr;      // o_proj's per-workgroup sums of squares
+    float* rope = nullptr;     // [max_seq][head_dim / 2] (cos, sin) of every position
     float* am_val = nullptr;   // lm_head's per-workgroup best logit
     int32_t* am_idx = nullptr;
     std::vector<void*> allocs;
@@ -210,6 +213,11 @@ int32_t m1moe_attention_decode(m1moe_ctx_t ctx, const float* d_q, const float* d
     a.qh = attention_qh(a.hpkv);
     a.chunk = attention_chunk(seq_len);
     a.scale = 1.0f / sqrtf((float)head_dim);
+    a.gen = ctx->attn_cnt + kAttnCounters;
+    a.fin = ctx->attn_cnt + kAttnCounters + 1;
+    a.cus = ctx->cus;
+    a.spin_limit = kAttnSpinLimit;
+    a.sync_merge = attention_grid_fits(a) ? 1 : 0;
     return launched(launch_attention(a, ctx->stream), "attention");
 }
 
@@ -285,17 +293,20 @@ int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* s, m1moe_dec_t*
         (rc = dec_alloc(d, (void**)&d->attn, qd * 4, "attention output")) ||
         (rc = dec_alloc(d, (void**)&d->logits, V * 4, "logits")) ||
         (rc = dec_alloc(d, (void**)&d->part, part * 4, "attention scratch")) ||
-        (rc = dec_alloc(d, (void**)&d->cnt, (2 + (uint64_t)s->num_heads) * 4, "counters")) ||
+        (rc = dec_alloc(d, (void**)&d->cnt, (4 + (uint64_t)s->num_heads) * 4, "counters")) ||
         (rc = dec_alloc(d, (void**)&d->ssq, (uint64_t)matvec_workgroups(d->h) * 4, "o_proj sums")) ||
+        (rc = dec_alloc(d, (void**)&d->rope, ms * hd * 4, "RoPE table")) ||
         (rc = dec_alloc(d, (void**)&d->am_val, (uint64_t)matvec_workgroups(s->vocab) * 4, "argmax scratch")) ||
         (rc = dec_alloc(d, (void**)&d->am_idx, (uint64_t)matvec_workgroups(s->vocab) * 4, "argmax scratch"))) {
         m1moe_dec_destroy(d);
         return rc;
     }
     if (hipMemset(d->pos, 0, 16) != hipSuccess ||
-        hipMemset(d->cnt, 0, (2 + (size_t)s->num_heads) * 4) != hipSuccess) {
+        hipMemset(d->cnt, 0, (4 + (size_t)s->num_heads) * 4) != hipSuccess ||
+        launch_rope_table(d->rope, s->max_seq, s->head_dim, s->rope_theta, moe->stream) != 0 ||
+        hipStreamSynchronize(moe->stream) != hipSuccess) {
         m1moe_dec_destroy(d);
-        return fail(M1MOE_ERR_HIP, "hipMemset(position / counters) failed");
+        return fail(M1MOE_ERR_HIP, "decoder state initialisation failed");
     }
     *out = d;
     return M1MOE_OK;
@@ -390,6 +401,12 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
     at.scale = 1.0f / sqrtf((float)hd);
     at.rope_theta = dec->sh.rope_theta;
     at.eps = eps;
+    at.gen = dec->cnt + 2 + dec->sh.num_heads;
+    at.fin = dec->cnt + 3 + dec->sh.num_heads;
+    at.cus = ctx->cus;
+    at.spin_limit = kAttnSpinLimit;
+    at.sync_merge = attention_grid_fits(at) ? 1 : 0;
+    at.rope = dec->rope;
     // short contexts: o_proj merges the attention partials while staging its
     // input (only a staged input can: q widths up to kMvStageMax)
     at.defer = qd <= kMvStageMax ? 1 : 0;

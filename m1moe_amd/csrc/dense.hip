@@ -30,6 +30,8 @@
 // back to 0, so a captured graph can replay the kernels.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "device.hpp"
 #include "internal.hpp"
 
@@ -409,6 +411,177 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
 
 // ---- attention --------------------------------------------------------------------------
 
+// Sum over aligned groups of LP lanes (8, 16 or 32), the total in every lane
+// of the group: quad sums on DPP quad permutes, then the half-row mirror
+// (LP 8) or two row rotations (LP 16, 32), then the neighbouring row by a
+// row swap (LP 32).  No LDS crossbar round trips.
+__device__ __forceinline__ float rows_pair_sum(float v) {  // rows 0+1 and 2+3
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float halves_sum(float v) {  // lanes l and l ^ 32
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int LP>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    static_assert(LP == 8 || LP == 16 || LP == 32, "8, 16 or 32 lanes");
+    v += dpp_f32<kDppXor1>(v, v);
+    v += dpp_f32<kDppXor2>(v, v);
+    if (LP == 8) {
+        v += dpp_f32<0x141>(v, v);  // row_half_mirror: the other quad of the 8
+    } else {
+        v += dpp_f32<kDppRor4>(v, v);
+        v += dpp_f32<kDppRor8>(v, v);
+        if (LP == 32) v = rows_pair_sum(v);
+    }
+    return v;
+}
+// Sum of the lanes l, l ^ LP, l ^ 2 LP, ... (every lane of the wave with the
+// same l % LP), the total in all of them.
+template <int LP>
+__device__ __forceinline__ float lane_stride_sum(float v) {
+    if (LP == 8) v += dpp_f32<kDppRor8>(v, v);  // l ^ 8 within the 16-lane row
+    if (LP <= 16) v = rows_pair_sum(v);
+    return halves_sum(v);
+}
+
+__device__ __forceinline__ uint32_t ld_coh_u32(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_u64(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_coh_u64(const unsigned long long* p) {
+    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long tagged64(uint32_t tag, float v) {
+    return ((unsigned long long)tag << 32) | __float_as_uint(v);
+}
+
+// Lanes per output in a synchronous-merge share of S outputs (R S <= 256,
+// R <= 16, so the R lanes of an output lie in one 16-lane row).
+__host__ __device__ constexpr int attn_share_lanes(int S) {
+    return S <= 16 ? 16 : S <= 32 ? 8 : S <= 64 ? 4 : S <= 128 ? 2 : 1;
+}
+// Chunks per lane the share handles at most: (the merge is used only when
+// the share of nact chunks fits, attn_sync_fits)
+template <int HD, int QH>
+__host__ __device__ constexpr int attn_share_max() { return QH * HD / 128 + 2; }
+template <int HD, int QH>
+__host__ __device__ constexpr bool attn_sync_fits(int nact) {
+    return nact > 1 && nact <= kAttnMaxChunks && QH * HD <= 256 * nact &&
+           (nact + attn_share_lanes((QH * HD + nact - 1) / nact) - 1) /
+                   attn_share_lanes((QH * HD + nact - 1) / nact) <=
+               attn_share_max<HD, QH>();
+}
+
+// The synchronous merge, workgroup (g, c)'s share: outputs o0 .. o0 + S - 1 of
+// its group's QH * HD (S = ceil(QH HD / nact), o0 = c S), each taken by R
+// lanes (R S <= 256, R <= 16) that add every R-th chunk; per head M = max_c
+// m_c, f_c = e^(m_c - M), L = sum_c l_c f_c (from the chunk statistics,
+// staged in LDS), out = sum_c acc_c f_c / L.  Every value is read until it
+// carries this launch's number (the other workgroups' stores are not
+// waited for); the waits are bounded (a timeout raises device flag 4).
+template <int HD, int QH>
+__device__ void attn_merge_share(const AttnArgs& a, int g, int c, int nch, int nact, uint32_t tag,
+                                 float (*s_st)[QH][kAttnMaxChunks], float* s_l) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t cstride = (size_t)QH * (HD + 2);
+    const unsigned long long* base =
+        reinterpret_cast<const unsigned long long*>(a.partial) + (size_t)g * nch * cstride;
+    // the statistics of every (head, chunk): 2 QH nact pairs, up to 4 per thread
+    constexpr int kSt = (2 * QH * kAttnMaxChunks + 255) / 256;
+    bool ok = true;
+    for (int it = 0;; ++it) {
+        bool cur = true;
+        unsigned long long u[kSt];
+#pragma unroll
+        for (int s = 0; s < kSt; ++s) {
+            const int e = tid + 256 * s;  // (head i, chunk k, m or l)
+            const int i = e / (2 * nact), r = e - i * 2 * nact, k = r >> 1;
+            u[s] = (e < 2 * QH * nact) ? ld_coh_u64(base + k * cstride + i * (HD + 2) + (r & 1))
+                                       : ((unsigned long long)tag << 32);
+        }
+#pragma unroll
+        for (int s = 0; s < kSt; ++s) {
+            const int e = tid + 256 * s;
+            const int i = e / (2 * nact), r = e - i * 2 * nact, k = r >> 1;
+            if ((uint32_t)(u[s] >> 32) != tag) cur = false;
+            else if (e < 2 * QH * nact) s_st[r & 1][i][k] = __uint_as_float((uint32_t)u[s]);
+        }
+        if (__syncthreads_and(cur)) break;
+        if (it >= a.spin_limit) {
+            if (tid == 0) flag_error(a.err, 4u);
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    // per head: M, the factors (in place of m), L
+    for (int i = wave; i < QH; i += 4) {
+        const bool on = lane < nact;
+        const float m = on ? s_st[0][i][lane] : -INFINITY;
+        const float mx = wave_max(m);
+        const float f = on ? expf(m - mx) : 0.f;
+        const float l = wave_sum(on ? s_st[1][i][lane] * f : 0.f);
+        if (on) s_st[0][i][lane] = f;
+        if (lane == 0) s_l[i] = l;
+    }
+    __syncthreads();
+    const int S = (QH * HD + nact - 1) / nact;
+    const int R = attn_share_lanes(S);
+    const int oi = tid / R, r = tid - oi * R, o = c * S + oi;
+    const bool mine = oi < S && o < QH * HD;
+    const int i = mine ? o / HD : 0, d = mine ? o - i * HD : 0;
+    constexpr int kMaxPer = attn_share_max<HD, QH>();
+    const int nper = mine ? (nact - r + R - 1) / R : 0;  // chunks r, r + R, ...
+    float vals[kMaxPer];
+    bool have[kMaxPer];
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j) {
+        vals[j] = 0.f;
+        have[j] = !(ok && j < nper);
+    }
+    for (int it = 0; ok; ++it) {
+        // every missing value of the lane is requested before any is examined
+        unsigned long long u[kMaxPer];
+#pragma unroll
+        for (int j = 0; j < kMaxPer; ++j)
+            u[j] = have[j] ? 0ull
+                           : ld_coh_u64(base + (size_t)(r + R * j) * cstride + i * (HD + 2) + 2 + d);
+        bool cur = true;
+#pragma unroll
+        for (int j = 0; j < kMaxPer; ++j) {
+            if (!have[j]) {
+                if ((uint32_t)(u[j] >> 32) == tag) {
+                    have[j] = true;
+                    vals[j] = __uint_as_float((uint32_t)u[j]);
+                } else {
+                    cur = false;
+                }
+            }
+        }
+        if (__all(cur)) break;
+        if (it >= a.spin_limit) {
+            flag_error(a.err, 4u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    float acc = 0.f;  // the chunks in order
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j)
+        if (j < nper) acc = fmaf(vals[j], s_st[0][i][r + R * j], acc);
+    // the R lanes of an output (aligned in a 16-lane row), in a fixed order
+    for (int off = R >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (mine && r == 0) a.out[(size_t)(g * QH + i) * HD + d] = acc / s_l[i];
+}
+
+
 // Workgroup (g, c): q heads g*QH .. g*QH+QH-1 (one kv head), positions
 // c*a.chunk .. (c+1)*a.chunk - 1, walked 64 at a time with a running max
 // and sum (the softmax of attnSoftmax, Shaders.metal:245-289, in pieces).
@@ -428,6 +601,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __shared__ float s_m[QH], s_l[QH], s_f[QH];
     __shared__ float s_st[2][QH][kAttnMaxChunks];  // merge: chunk max and sum
     __shared__ int s_flag;
+    __shared__ uint32_t s_tag;
 
     const int g = blockIdx.x, c = blockIdx.y, nch = gridDim.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -450,7 +624,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int c0 = c * a.chunk, c1 = min(c0 + a.chunk, seq);
     const int nact = min(nch, (seq + a.chunk - 1) / a.chunk);  // workgroups with positions
     const bool defer = a.defer && attn_defer_nact(p, a.max_seq, a.chunk, a.num_heads) > 0;
+    const bool sync = a.sync_merge && !defer && attn_sync_fits<HD, QH>(nact);
     float* part = a.partial + ((size_t)g * nch + c) * QH * (HD + 2);
+    unsigned long long* part64 =
+        reinterpret_cast<unsigned long long*>(a.partial) + ((size_t)g * nch + c) * QH * (HD + 2);
+    if (sync && tid == 0) s_tag = ld_coh_u32(a.gen) + 1u;
 
     if (c0 < seq) {
         // this lane's K and V rows of a 64-position sub-chunk (row p, not yet
@@ -518,9 +696,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             for (int t = tid; t < items * HALF; t += 256) {
                 const int it = t / HALF, d = t - it * HALF;
                 float* vec = it == QH ? s_kv[0] : s_q[it];
-                const float freq = 1.0f / powf(a.rope_theta, (float)(2 * d) / (float)HD);
-                const float ang = (float)p * freq;
-                const float cs = cosf(ang), sn = sinf(ang);
+                float cs, sn;
+                if (a.rope && p < a.max_seq) {  // rope_table_kernel's table (the same arithmetic)
+                    const float2 r = reinterpret_cast<const float2*>(a.rope)[(size_t)p * HALF + d];
+                    cs = r.x;
+                    sn = r.y;
+                } else {
+                    const float freq = 1.0f / powf(a.rope_theta, (float)(2 * d) / (float)HD);
+                    const float ang = (float)p * freq;
+                    cs = cosf(ang);
+                    sn = sinf(ang);
+                }
                 const float x0 = vec[d], x1 = vec[d + HALF];
                 vec[d] = x0 * cs - x1 * sn;
                 vec[d + HALF] = x0 * sn + x1 * cs;
@@ -573,8 +759,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     float d = 0.f;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) d = fmaf(qv[i][e], R.k[it][e], d);
-#pragma unroll
-                    for (int o = 1; o < LP; o <<= 1) d += __shfl_xor(d, o);
+                    d = lane_group_sum<LP>(d);
                     if (lp == 0) s_p[i][pl] = p0 + pl < c1 ? d * a.scale : -INFINITY;
                 }
             }
@@ -629,11 +814,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
         }
 #pragma unroll
-        for (int o = LP; o < 64; o <<= 1)
+        for (int i = 0; i < QH; ++i)
 #pragma unroll
-            for (int i = 0; i < QH; ++i)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[i][e] += __shfl_xor(acc[i][e], o);
+            for (int e = 0; e < 8; ++e) acc[i][e] = lane_stride_sum<LP>(acc[i][e]);
         if (pg == 0) {
 #pragma unroll
             for (int i = 0; i < QH; ++i) {
@@ -653,17 +836,24 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
             return;
         }
-        // (a deferred merge reads the partials in the next launch: plain stores)
+        // (a deferred merge reads the partials in the next launch: plain stores;
+        // the synchronous merge: (launch number, value) pairs)
+        const uint32_t tag = s_tag;
         for (int t = tid; t < QH * HD; t += 256) {
             const int i = t / HD, d = t - i * HD;
             const float v = ((s_acc[0][i][d] + s_acc[1][i][d]) + s_acc[2][i][d]) + s_acc[3][i][d];
-            if (defer)
+            if (sync)
+                st_coh_u64(part64 + i * (HD + 2) + 2 + d, tagged64(tag, v));
+            else if (defer)
                 part[i * (HD + 2) + 2 + d] = v;
             else
                 st_coh(part + i * (HD + 2) + 2 + d, v);
         }
         if (tid < QH) {
-            if (defer) {
+            if (sync) {
+                st_coh_u64(part64 + tid * (HD + 2), tagged64(tag, s_m[tid]));
+                st_coh_u64(part64 + tid * (HD + 2) + 1, tagged64(tag, s_l[tid]));
+            } else if (defer) {
                 part[tid * (HD + 2)] = s_m[tid];
                 part[tid * (HD + 2) + 1] = s_l[tid];
             } else {
@@ -674,6 +864,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     if (nact == 1) return;  // (workgroups past the sequence are not read by the merge)
     if (defer) return;      // merged by the next launch (mv_stage_attn)
+    if (sync) {
+        if (c < nact) attn_merge_share<HD, QH>(a, g, c, nch, nact, s_tag, s_st, s_l);
+        // count this workgroup out; the last one advances the launch number
+        // (every workgroup read it before counting itself out)
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t total = gridDim.x * gridDim.y;
+            const uint32_t old =
+                __hip_atomic_fetch_add(a.fin, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old == total - 1) {
+                __hip_atomic_store(a.gen, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                reset_counter(a.fin);
+            }
+        }
+        return;
+    }
 
     // the last workgroup of the group merges the nact partials:
     // out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M)
@@ -792,6 +998,20 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* x, int n, int
     }
 }
 
+// RoPE (InferenceEngine.swift:521-536) factors of every position and pair:
+// table[p][d] = (cos, sin) of p / theta^(2d / head_dim), the arithmetic of
+// the in-kernel form of attn_kernel, made once per decoder.
+__global__ __launch_bounds__(256) void rope_table_kernel(float* table, int max_seq, int half,
+                                                         float theta, int hd) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= max_seq * half) return;
+    const int p = i / half, d = i - p * half;
+    const float freq = 1.0f / powf(theta, (float)(2 * d) / (float)hd);
+    const float ang = (float)p * freq;
+    table[2 * i] = cosf(ang);
+    table[2 * i + 1] = sinf(ang);
+}
+
 __global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
 
 // Rows per wave: more rows per workgroup for taller matrices (each workgroup
@@ -871,13 +1091,57 @@ int attention_chunk(int max_positions) {
 
 int attention_partial_floats(int num_heads, int head_dim, int max_positions) {
     const int chunk = attention_chunk(max_positions);
-    return num_heads * ((max_positions + chunk - 1) / chunk) * (head_dim + 2);
+    return 2 * num_heads * ((max_positions + chunk - 1) / chunk) * (head_dim + 2);
+}
+
+namespace {
+template <int HD>
+int attn_occupancy_hd(int qh, bool two) {
+    int n = 0;
+    hipError_t e = hipErrorInvalidValue;
+    switch (qh * 2 + (two ? 1 : 0)) {
+        case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 1, false>, 256, 0); break;
+        case 3: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 1, true>, 256, 0); break;
+        case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 2, false>, 256, 0); break;
+        case 5: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 2, true>, 256, 0); break;
+        case 8: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 4, false>, 256, 0); break;
+        case 9: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 4, true>, 256, 0); break;
+        case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 8, false>, 256, 0); break;
+        case 17: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 8, true>, 256, 0); break;
+        default: break;
+    }
+    return e == hipSuccess ? n : 0;
+}
+
+// Workgroups of the attention kernel of (head_dim, qh, two sub-chunk sets)
+// one CU holds, from the occupancy query, kept after the first ask.
+std::atomic<int> g_attn_occ[3][9][2];
+
+int attn_blocks_per_cu(int hd, int qh, bool two) {
+    const int hi = hd == 64 ? 0 : hd == 128 ? 1 : 2;
+    std::atomic<int>& slot = g_attn_occ[hi][qh][two ? 1 : 0];
+    int v = slot.load(std::memory_order_relaxed);
+    if (v == 0) {
+        v = hd == 64 ? attn_occupancy_hd<64>(qh, two)
+                     : hd == 128 ? attn_occupancy_hd<128>(qh, two) : attn_occupancy_hd<256>(qh, two);
+        v = v > 0 ? v : -1;
+        slot.store(v, std::memory_order_relaxed);
+    }
+    return v > 0 ? v : 0;
+}
+}  // namespace
+
+bool attention_grid_fits(const AttnArgs& a) {
+    if (a.qh <= 0 || a.qh > 8 || a.cus <= 0) return false;
+    const int64_t grid = (int64_t)(a.num_heads / a.qh) * ((a.max_seq + a.chunk - 1) / a.chunk);
+    return (int64_t)attn_blocks_per_cu(a.head_dim, a.qh, a.chunk > kAttnChunk) * a.cus >= grid;
 }
 
 int launch_attention(const AttnArgs& a, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (a.qh <= 0 || a.num_heads % a.qh || a.hpkv % a.qh || a.chunk != attention_chunk(a.max_seq))
         return (int)hipErrorInvalidValue;
+    if (a.sync_merge && !(a.gen && a.fin && attention_grid_fits(a))) return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.num_heads / a.qh), (unsigned)((a.max_seq + a.chunk - 1) / a.chunk));
     switch (a.head_dim) {
         case 64: return launch_attn_hd<64>(a, grid, st);
@@ -885,6 +1149,14 @@ int launch_attention(const AttnArgs& a, void* stream) {
         case 256: return launch_attn_hd<256>(a, grid, st);
         default: return (int)hipErrorInvalidValue;
     }
+}
+
+int launch_rope_table(float* table, int max_seq, int head_dim, float theta, void* stream) {
+    const int n = max_seq * (head_dim / 2);
+    hipLaunchKernelGGL(rope_table_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), table, max_seq, head_dim / 2, theta,
+                       head_dim);
+    return (int)hipGetLastError();
 }
 
 int launch_argmax(const float* x, int n, int32_t* out, void* stream) {

@@ -199,16 +199,24 @@ struct PrefillArgs {
     PfTile* tile_desc;           // [T*K/kPfTN + E + 1] per N-tile (np = 0 past the last):
                                  // tiles of more than kPfTN / 2 pairs first
     int32_t cus;                 // compute units of the device
-    _Float16* act;               // [T*K][I] silu(gate)*up per sorted pair
-    float* y;                    // [T*K][h] expert outputs per sorted pair
+    _Float16* act;               // [T*K][I] silu(gate)*up per sorted pair, times 2^-E of the pair
+    float* y;                    // [T*K][h] expert outputs per sorted pair, times 2^-E of the pair
+    uint8_t* act_exp;            // [T*K][I/32] e >= 0 of each 32-value block: act held act * 2^-e
+    float* pair_scale;           // [T*K] 2^E, E the largest e of the pair (written when act_flag)
+    uint32_t* act_flag;          // 1 when some e > 0 (else every E is 0 and pair_scale unwritten)
     uint32_t* err;               // sticky device error flag
 };
+
+// Prefill scratch buffers (in the order of PrefillArgs: xq, xinv, pos,
+// sorted_tok, expert_off, tile_off, tile_desc, act, y, act_exp, pair_scale,
+// act_flag).
+constexpr int kPfBufs = 12;
 
 constexpr int kPfTN = 128;  // prefill GEMM: (token, slot) pairs per workgroup tile
 
 // m1moe_moe_prefill_noalloc: bytes of the per-GPU static scratch (scratch.hip)
-// that holds its prefill buffers.  64 MiB: 779 tokens at hidden 2048,
-// 8 x 1024 experts, 682 at hidden 4096, 2 x 14336.
+// that holds its prefill buffers.  64 MiB: 776 tokens at hidden 2048,
+// 8 x 1024 experts, 676 at hidden 4096, 2 x 14336.
 constexpr uint64_t kStaticScratchBytes = 64ull << 20;
 // Device address of this GPU's static scratch; `device` must be current.
 // Looks it up on the first call per device and returns the kept address
@@ -331,6 +339,19 @@ struct AttnArgs {
     // <= kAttnDeferHeadChunks, write the partials and leave their merge to the
     // next launch (the o_proj matvec, which stages them as its input)
     int32_t defer;
+    // 1 when the whole grid fits on the device at once (set by the launcher
+    // from the occupancy query): the partials are stored as (launch number,
+    // value) pairs in `partial` read as u64, and every workgroup with
+    // positions merges a share of its group's outputs, waiting for the
+    // current launch number instead of a completion count.  gen holds the
+    // launch number, fin counts finished workgroups (the last one advances
+    // gen and puts fin back to 0).
+    int32_t sync_merge;
+    const float* rope;           // fused: [max_seq][head_dim / 2] (cos, sin) table, or null
+    uint32_t* gen;
+    uint32_t* fin;
+    int32_t cus;                 // compute units of the device
+    int32_t spin_limit;
 };
 
 constexpr int kAttnChunk = 64;   // positions per attention workgroup
@@ -406,6 +427,14 @@ int launch_matvec_bf16(const MvArgs& a, void* stream);
 int attention_qh(int hpkv);
 // Positions per attention workgroup for a cache of max_positions.
 int attention_chunk(int max_positions);
+// The whole attention grid of `a` fits on the device at once (a.cus CUs, the
+// occupancy of the kernel instance it launches): the synchronous merge may
+// be used.
+bool attention_grid_fits(const AttnArgs& a);
+// The RoPE table of attn_kernel: [max_seq][head_dim / 2] (cos, sin) pairs.
+int launch_rope_table(float* table, int max_seq, int head_dim, float theta, void* stream);
+constexpr int32_t kAttnSpinLimit = 1 << 20;  // bounded waits of the synchronous merge (~1 s)
+// floats of the partials buffer (room for the u64 pairs of the synchronous merge)
 int attention_partial_floats(int num_heads, int head_dim, int max_positions);
 int launch_attention(const AttnArgs& a, void* stream);
 // Greedy token of x[0..n) to *out (ties to the lower index; x[0] NaN gives 0).

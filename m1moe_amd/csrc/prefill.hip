@@ -93,6 +93,7 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, P = a.T * a.K;
     if (tid < kMaxE) cnt[tid] = 0;
+    if (tid == 0) *a.act_flag = 0u;   // set by the gate/up GEMM when a block of act needs e > 0
     __syncthreads();
     const bool one_pass = P <= 1024 * kGP;
     int pe[kGP], pr[kGP];
@@ -585,26 +586,49 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
                         rs[m][v][i] =
                             row_scale((col < 4 ? kx[m][v].x : kx[m][v].y) >> (8 * (col & 3)));
                     }
+            // act goes out in blocks of 32 values, this wave's 32 rows of one pair
+            // (16 on each lane of c and c + 32): a block whose largest |value|
+            // is past the f16 range is stored times 2^-e, e >= 1 the least that
+            // fits, and e is kept per block (0 for the others).  A value that is
+            // not finite is clamped and reported (device flag 64).
+            bool bad = false, scaled = false;
+            const int nb = a.I >> 5;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int n = q * 32 + c;
-                if (n >= np) continue;
+                if (n >= np) continue;   // both lanes of the pair's block skip together
                 const float inv = s_inv[n];
+                float y[4][4], mx = 0.f;
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float g = acc[0][q][4 * v + i] * rs[0][v][i] * inv;
+                        const float u = acc[1][q][4 * v + i] * rs[1][v][i] * inv;
+                        y[v][i] = silu_fast(g) * u;  // Shaders.metal:148
+                        const bool fin = isfinite(y[v][i]);
+                        bad |= !fin;
+                        mx = fin ? fmaxf(mx, fabsf(y[v][i])) : mx;
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                // mx / 65504 = m 2^e with m in [0.5, 1): mx 2^-e < 65504
+                int e = 0;
+                if (mx > 65504.f) (void)frexpf(mx * (1.f / 65504.f), &e);
+                scaled |= e > 0;
+                const float sc = __builtin_bit_cast(float, (127 - e) << 23);   // 2^-e, e <= 113
                 _Float16* dst = a.act + (size_t)(p0 + n) * a.I + wrow0 + 4 * kh;
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     _Float16 o[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float g = acc[0][q][4 * v + i] * rs[0][v][i] * inv;
-                        const float u = acc[1][q][4 * v + i] * rs[1][v][i] * inv;
-                        float y = silu_fast(g) * u;  // Shaders.metal:148
-                        y = fminf(fmaxf(y, -65504.f), 65504.f);
-                        o[i] = (_Float16)y;
-                    }
+                    for (int i = 0; i < 4; ++i)
+                        o[i] = (_Float16)fminf(fmaxf(y[v][i] * sc, -65504.f), 65504.f);
                     *reinterpret_cast<uint2*>(dst + 8 * v) = __builtin_bit_cast(uint2, o);
                 }
+                if (kh == 0) a.act_exp[(size_t)(p0 + n) * nb + (wrow0 >> 5)] = (uint8_t)e;
             }
+            if (__any(bad) && lane == 0) flag_error(a.err, 64u);
+            if (__any(scaled) && lane == 0) *a.act_flag = 1u;
         } else if (NMAT == 1) {
 #pragma unroll
             for (int rm = 0; rm < 2; ++rm) {
@@ -740,20 +764,54 @@ __global__ __launch_bounds__(256) void pf_tile_copy_kernel(const uint8_t* src, u
                               within) = v;
 }
 
+// ---- act exponents ----------------------------------------------------------------
+
+// After the gate/up GEMM, and only when it stored some block of act with
+// e > 0: every pair's blocks are brought to the pair's largest e, E (a block
+// with e < E is multiplied by 2^(e - E) in place, in f16), and pair_scale
+// gets 2^E, which the combine multiplies the pair's down output by.  One
+// wave per pair, 8 values per lane and step.
+__global__ __launch_bounds__(256) void pf_act_fix_kernel(PrefillArgs a) {
+    if (*a.act_flag == 0u) return;
+    const int P = a.T * a.K, nb = a.I >> 5, lane = threadIdx.x & 63;
+    for (int p = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6); p < P; p += (int)gridDim.x * 4) {
+        const uint8_t* ep = a.act_exp + (size_t)p * nb;
+        int E = 0;
+        for (int b = lane; b < nb; b += 64) E = max(E, (int)ep[b]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) E = max(E, __shfl_xor(E, o));
+        if (lane == 0) a.pair_scale[p] = __builtin_bit_cast(float, (127 + E) << 23);
+        if (E == 0) continue;
+        _Float16* row = a.act + (size_t)p * a.I;
+        for (int j = lane * 8; j < a.I; j += 512) {
+            const int e = ep[j >> 5];
+            if (e == E) continue;
+            const float f = __builtin_bit_cast(float, (127 + e - E) << 23);   // e - E >= -113
+            _Float16 v[8];
+            *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(row + j);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = (_Float16)((float)v[i] * f);
+            *reinterpret_cast<uint4*>(row + j) = *reinterpret_cast<const uint4*>(v);
+        }
+    }
+}
+
 // ---- combine ----------------------------------------------------------------------
 
 // out[t][d] = residual[t][d] + sum_k w[t][k] * y[pos[t,k]][d], k ascending
-// (Shaders.metal:371-374); four columns per thread.
+// (Shaders.metal:371-374); four columns per thread.  y of a pair with E > 0
+// is the output times 2^-E: w is multiplied by 2^E (exact).
 __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     const int t = blockIdx.y;
     const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (d >= a.h) return;
+    const bool scaled = *a.act_flag != 0u;
     float4 acc = a.residual ? *reinterpret_cast<const float4*>(a.residual + (size_t)t * a.h + d)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k = 0; k < a.K; ++k) {
-        const float w = a.w[(size_t)t * a.K + k];
-        const float4 y = *reinterpret_cast<const float4*>(
-            a.y + (size_t)a.pos[(size_t)t * a.K + k] * a.h + d);
+        const int q = a.pos[(size_t)t * a.K + k];
+        const float w = a.w[(size_t)t * a.K + k] * (scaled ? a.pair_scale[q] : 1.f);
+        const float4 y = *reinterpret_cast<const float4*>(a.y + (size_t)q * a.h + d);
         acc.x = fmaf(w, y.x, acc.x);
         acc.y = fmaf(w, y.y, acc.y);
         acc.z = fmaf(w, y.z, acc.z);
@@ -783,6 +841,9 @@ int launch_gemms(const PrefillArgs& a, hipStream_t st) {
     launch_one<2, GSL>(a, st, ntiles_max);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL(pf_act_fix_kernel, dim3((unsigned)std::min((P + 3) / 4, 1024)), dim3(256), 0,
+                       st, a);
+    if ((e = hipGetLastError()) != hipSuccess) return (int)e;
     launch_one<1, GSL>(a, st, ntiles_max);
     return (int)hipGetLastError();
 }

@@ -336,8 +336,8 @@ class MoEBlock:
     def prefill_noalloc(self, layer: int, T: int, x, x_dtype, residual, out, topk_idx=None,
                         topk_w=None) -> None:
         """prefill() on the device's fixed static scratch: allocates nothing,
-        T limited by that scratch's 64 MiB (779 tokens at the OLMoE shape,
-        682 at the Mixtral shape)."""
+        T limited by that scratch's 64 MiB (776 tokens at the OLMoE shape,
+        676 at the Mixtral shape)."""
         check(self.lib.m1moe_moe_prefill_noalloc(
             self.ctx.handle, int(layer), int(T), _ptr(x), _dtype_code(x_dtype), _ptr(residual),
             _ptr(out), _ptr(topk_idx), _ptr(topk_w)), "m1moe_moe_prefill_noalloc")

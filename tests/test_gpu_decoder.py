@@ -760,3 +760,23 @@ def test_decoder_mixtral_32_layers_2048_prompt_64_greedy():
         if dec is not None:
             dec.close()
         ctx.close()
+
+
+@pytest.mark.parametrize("layers", [2, 4, 8])
+def test_decoder_mixtral_width_error_against_depth(layers):
+    """How the batched prefill's error grows with depth at Mixtral widths:
+    a 256-token prompt through `layers` layers in one batch per layer
+    against the oracle fed token by token (the last position's logits,
+    then two greedy steps), each within the 1e-2 bar."""
+    wl = synth.DECODERS["cfg4"]
+    p = Pair(wl, seed=77, max_seq=264, num_layers=layers, nthreads=NTHREADS)
+    try:
+        prompt = synth.prompt_tokens(wl, 77, 256)
+        say(f"mixtral width, {layers} layers: prefill of 256 tokens (GPU, then oracle)")
+        tok, g_lg = p.dec.prefill(prompt, return_logits=True)
+        w_tok, w_lg = p.orc.prefill(prompt)
+        pre = check_step(tok, g_lg, w_tok, w_lg, f"{layers}-layer prefill of 256")
+        errs, differ = _greedy_against_oracle(p, w_tok, 2, 256, f"{layers} layers")
+        say(f"  depth {layers}: logits rel L2 prefill {pre:.2e}, greedy max {max(errs):.2e}")
+    finally:
+        p.close()

@@ -256,3 +256,44 @@ def test_prefill_graph_replay_matches_eager(cfg3):
         cfg3.ctx.sync()
         got = dout.download(np.float32)
         assert np.array_equal(got.view(np.uint32), eager[rep % 2].view(np.uint32)), rep
+
+
+def test_prefill_takes_act_beyond_f16():
+    """Gate and up scales of the even experts times 2^10: their SwiGLU
+    products pass the f16 range (checked below on the oracle's own act).  The
+    prefill stores each 32-value block of act times its own power of two,
+    brings a pair's blocks to one exponent and scales the pair's output back;
+    against the oracle at the usual bar, with the odd experts' pairs
+    (unscaled) in the same call, and no device error."""
+    c = make_case("tiny", seed=12)
+    try:
+        s = c.shape
+        eb = c.ctx.expert_bytes
+        offs = m.expert_offsets(s)
+        gh = s.hidden // s.group_size
+        img = c.images[0].copy()
+        for e in range(0, s.num_experts, 2):
+            for k in (1, 4):  # gate_s, up_s
+                _scale_pow2(img, e * eb + offs[k], s.intermediate * gh, 10)
+        c.ctx.upload_layer_experts(0, img)
+        c.images[0] = img
+        c.ctx.sync()
+        T = 48
+        say("prefill with SwiGLU products beyond the f16 range")
+        got, gidx, gw, x32, res = _run_prefill(c, T, stream=5)
+        assert np.all(np.isfinite(got))
+        # the oracle's act of the routed pairs: some past 65504, some within
+        big = small = 0
+        for t in range(T):
+            for e in gidx[t]:
+                blk = img[int(e) * eb:(int(e) + 1) * eb]
+                g = orc.dequant_proj(c.oshape, blk, 0) @ x32[t]
+                u = orc.dequant_proj(c.oshape, blk, 1) @ x32[t]
+                a = np.abs(orc.swiglu(g.astype(np.float32), u.astype(np.float32))).max()
+                big += int(a > 65504.0)
+                small += int(a <= 65504.0)
+        say(f"  pairs with max |act| past f16: {big}, within: {small}")
+        assert big > 0 and small > 0
+        _check(c, T, got, gidx, gw, x32, res)
+    finally:
+        c.close()

@@ -17,7 +17,7 @@ from cases import make_case, say
 
 pytestmark = pytest.mark.gpu
 
-T_LIMIT_CFG3 = 779     # 64 MiB of static scratch at hidden 2048, 8 x 1024 experts
+T_LIMIT_CFG3 = 776     # 64 MiB of static scratch at hidden 2048, 8 x 1024 experts
 
 
 @pytest.fixture(scope="module")

@@ -233,7 +233,7 @@ int32_t enqueue_router(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* x,
 
 // Sizes in bytes of the kPfBufs prefill scratch buffers for T tokens, in the
 // order of PrefillArgs: xq, xinv, pos, sorted_tok, expert_off, tile_off,
-// tile_desc, act, y, act_exp, pair_scale, act_flag.
+// tile_desc, act, y, act_exp, act_flag.
 void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[m1moe::kPfBufs]) {
     const uint64_t t = (uint64_t)T, P = t * (uint64_t)g.K, E = (uint64_t)g.E;
     sz[0] = t * g.h * 2;
@@ -246,8 +246,7 @@ void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[m1moe::k
     sz[7] = P * g.I * 2;
     sz[8] = P * g.h * 4;
     sz[9] = P * (g.I / 32);
-    sz[10] = P * 4;
-    sz[11] = 4;
+    sz[10] = 8;
 }
 
 // Bytes of the kPfBufs buffers carved from one block, each 256-byte aligned.
@@ -270,12 +269,12 @@ int32_t ensure_prefill_scratch(m1moe_ctx_t ctx, int32_t T) {
         (void**)&ctx->pf_xq,    (void**)&ctx->pf_xinv, (void**)&ctx->pf_pos,
         (void**)&ctx->pf_sorted, (void**)&ctx->pf_eoff, (void**)&ctx->pf_toff,
         (void**)&ctx->pf_tdesc, (void**)&ctx->pf_act,  (void**)&ctx->pf_y,
-        (void**)&ctx->pf_aexp,  (void**)&ctx->pf_pscale, (void**)&ctx->pf_aflag};
+        (void**)&ctx->pf_aexp,  (void**)&ctx->pf_aflag};
     static const char* const names[m1moe::kPfBufs] = {
         "prefill x",       "prefill x scales",   "prefill positions",
         "prefill sorted tokens", "prefill expert offsets", "prefill tile offsets",
         "prefill tile descriptors", "prefill act",        "prefill expert outputs",
-        "prefill act exponents", "prefill pair scales", "prefill act flag"};
+        "prefill act exponents", "prefill act flag"};
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     if (ctx->pf_cap > 0) ++ctx->scratch_gen;  // earlier graphs hold the old buffers
     for (void** b : bufs) {
@@ -383,8 +382,7 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
         a.act = static_cast<_Float16*>(p[7]);
         a.y = static_cast<float*>(p[8]);
         a.act_exp = static_cast<uint8_t*>(p[9]);
-        a.pair_scale = static_cast<float*>(p[10]);
-        a.act_flag = static_cast<uint32_t*>(p[11]);
+        a.act_flag = static_cast<uint32_t*>(p[10]);
     } else {
         a.xq = ctx->pf_xq;
         a.xinv = ctx->pf_xinv;
@@ -396,7 +394,6 @@ int32_t prefill_common(m1moe_ctx_t ctx, int32_t layer, int32_t T, const void* d_
         a.act = ctx->pf_act;
         a.y = ctx->pf_y;
         a.act_exp = ctx->pf_aexp;
-        a.pair_scale = ctx->pf_pscale;
         a.act_flag = ctx->pf_aflag;
     }
     a.err = ctx->err;
@@ -484,7 +481,7 @@ void m1moe_destroy(m1moe_ctx_t ctx) {
                      ctx->topk_w,  ctx->counters, ctx->act,     ctx->sync,    ctx->err,
                      ctx->pf_xq,   ctx->pf_xinv,  ctx->pf_pos,  ctx->pf_sorted, ctx->pf_eoff,
                      ctx->pf_toff, ctx->pf_tdesc,  ctx->pf_act,  ctx->pf_y,     ctx->pf_aexp,
-                     ctx->pf_pscale, ctx->pf_aflag, ctx->attn_part, ctx->attn_cnt};
+                     ctx->pf_aflag, ctx->attn_part, ctx->attn_cnt};
     for (void* p : owned)
         if (p) (void)hipFree(p);
     share_leave(ctx);
@@ -768,8 +765,13 @@ int32_t m1moe_sync(m1moe_ctx_t ctx) {
                         "embedded (device flag 0x%x)", flag);
         if (flag & 64u)
             return fail(M1MOE_ERR_DEVICE,
-                        "a prefill's SwiGLU product was outside the f16 range (|act| > 65504) or "
-                        "not finite; it was clamped to +-65504 (device flag 0x%x)", flag);
+                        "a prefill's SwiGLU product was not finite; it was clamped to +-65504 "
+                        "(device flag 0x%x)", flag);
+        if (flag & 128u)
+            return fail(M1MOE_ERR_DEVICE,
+                        "a prefill's down GEMM timed out waiting for its workgroups (another "
+                        "kernel held compute units); the layer output is not valid (device flag "
+                        "0x%x)", flag);
         if (flag & 32u)
             return fail(M1MOE_ERR_DEVICE,
                         "a decoder step ran with the KV cache full (position == max_seq); "

@@ -92,7 +92,6 @@ struct m1moe_ctx {
     _Float16* pf_act = nullptr;      // [cap*K][I]
     float* pf_y = nullptr;           // [cap*K][h]
     uint8_t* pf_aexp = nullptr;      // [cap*K][I/32]
-    float* pf_pscale = nullptr;      // [cap*K]
     uint32_t* pf_aflag = nullptr;    // [1]
     // this device's static scratch (scratch.hip), for m1moe_moe_prefill_noalloc;
     // shared with every other context on the device, never freed

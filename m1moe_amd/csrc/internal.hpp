@@ -199,20 +199,20 @@ struct PrefillArgs {
     PfTile* tile_desc;           // [T*K/kPfTN + E + 1] per N-tile (np = 0 past the last):
                                  // tiles of more than kPfTN / 2 pairs first
     int32_t cus;                 // compute units of the device
-    _Float16* act;               // [T*K][I] silu(gate)*up per sorted pair, times 2^-E of the pair
-    float* y;                    // [T*K][h] expert outputs per sorted pair, times 2^-E of the pair
+    _Float16* act;               // [T*K][I] silu(gate)*up per sorted pair (per block: act_exp)
+    float* y;                    // [T*K][h] expert outputs per sorted pair
     uint8_t* act_exp;            // [T*K][I/32] e >= 0 of each 32-value block: act held act * 2^-e
-    float* pair_scale;           // [T*K] 2^E, E the largest e of the pair (written when act_flag)
-    uint32_t* act_flag;          // 1 when some e > 0 (else every E is 0 and pair_scale unwritten)
+    uint32_t* act_flag;          // [2] 1 when some e > 0 (the down GEMM then reads act_exp);
+                                 // the down GEMM's barrier count
     uint32_t* err;               // sticky device error flag
 };
 
 // Prefill scratch buffers (in the order of PrefillArgs: xq, xinv, pos,
-// sorted_tok, expert_off, tile_off, tile_desc, act, y, act_exp, pair_scale,
-// act_flag).
-constexpr int kPfBufs = 12;
+// sorted_tok, expert_off, tile_off, tile_desc, act, y, act_exp, act_flag).
+constexpr int kPfBufs = 11;
 
 constexpr int kPfTN = 128;  // prefill GEMM: (token, slot) pairs per workgroup tile
+constexpr int kPfSpinLimit = 1 << 20;   // bounded wait of the down GEMM's rare grid barrier
 
 // m1moe_moe_prefill_noalloc: bytes of the per-GPU static scratch (scratch.hip)
 // that holds its prefill buffers.  64 MiB: 776 tokens at hidden 2048,

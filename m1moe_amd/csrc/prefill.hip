@@ -14,8 +14,12 @@
 //                              inputs, no f16 overflow)
 //   group                      pairs sorted by expert; N-tiles of kPfTN pairs
 //   gemm<2>                    gate and up for a (rows x 64 pairs) tile,
-//                              epilogue act = silu(g) * u  -> f16 [pair][I]
-//   gemm<1>                    down for a (rows x 64 pairs) tile -> f32 y
+//                              epilogue act = silu(g) * u  -> f16 [pair][I],
+//                              each 32-value block times 2^-e (e = 0 unless
+//                              the block passes the f16 range)
+//   gemm<1>                    down for a (rows x 64 pairs) tile -> f32 y; only
+//                              when some e > 0, first each pair's blocks
+//                              brought to its largest e, E, and y times 2^E
 //   combine                    out[t] = residual[t] + sum_k w_tk y[pair(t,k)]
 //                              in slot order (deterministic, no atomics)
 //
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, P = a.T * a.K;
     if (tid < kMaxE) cnt[tid] = 0;
-    if (tid == 0) *a.act_flag = 0u;   // set by the gate/up GEMM when a block of act needs e > 0
+    if (tid < 2) a.act_flag[tid] = 0u;   // the down GEMM's flag (set by gate/up) and barrier count
     __syncthreads();
     const bool one_pass = P <= 1024 * kGP;
     int pe[kGP], pr[kGP];
@@ -451,6 +455,58 @@ __device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint
     wait_vm<0>();
 }
 
+// act blocks to one exponent per pair (the down GEMM's prologue when
+// act_flag[0] is set; every workgroup of the launch, all of them resident):
+// wave w of the grid takes pairs w, w + 4 grid, ...; a block with e < E, E
+// the pair's largest e, is multiplied by 2^(e - E) in place (in f16), and E
+// goes to the pair's first act exponent byte, where the epilogue reads it.
+// Then a grid barrier: act_flag[1] counts the workgroups that are done
+// (zeroed by group_kernel); the release fence before the count writes
+// their act back to memory, the acquire fence after the wait drops stale
+// lines from this XCD's L2.  The wait is bounded (device flag 128).
+__device__ __forceinline__ void act_fix(const PrefillArgs& a) {
+    const int P = a.T * a.K, nb = a.I >> 5, lane = threadIdx.x & 63;
+    for (int p = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6); p < P; p += (int)gridDim.x * 4) {
+        uint8_t* ep = a.act_exp + (size_t)p * nb;
+        int E = 0;
+        for (int b = lane; b < nb; b += 64) E = max(E, (int)ep[b]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) E = max(E, __shfl_xor(E, o));
+        if (E == 0) continue;
+        _Float16* row = a.act + (size_t)p * a.I;
+        for (int j = lane * 8; j < a.I; j += 512) {
+            const int e = ep[j >> 5];
+            if (e == E) continue;
+            const float f = __builtin_bit_cast(float, (127 + e - E) << 23);   // e - E >= -113
+            _Float16 v[8];
+            *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(row + j);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = (_Float16)((float)v[i] * f);
+            *reinterpret_cast<uint4*>(row + j) = *reinterpret_cast<const uint4*>(v);
+        }
+        // every lane has read ep[] (the loop above ends in its last read)
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) ep[0] = (uint8_t)E;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __hip_atomic_fetch_add(&a.act_flag[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int it = 0;; ++it) {
+            if (__hip_atomic_load(&a.act_flag[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+                gridDim.x)
+                break;
+            if (it >= kPfSpinLimit) {
+                flag_error(a.err, 128u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+}
+
 // Persistent: the workgroups of an XCD take the (N-tile, M-tile) items of
 // their queue in rounds of W (W workgroups on the queue), workgroup j taking
 // item j of the even rounds and item W - 1 - j of the odd ones.  Queue x
@@ -478,6 +534,10 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
     const int xcds = (8 - queue + nq - 1) / nq;               // block id residues on this queue
     const int per_queue = (int)(gridDim.x >> 3) * xcds;       // workgroups taking this queue
     const int first = (int)(blockIdx.x >> 3) * xcds + (int)(blockIdx.x & 7) / nq;
+    // down, only when the gate/up GEMM stored some block of act times 2^-e,
+    // e > 0: every pair brought to one exponent first, by all workgroups
+    const bool scaled = NMAT == 1 && a.act_flag[0] != 0u;
+    if (NMAT == 1 && scaled) act_fix(a);
     for (int r = 0;; ++r) {
         // the queue is dealt out forwards in even rounds and backwards in odd
         // ones: the workgroups that took the largest items of a round take
@@ -575,17 +635,12 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
         // epilogue: lane holds pair q * 32 + c and, per row-mat, accumulator rows
         // 8 v + 4 kh + i (element 4 v + i); each row's 2^k comes back on it
         if (NMAT == 2 && wrow0 < M) {
-            float rs[2][4][4];
-#pragma unroll
-            for (int m = 0; m < 2; ++m)
-#pragma unroll
-                for (int v = 0; v < 4; ++v)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int col = perm8(4 * kh + i);
-                        rs[m][v][i] =
-                            row_scale((col < 4 ? kx[m][v].x : kx[m][v].y) >> (8 * (col & 3)));
-                    }
+            // the row's 2^k, taken from kx where it is used (a table of all 32
+            // would stay live through the epilogue)
+            auto rs = [&](int m, int v, int i) {
+                const int col = perm8(4 * kh + i);
+                return row_scale((col < 4 ? kx[m][v].x : kx[m][v].y) >> (8 * (col & 3)));
+            };
             // act goes out in blocks of 32 values, this wave's 32 rows of one pair
             // (16 on each lane of c and c + 32): a block whose largest |value|
             // is past the f16 range is stored times 2^-e, e >= 1 the least that
@@ -603,17 +658,18 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
                 for (int v = 0; v < 4; ++v)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float g = acc[0][q][4 * v + i] * rs[0][v][i] * inv;
-                        const float u = acc[1][q][4 * v + i] * rs[1][v][i] * inv;
+                        const float g = acc[0][q][4 * v + i] * rs(0, v, i) * inv;
+                        const float u = acc[1][q][4 * v + i] * rs(1, v, i) * inv;
                         y[v][i] = silu_fast(g) * u;  // Shaders.metal:148
                         const bool fin = isfinite(y[v][i]);
                         bad |= !fin;
                         mx = fin ? fmaxf(mx, fabsf(y[v][i])) : mx;
                     }
                 mx = fmaxf(mx, __shfl_xor(mx, 32));
-                // mx / 65504 = m 2^e with m in [0.5, 1): mx 2^-e < 65504
-                int e = 0;
-                if (mx > 65504.f) (void)frexpf(mx * (1.f / 65504.f), &e);
+                // r = mx / 65504 > 1 is m 2^e with m in [0.5, 1) (e its exponent
+                // field - 126): mx 2^-e < 65504
+                const float r = mx * (1.f / 65504.f);
+                const int e = mx > 65504.f ? (int)((__float_as_uint(r) >> 23) & 255u) - 126 : 0;
                 scaled |= e > 0;
                 const float sc = __builtin_bit_cast(float, (127 - e) << 23);   // 2^-e, e <= 113
                 _Float16* dst = a.act + (size_t)(p0 + n) * a.I + wrow0 + 4 * kh;
@@ -628,7 +684,7 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
                 if (kh == 0) a.act_exp[(size_t)(p0 + n) * nb + (wrow0 >> 5)] = (uint8_t)e;
             }
             if (__any(bad) && lane == 0) flag_error(a.err, 64u);
-            if (__any(scaled) && lane == 0) *a.act_flag = 1u;
+            if (__any(scaled) && lane == 0) a.act_flag[0] = 1u;
         } else if (NMAT == 1) {
 #pragma unroll
             for (int rm = 0; rm < 2; ++rm) {
@@ -644,11 +700,15 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
                     const int n = q * 32 + c;
                     if (n >= np) continue;
                     float* dst = a.y + (size_t)(p0 + n) * a.h + rb + 4 * kh;
+                    // the pair's 2^E (1 unless scaled; exact): E in the first
+                    // byte of its act exponents (act_fix)
+                    const int pE = scaled ? a.act_exp[(size_t)(p0 + n) * (a.I >> 5)] : 0;
+                    const float pe = __builtin_bit_cast(float, (127 + pE) << 23);
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
                         *reinterpret_cast<f32x4*>(dst + 8 * v) = f32x4{
-                            acc[rm][q][4 * v] * rs[v][0], acc[rm][q][4 * v + 1] * rs[v][1],
-                            acc[rm][q][4 * v + 2] * rs[v][2], acc[rm][q][4 * v + 3] * rs[v][3]};
+                            acc[rm][q][4 * v] * rs[v][0] * pe, acc[rm][q][4 * v + 1] * rs[v][1] * pe,
+                            acc[rm][q][4 * v + 2] * rs[v][2] * pe, acc[rm][q][4 * v + 3] * rs[v][3] * pe};
                 }
             }
         }
@@ -764,54 +824,20 @@ __global__ __launch_bounds__(256) void pf_tile_copy_kernel(const uint8_t* src, u
                               within) = v;
 }
 
-// ---- act exponents ----------------------------------------------------------------
-
-// After the gate/up GEMM, and only when it stored some block of act with
-// e > 0: every pair's blocks are brought to the pair's largest e, E (a block
-// with e < E is multiplied by 2^(e - E) in place, in f16), and pair_scale
-// gets 2^E, which the combine multiplies the pair's down output by.  One
-// wave per pair, 8 values per lane and step.
-__global__ __launch_bounds__(256) void pf_act_fix_kernel(PrefillArgs a) {
-    if (*a.act_flag == 0u) return;
-    const int P = a.T * a.K, nb = a.I >> 5, lane = threadIdx.x & 63;
-    for (int p = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6); p < P; p += (int)gridDim.x * 4) {
-        const uint8_t* ep = a.act_exp + (size_t)p * nb;
-        int E = 0;
-        for (int b = lane; b < nb; b += 64) E = max(E, (int)ep[b]);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) E = max(E, __shfl_xor(E, o));
-        if (lane == 0) a.pair_scale[p] = __builtin_bit_cast(float, (127 + E) << 23);
-        if (E == 0) continue;
-        _Float16* row = a.act + (size_t)p * a.I;
-        for (int j = lane * 8; j < a.I; j += 512) {
-            const int e = ep[j >> 5];
-            if (e == E) continue;
-            const float f = __builtin_bit_cast(float, (127 + e - E) << 23);   // e - E >= -113
-            _Float16 v[8];
-            *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(row + j);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (_Float16)((float)v[i] * f);
-            *reinterpret_cast<uint4*>(row + j) = *reinterpret_cast<const uint4*>(v);
-        }
-    }
-}
-
 // ---- combine ----------------------------------------------------------------------
 
 // out[t][d] = residual[t][d] + sum_k w[t][k] * y[pos[t,k]][d], k ascending
-// (Shaders.metal:371-374); four columns per thread.  y of a pair with E > 0
-// is the output times 2^-E: w is multiplied by 2^E (exact).
+// (Shaders.metal:371-374); four columns per thread.
 __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     const int t = blockIdx.y;
     const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (d >= a.h) return;
-    const bool scaled = *a.act_flag != 0u;
     float4 acc = a.residual ? *reinterpret_cast<const float4*>(a.residual + (size_t)t * a.h + d)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k = 0; k < a.K; ++k) {
-        const int q = a.pos[(size_t)t * a.K + k];
-        const float w = a.w[(size_t)t * a.K + k] * (scaled ? a.pair_scale[q] : 1.f);
-        const float4 y = *reinterpret_cast<const float4*>(a.y + (size_t)q * a.h + d);
+        const float w = a.w[(size_t)t * a.K + k];
+        const float4 y = *reinterpret_cast<const float4*>(
+            a.y + (size_t)a.pos[(size_t)t * a.K + k] * a.h + d);
         acc.x = fmaf(w, y.x, acc.x);
         acc.y = fmaf(w, y.y, acc.y);
         acc.z = fmaf(w, y.z, acc.z);
@@ -841,9 +867,6 @@ int launch_gemms(const PrefillArgs& a, hipStream_t st) {
     launch_one<2, GSL>(a, st, ntiles_max);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(pf_act_fix_kernel, dim3((unsigned)std::min((P + 3) / 4, 1024)), dim3(256), 0,
-                       st, a);
-    if ((e = hipGetLastError()) != hipSuccess) return (int)e;
     launch_one<1, GSL>(a, st, ntiles_max);
     return (int)hipGetLastError();
 }

@@ -245,8 +245,8 @@ void prefill_scratch_sizes(const m1moe::Geom& g, int32_t T, uint64_t sz[m1moe::k
     sz[6] = (P / m1moe::kPfTN + E + 1) * 16;
     sz[7] = P * g.I * 2;
     sz[8] = P * g.h * 4;
-    sz[9] = P * (g.I / 32);
-    sz[10] = 8;
+    sz[9] = P * (g.I / 32) + 4;   // (+4: the down GEMM reads E as a whole aligned word)
+    sz[10] = 4 * (m1moe::kPfFlagWords + (P + 31) / 32);
 }
 
 // Bytes of the kPfBufs buffers carved from one block, each 256-byte aligned.

@@ -211,11 +211,13 @@ int32_t m1moe_attention_decode(m1moe_ctx_t ctx, const float* d_q, const float* d
     a.hpkv = num_heads / num_kv_heads;
     a.head_dim = head_dim;
     a.qh = attention_qh(a.hpkv);
-    a.chunk = attention_chunk(seq_len);
+    a.cus = ctx->cus;
+    a.chunk = attention_chunk(seq_len, num_heads / a.qh, a.cus);
+    a.kv_pos = (int64_t)num_kv_heads * head_dim;   // the caller's [seq_len][num_kv_heads][head_dim]
+    a.kv_head = head_dim;
     a.scale = 1.0f / sqrtf((float)head_dim);
     a.gen = ctx->attn_cnt + kAttnCounters;
     a.fin = ctx->attn_cnt + kAttnCounters + 1;
-    a.cus = ctx->cus;
     a.spin_limit = kAttnSpinLimit;
     a.sync_merge = attention_grid_fits(a) ? 1 : 0;
     return launched(launch_attention(a, ctx->stream), "attention");
@@ -397,13 +399,15 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
     at.hpkv = dec->sh.num_heads / dec->sh.num_kv_heads;
     at.head_dim = hd;
     at.qh = attention_qh(at.hpkv);
-    at.chunk = attention_chunk(dec->sh.max_seq);
+    at.cus = ctx->cus;
+    at.chunk = attention_chunk(dec->sh.max_seq, at.num_heads / at.qh, at.cus);
+    at.kv_pos = kvd;
+    at.kv_head = hd;
     at.scale = 1.0f / sqrtf((float)hd);
     at.rope_theta = dec->sh.rope_theta;
     at.eps = eps;
     at.gen = dec->cnt + 2 + dec->sh.num_heads;
     at.fin = dec->cnt + 3 + dec->sh.num_heads;
-    at.cus = ctx->cus;
     at.spin_limit = kAttnSpinLimit;
     at.sync_merge = attention_grid_fits(at) ? 1 : 0;
     at.rope = dec->rope;

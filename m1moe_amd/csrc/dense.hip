@@ -30,6 +30,7 @@
 // back to 0, so a captured graph can replay the kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "device.hpp"
@@ -493,6 +494,20 @@ __device__ void attn_merge_share(const AttnArgs& a, int g, int c, int nch, int n
     const size_t cstride = (size_t)QH * (HD + 2);
     const unsigned long long* base =
         reinterpret_cast<const unsigned long long*>(a.partial) + (size_t)g * nch * cstride;
+    // this lane's share (below) is requested first, with the statistics: one
+    // memory round trip when every chunk is in
+    const int S = (QH * HD + nact - 1) / nact;
+    const int R = attn_share_lanes(S);
+    const int oi = tid / R, r = tid - oi * R, o = c * S + oi;
+    const bool mine = oi < S && o < QH * HD;
+    const int i = mine ? o / HD : 0, d = mine ? o - i * HD : 0;
+    constexpr int kMaxPer = attn_share_max<HD, QH>();
+    const int nper = mine ? (nact - r + R - 1) / R : 0;  // chunks r, r + R, ...
+    unsigned long long u0[kMaxPer];
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j)
+        u0[j] = j < nper ? ld_coh_u64(base + (size_t)(r + R * j) * cstride + i * (HD + 2) + 2 + d)
+                         : 0ull;
     // the statistics of every (head, chunk): 2 QH nact pairs, up to 4 per thread
     constexpr int kSt = (2 * QH * kAttnMaxChunks + 255) / 256;
     bool ok = true;
@@ -532,13 +547,6 @@ __device__ void attn_merge_share(const AttnArgs& a, int g, int c, int nch, int n
         if (lane == 0) s_l[i] = l;
     }
     __syncthreads();
-    const int S = (QH * HD + nact - 1) / nact;
-    const int R = attn_share_lanes(S);
-    const int oi = tid / R, r = tid - oi * R, o = c * S + oi;
-    const bool mine = oi < S && o < QH * HD;
-    const int i = mine ? o / HD : 0, d = mine ? o - i * HD : 0;
-    constexpr int kMaxPer = attn_share_max<HD, QH>();
-    const int nper = mine ? (nact - r + R - 1) / R : 0;  // chunks r, r + R, ...
     float vals[kMaxPer];
     bool have[kMaxPer];
 #pragma unroll
@@ -548,11 +556,13 @@ __device__ void attn_merge_share(const AttnArgs& a, int g, int c, int nch, int n
     }
     for (int it = 0; ok; ++it) {
         // every missing value of the lane is requested before any is examined
+        // (the first round's were requested with the statistics)
         unsigned long long u[kMaxPer];
 #pragma unroll
         for (int j = 0; j < kMaxPer; ++j)
-            u[j] = have[j] ? 0ull
-                           : ld_coh_u64(base + (size_t)(r + R * j) * cstride + i * (HD + 2) + 2 + d);
+            u[j] = it == 0 ? u0[j]
+                   : have[j] ? 0ull
+                             : ld_coh_u64(base + (size_t)(r + R * j) * cstride + i * (HD + 2) + 2 + d);
         bool cur = true;
 #pragma unroll
         for (int j = 0; j < kMaxPer; ++j) {
@@ -607,7 +617,22 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lp = lane % LP, pg = lane / LP;
     const int h0 = g * QH, kvh = h0 / a.hpkv;
-    const size_t kvd = (size_t)a.num_kv_heads * HD;
+    // this wave's q heads it = wave, wave + 4, ... (it == QH: the new k row)
+    // and the new v row, requested before the position they wait on
+    constexpr int QW = (QH + 4) / 4;   // items per wave at most
+    float qpre[QW][HD / 64];
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+        const int it = wave + 4 * j;
+        const float* src = it < QH ? a.q + (size_t)(h0 + it) * HD
+                                   : (it == QH && a.fused ? a.k_new + (size_t)kvh * HD : nullptr);
+#pragma unroll
+        for (int e = 0; e < HD / 64; ++e) qpre[j][e] = src ? src[lane + 64 * e] : 0.f;
+    }
+    float vpre[(HD + 255) / 256];
+#pragma unroll
+    for (int e = 0; e < (HD + 255) / 256; ++e)
+        vpre[e] = (a.fused && tid + 256 * e < HD) ? a.v_new[(size_t)kvh * HD + tid + 256 * e] : 0.f;
     int p = -1, seq;
     if (a.fused) {
         p = *a.pos;
@@ -644,7 +669,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 const int pp = p0 + wave * PW + it * PPI + pg;
                 float4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, v0 = k0, v1 = k0;
                 if (pp < c1 && !(has_new && pp == p)) {
-                    const size_t off = (size_t)pp * kvd + (size_t)kvh * HD + 8 * lp;
+                    const size_t off = (size_t)pp * a.kv_pos + (size_t)kvh * a.kv_head + 8 * lp;
                     k0 = *reinterpret_cast<const float4*>(a.kcache + off);
                     k1 = *reinterpret_cast<const float4*>(a.kcache + off + 4);
                     v0 = *reinterpret_cast<const float4*>(a.vcache + off);
@@ -669,16 +694,18 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         // RMSNorm (InferenceEngine.swift:538-548), then RoPE (:521-536)
         const bool mine_new = has_new && p >= c0 && p < c1;
         const int items = QH + (mine_new ? 1 : 0);
-        for (int it = wave; it < items; it += 4) {
+#pragma unroll
+        for (int jw = 0; jw < QW; ++jw) {
+            const int it = wave + 4 * jw;
+            if (it >= items) break;
             const bool is_k = it == QH;
-            const float* src = is_k ? a.k_new + (size_t)kvh * HD : a.q + (size_t)(h0 + it) * HD;
             float* dst = is_k ? s_kv[0] : s_q[it];
             const uint16_t* nw = is_k ? a.k_norm : a.q_norm;
             float v[HD / 64];
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < HD / 64; ++j) {
-                v[j] = src[lane + 64 * j];
+                v[j] = qpre[jw][j];
                 ss = fmaf(v[j], v[j], ss);
             }
             if (a.fused && nw) {
@@ -689,8 +716,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
             for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = v[j];
         }
-        if (mine_new)
-            for (int d = tid; d < HD; d += 256) s_kv[1][d] = a.v_new[(size_t)kvh * HD + d];
+        if (mine_new) {
+#pragma unroll
+            for (int e = 0; e < (HD + 255) / 256; ++e)
+                if (tid + 256 * e < HD) s_kv[1][tid + 256 * e] = vpre[e];
+        }
         __syncthreads();
         if (a.fused) {
             for (int t = tid; t < items * HALF; t += 256) {
@@ -715,8 +745,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             // the new row into the caches, by the first group of its kv head
             if (mine_new && h0 % a.hpkv == 0) {
                 for (int d = tid; d < HD; d += 256) {
-                    a.kcache[(size_t)p * kvd + (size_t)kvh * HD + d] = s_kv[0][d];
-                    a.vcache[(size_t)p * kvd + (size_t)kvh * HD + d] = s_kv[1][d];
+                    a.kcache[(size_t)p * a.kv_pos + (size_t)kvh * a.kv_head + d] = s_kv[0][d];
+                    a.vcache[(size_t)p * a.kv_pos + (size_t)kvh * a.kv_head + d] = s_kv[1][d];
                 }
             }
         }
@@ -1084,13 +1114,30 @@ int attention_qh(int hpkv) {
     return 1;
 }
 
-int attention_chunk(int max_positions) {
+// The fewest 64-position sub-chunks per workgroup that keep at most
+// kAttnMaxChunks workgroups per group.
+int attention_chunk_min(int max_positions) {
     const int sub = (max_positions + kAttnChunk - 1) / kAttnChunk;  // 64-position sub-chunks
     return kAttnChunk * ((sub + kAttnMaxChunks - 1) / kAttnMaxChunks);
 }
 
+// When that grid is two or more workgroups per CU, one workgroup per CU
+// taking more sub-chunks instead: measured (32 q / 8 kv heads of 128, 256
+// CUs) 19.8 -> 16.1 us at 4096 positions, 34.5 -> 25.7 us at 8192; below two
+// rounds (2112 positions: 264 workgroups) the 64-position chunks stay
+// (13.5 us, against 14.4 us for 256 workgroups of 66).
+int attention_chunk(int max_positions, int groups, int cus) {
+    const int c = attention_chunk_min(max_positions);
+    const long wgs = (long)groups * ((max_positions + c - 1) / c);
+    const int per = std::min(kAttnMaxChunks, groups > 0 ? cus / groups : 0);   // chunks per group
+    if (per < 1 || wgs < 2L * cus) return c;
+    const int sub = (max_positions + kAttnChunk - 1) / kAttnChunk;
+    return std::max(c, kAttnChunk * ((sub + per - 1) / per));
+}
+
+// (sized for attention_chunk_min, whose chunk count bounds attention_chunk's)
 int attention_partial_floats(int num_heads, int head_dim, int max_positions) {
-    const int chunk = attention_chunk(max_positions);
+    const int chunk = attention_chunk_min(max_positions);
     return 2 * num_heads * ((max_positions + chunk - 1) / chunk) * (head_dim + 2);
 }
 
@@ -1139,8 +1186,10 @@ bool attention_grid_fits(const AttnArgs& a) {
 
 int launch_attention(const AttnArgs& a, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (a.qh <= 0 || a.num_heads % a.qh || a.hpkv % a.qh || a.chunk != attention_chunk(a.max_seq))
+    if (a.qh <= 0 || a.num_heads % a.qh || a.hpkv % a.qh ||
+        a.chunk != attention_chunk(a.max_seq, a.num_heads / a.qh, a.cus))
         return (int)hipErrorInvalidValue;
+    if (a.kv_pos <= 0 || a.kv_head <= 0) return (int)hipErrorInvalidValue;
     if (a.sync_merge && !(a.gen && a.fin && attention_grid_fits(a))) return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.num_heads / a.qh), (unsigned)((a.max_seq + a.chunk - 1) / a.chunk));
     switch (a.head_dim) {

@@ -202,8 +202,10 @@ struct PrefillArgs {
     _Float16* act;               // [T*K][I] silu(gate)*up per sorted pair (per block: act_exp)
     float* y;                    // [T*K][h] expert outputs per sorted pair
     uint8_t* act_exp;            // [T*K][I/32] e >= 0 of each 32-value block: act held act * 2^-e
-    uint32_t* act_flag;          // [2] 1 when some e > 0 (the down GEMM then reads act_exp);
-                                 // the down GEMM's barrier count
+    uint32_t* act_flag;          // [kPfFlagWords + ceil(T*K/32)]: word 0 is 1 when some e > 0
+                                 // (the down GEMM then reads act_exp); words 32 .. 32 * 18 - 1
+                                 // the down GEMM's barrier; then a bit per pair whose act
+                                 // row its prologue rewrote
     uint32_t* err;               // sticky device error flag
 };
 
@@ -213,6 +215,7 @@ constexpr int kPfBufs = 11;
 
 constexpr int kPfTN = 128;  // prefill GEMM: (token, slot) pairs per workgroup tile
 constexpr int kPfSpinLimit = 1 << 20;   // bounded wait of the down GEMM's rare grid barrier
+constexpr int kPfFlagWords = 32 * 18;    // act_flag words before the rewritten-row bitmap
 
 // m1moe_moe_prefill_noalloc: bytes of the per-GPU static scratch (scratch.hip)
 // that holds its prefill buffers.  64 MiB: 776 tokens at hidden 2048,
@@ -307,7 +310,7 @@ struct MvArgs {
 
 // Decode attention of one query position.  Workgroup (g, c): q heads
 // g*qh .. g*qh+qh-1 (one kv head) over positions c*chunk .. (c+1)*chunk - 1
-// (chunk = attention_chunk(max_seq): a multiple of 64, at most
+// (chunk = attention_chunk(max_seq, groups, cus): a multiple of 64, at most
 // kAttnMaxChunks workgroups per kv head).
 //   fused = 1: q, k_new, v_new are the raw projections of the current token;
 //     q and k get the per-head RMSNorm (q_norm/k_norm non-null) and RoPE at
@@ -323,8 +326,9 @@ struct AttnArgs {
     const float* v_new;
     const uint16_t* q_norm;      // [head_dim] or null
     const uint16_t* k_norm;
-    float* kcache;               // [max_seq][num_kv_heads * head_dim]
+    float* kcache;               // row (position pp, kv head h) at pp * kv_pos + h * kv_head
     float* vcache;
+    int64_t kv_pos, kv_head;     // floats between positions and between kv heads
     float* out;                  // [num_heads][head_dim]
     float* partial;              // [groups][chunks][qh][head_dim + 2]
     uint32_t* counters;          // [groups]
@@ -425,8 +429,10 @@ int matvec_workgroups(int rows);
 int launch_matvec_bf16(const MvArgs& a, void* stream);
 // q heads per attention workgroup (0: unsupported hpkv).
 int attention_qh(int hpkv);
-// Positions per attention workgroup for a cache of max_positions.
-int attention_chunk(int max_positions);
+// Positions per attention workgroup for a cache of max_positions, groups
+// (num_heads / qh) workgroups per chunk and cus compute units: a multiple of
+// 64, at most kAttnMaxChunks chunks.
+int attention_chunk(int max_positions, int groups, int cus);
 // The whole attention grid of `a` fits on the device at once (a.cus CUs, the
 // occupancy of the kernel instance it launches): the synchronous merge may
 // be used.

@@ -97,7 +97,9 @@ __global__ __launch_bounds__(1024) void group_kernel(PrefillArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.E, P = a.T * a.K;
     if (tid < kMaxE) cnt[tid] = 0;
-    if (tid < 2) a.act_flag[tid] = 0u;   // the down GEMM's flag (set by gate/up) and barrier count
+    // the down GEMM's flag (set by gate/up), barrier words and bitmap of
+    // rewritten act rows (act_fix)
+    for (int j = tid; j < kPfFlagWords + (P + 31) / 32; j += 1024) a.act_flag[j] = 0u;
     __syncthreads();
     const bool one_pass = P <= 1024 * kGP;
     int pe[kGP], pr[kGP];
@@ -336,6 +338,14 @@ __device__ __forceinline__ void lds_copy16(uint32_t voff, const uint8_t* sbase, 
                  : "v"(voff), "s"(sbase), "s"(lds)
                  : "memory");
 }
+// The same, coherent across the XCDs (sc1: the line is read from memory, not
+// from this XCD's L2): the down GEMM's B when act_fix rewrote act in this launch.
+__device__ __forceinline__ void lds_copy16_coh(uint32_t voff, const uint8_t* sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 sc1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory");
+}
 __device__ __forceinline__ void lds_copy4(uint32_t voff, const uint8_t* sbase, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
                  :
@@ -356,7 +366,7 @@ constexpr int mma_ops() { return 2 + (GSL == 0 ? 2 : 1) + NQ; }
 // Issued for every step, also past the last block (kb is then clamped: the
 // last block is read again into a slot no step reads), so that every wave
 // always has the same number of copies issued after any block's.
-template <int GSL, int NQ, int SLOT>
+template <int GSL, int NQ, int SLOT, bool COH>
 __device__ __forceinline__ void mma_issue(const MmaSrc& src, int kb, int nblk, uint32_t ring) {
     kb = min(kb, nblk - 1);
     const uint32_t st = ring + SLOT * mma_stage_q<GSL, NQ>();
@@ -368,8 +378,12 @@ __device__ __forceinline__ void mma_issue(const MmaSrc& src, int kb, int nblk, u
         lds_copy4(src.soff[i], ab, st + kMA + i * 1024 + src.wave * 256);
     const uint8_t* bb = src.bbase + (size_t)kb * (kMK * 2);
 #pragma unroll
-    for (int i = 0; i < NQ; ++i)
-        lds_copy16(src.boff[i], bb, st + kMA + mma_sbytes<GSL>() + (NQ * src.wave + i) * 1024);
+    for (int i = 0; i < NQ; ++i) {
+        if (COH)
+            lds_copy16_coh(src.boff[i], bb, st + kMA + mma_sbytes<GSL>() + (NQ * src.wave + i) * 1024);
+        else
+            lds_copy16(src.boff[i], bb, st + kMA + mma_sbytes<GSL>() + (NQ * src.wave + i) * 1024);
+    }
 }
 
 template <int GSL, int NQ>
@@ -427,7 +441,8 @@ __device__ __forceinline__ void mma_round(int kb, F& step) {
 // in flight), passes the barrier after which every wave is done with block
 // kb - 1's slot, issues block kb + NS - 1 into that slot and multiplies
 // block kb.
-template <int GSL, int NQ>
+// (COH: B copied with lds_copy16_coh)
+template <int GSL, int NQ, bool COH>
 __device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint8_t* ring,
                                          f32x16 (&acc)[2][4]) {
     constexpr int ops = mma_ops<GSL, NQ>();
@@ -437,7 +452,7 @@ __device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint
     const uint32_t rl = lds_addr(ring);
     auto first = [&](int kb, auto slot) {
         constexpr int S = decltype(slot)::value;
-        if constexpr (S < NS - 1) mma_issue<GSL, NQ, S>(src, kb, nblk, rl);
+        if constexpr (S < NS - 1) mma_issue<GSL, NQ, S, COH>(src, kb, nblk, rl);
     };
     mma_round<0, NS>(0, first);
     auto step = [&](int kb, auto slot) {
@@ -446,7 +461,7 @@ __device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint
         wait_vm<ops * (NS - 2)>();  // block kb's copies are in (the next NS - 2 may not be)
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        mma_issue<GSL, NQ, (S + NS - 1) % NS>(src, kb + NS - 1, nblk, rl);
+        mma_issue<GSL, NQ, (S + NS - 1) % NS, COH>(src, kb + NS - 1, nblk, rl);
         __builtin_amdgcn_sched_barrier(0);
         mma_compute<GSL, NQ>(src, ring + S * stage, acc);
     };
@@ -455,15 +470,31 @@ __device__ __forceinline__ void mma_loop(const MmaSrc& src, int nblk, const uint
     wait_vm<0>();
 }
 
+// Stores coherent across the XCDs (sc1: written through to memory), for
+// what act_fix hands to other workgroups.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st_coh16(void* p, u32x4v v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_coh_u8(uint8_t* p, uint32_t v) {
+    asm volatile("global_store_byte %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
 // act blocks to one exponent per pair (the down GEMM's prologue when
 // act_flag[0] is set; every workgroup of the launch, all of them resident):
 // wave w of the grid takes pairs w, w + 4 grid, ...; a block with e < E, E
 // the pair's largest e, is multiplied by 2^(e - E) in place (in f16), and E
 // goes to the pair's first act exponent byte, where the epilogue reads it.
-// Then a grid barrier: act_flag[1] counts the workgroups that are done
-// (zeroed by group_kernel); the release fence before the count writes
-// their act back to memory, the acquire fence after the wait drops stale
-// lines from this XCD's L2.  The wait is bounded (device flag 128).
+// Those writes are coherent (st_coh16, st_coh_u8) and so are their readers
+// (lds_copy16_coh for the tiles with a rewritten row, agent-scope loads of
+// the E words): no cache
+// write-back or invalidation.  Bit p of the bitmap after the barrier words
+// marks pair p's row as rewritten.  Then a grid barrier in two levels (one
+// address taking every workgroup's count and poll costs microseconds): the
+// workgroups of residue x = block id % 8 count themselves on word x, the
+// last of them counts residue x on the second-level word, and the last of
+// those releases the 8 replicas that the workgroups of each residue poll
+// (all zeroed by group_kernel); the waits are bounded (device flag 128).
 __device__ __forceinline__ void act_fix(const PrefillArgs& a) {
     const int P = a.T * a.K, nb = a.I >> 5, lane = threadIdx.x & 63;
     for (int p = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6); p < P; p += (int)gridDim.x * 4) {
@@ -474,35 +505,49 @@ __device__ __forceinline__ void act_fix(const PrefillArgs& a) {
         for (int o = 32; o >= 1; o >>= 1) E = max(E, __shfl_xor(E, o));
         if (E == 0) continue;
         _Float16* row = a.act + (size_t)p * a.I;
+        bool rewrote = false;
         for (int j = lane * 8; j < a.I; j += 512) {
             const int e = ep[j >> 5];
             if (e == E) continue;
+            rewrote = true;
             const float f = __builtin_bit_cast(float, (127 + e - E) << 23);   // e - E >= -113
             _Float16 v[8];
             *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(row + j);
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = (_Float16)((float)v[i] * f);
-            *reinterpret_cast<uint4*>(row + j) = *reinterpret_cast<const uint4*>(v);
+            st_coh16(row + j, __builtin_bit_cast(u32x4v, v));
         }
         // every lane has read ep[] (the loop above ends in its last read)
         __builtin_amdgcn_wave_barrier();
-        if (lane == 0) ep[0] = (uint8_t)E;
+        const bool any = __any(rewrote);
+        if (lane == 0) {
+            st_coh_u8(ep, (uint32_t)E);
+            if (any)
+                __hip_atomic_fetch_or(a.act_flag + kPfFlagWords + (p >> 5), 1u << (p & 31),
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's stores are complete
     __syncthreads();
     if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __hip_atomic_fetch_add(&a.act_flag[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t x = blockIdx.x & 7u, per = gridDim.x >> 3;   // (the grid is a multiple of 8)
+        uint32_t* rel = a.act_flag + 32 * (10 + x);
+        if (__hip_atomic_fetch_add(a.act_flag + 32 * (1 + x), 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) == per - 1 &&
+            __hip_atomic_fetch_add(a.act_flag + 32 * 9, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) == 7u) {
+            for (int r = 0; r < 8; ++r)
+                __hip_atomic_store(a.act_flag + 32 * (10 + r), 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
         for (int it = 0;; ++it) {
-            if (__hip_atomic_load(&a.act_flag[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
-                gridDim.x)
-                break;
+            if (__hip_atomic_load(rel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
             if (it >= kPfSpinLimit) {
                 flag_error(a.err, 128u);
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
 }
@@ -625,11 +670,43 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[rm][q][v] = 0.f;
-        switch (nq4) {
-            case 1: mma_loop<GSL, 1>(src, K / kMK, s_ring, acc); break;
-            case 2: mma_loop<GSL, 2>(src, K / kMK, s_ring, acc); break;
-            case 3: mma_loop<GSL, 3>(src, K / kMK, s_ring, acc); break;
-            default: mma_loop<GSL, 4>(src, K / kMK, s_ring, acc); break;
+        // (scaled) B read coherently when a row of the tile was rewritten;
+        // the E of the lane's pair of quarter q (act_fix): the aligned word
+        // Ew[q] holding it is requested now, taken apart in the epilogue
+        // (byte Esh[q] / 8), so that its load's latency passes with the GEMM
+        bool coh = false;
+        uint32_t Ew[4] = {0u, 0u, 0u, 0u}, Esh = 0u;
+        if (NMAT == 1 && scaled) {
+            for (int wi = p0 >> 5; wi <= (p0 + np - 1) >> 5; ++wi) {
+                const uint32_t m = __hip_atomic_load(a.act_flag + kPfFlagWords + wi,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int lo = max(p0 - 32 * wi, 0), hi = min(p0 + np - 32 * wi, 32);   // bits [lo, hi)
+                const uint32_t mask = (hi >= 32 ? ~0u : (1u << hi) - 1u) & ~((1u << lo) - 1u);
+                coh = coh || (m & mask) != 0u;
+            }
+            // (act_exp is 256-byte aligned: byte offset o lies in word o / 4)
+            uint32_t* xw = reinterpret_cast<uint32_t*>(a.act_exp);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const size_t o = (size_t)(p0 + min(q * 32 + c, np - 1)) * (a.I >> 5);
+                Ew[q] = __hip_atomic_load(xw + (o >> 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                Esh |= (uint32_t)(o & 3) << (8 * q);
+            }
+        }
+        if (NMAT == 1 && coh) {
+            switch (nq4) {
+                case 1: mma_loop<GSL, 1, true>(src, K / kMK, s_ring, acc); break;
+                case 2: mma_loop<GSL, 2, true>(src, K / kMK, s_ring, acc); break;
+                case 3: mma_loop<GSL, 3, true>(src, K / kMK, s_ring, acc); break;
+                default: mma_loop<GSL, 4, true>(src, K / kMK, s_ring, acc); break;
+            }
+        } else {
+            switch (nq4) {
+                case 1: mma_loop<GSL, 1, false>(src, K / kMK, s_ring, acc); break;
+                case 2: mma_loop<GSL, 2, false>(src, K / kMK, s_ring, acc); break;
+                case 3: mma_loop<GSL, 3, false>(src, K / kMK, s_ring, acc); break;
+                default: mma_loop<GSL, 4, false>(src, K / kMK, s_ring, acc); break;
+            }
         }
 
         // epilogue: lane holds pair q * 32 + c and, per row-mat, accumulator rows
@@ -702,7 +779,7 @@ __global__ __launch_bounds__(256, 2) void pf_mma_kernel(PrefillArgs a, int m_til
                     float* dst = a.y + (size_t)(p0 + n) * a.h + rb + 4 * kh;
                     // the pair's 2^E (1 unless scaled; exact): E in the first
                     // byte of its act exponents (act_fix)
-                    const int pE = scaled ? a.act_exp[(size_t)(p0 + n) * (a.I >> 5)] : 0;
+                    const int pE = (int)((Ew[q] >> (8 * ((Esh >> (8 * q)) & 3u))) & 255u);
                     const float pe = __builtin_bit_cast(float, (127 + pE) << 23);
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
@@ -846,16 +923,33 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     *reinterpret_cast<float4*>(a.out + (size_t)t * a.h + d) = acc;
 }
 
-// Two persistent workgroups per compute unit (at most one per item), a
-// multiple of 8 so that every XCD holds the same number.
+// Workgroups of pf_mma_kernel<NMAT, GSL> one compute unit holds at once (2
+// by its launch bounds and LDS; asked of the runtime once per process).
+template <int NMAT, int GSL>
+int pf_resident_per_cu() {
+    static const int n = [] {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, pf_mma_kernel<NMAT, GSL>, 256, 0) !=
+                hipSuccess ||
+            b < 1)
+            b = 1;
+        return std::min(b, 2);
+    }();
+    return n;
+}
+
+// Persistent workgroups, as many as the compute units hold at once (two per
+// CU; at most one per item), a multiple of 8 so that every XCD holds the
+// same number.  All of them resident is what the down GEMM's rare grid
+// barrier (act_fix) needs.
 template <int NMAT, int GSL>
 void launch_one(const PrefillArgs& a, hipStream_t st, int ntiles_max) {
     const int M = NMAT == 2 ? a.I : a.h;
     constexpr int TM = NMAT == 2 ? 128 : 256;
     const int m_tiles = (M + TM - 1) / TM;
     const long items = (long)ntiles_max * m_tiles;
-    const long cap = 2L * (a.cus > 0 ? a.cus : 256);
-    const int grid = (int)((std::min(items, cap) + 7) / 8 * 8);
+    const long cap = (long)pf_resident_per_cu<NMAT, GSL>() * (a.cus > 0 ? a.cus : 256);
+    const int grid = (int)std::min((std::min(items, cap) + 7) / 8 * 8, std::max(cap / 8 * 8, 8L));
     hipLaunchKernelGGL((pf_mma_kernel<NMAT, GSL>), dim3((unsigned)grid), dim3(256), 0, st, a,
                        m_tiles);
 }

@@ -22,16 +22,23 @@ namespace {
 int32_t check_f32_vec(const void* p, const char* what) { return check_dev_ptr(p, what, false); }
 
 constexpr int kAttnCounters = 1024;  // >= num_heads (num_heads * 64 <= 65536); then the
-                                     // synchronous merge's launch number and finish count
+                                     // synchronous merge's launch number and, 32 words on,
+                                     // its finish counts (kCountWords)
+constexpr int kAttnCntWords = kAttnCounters + 32 + kCountWords;
+// the decoder's counters: 2 + num_heads + 1 words, then, 32-word aligned, the
+// attention's finish counts and lm_head's (kCountWords each)
+uint64_t dec_fin_offset(int num_heads) { return 32 * ((3 + (uint64_t)num_heads + 31) / 32); }
+uint64_t dec_lm_offset(int num_heads) { return dec_fin_offset(num_heads) + kCountWords; }
+uint64_t dec_cnt_words(int num_heads) { return dec_lm_offset(num_heads) + kCountWords; }
 
 int32_t ensure_attn_scratch(m1moe_ctx_t ctx, uint64_t floats) {
     ctx->capture_uses_scratch = true;
     if (!ctx->attn_cnt || floats > ctx->attn_part_floats)
         if (int32_t rc = refuse_growth_in_capture(ctx->stream, "the attention scratch")) return rc;
     if (!ctx->attn_cnt) {
-        int32_t rc = device_alloc((void**)&ctx->attn_cnt, (kAttnCounters + 2) * 4, "attention counters");
+        int32_t rc = device_alloc((void**)&ctx->attn_cnt, kAttnCntWords * 4, "attention counters");
         if (rc) return rc;
-        HIP_TRY(hipMemset(ctx->attn_cnt, 0, (kAttnCounters + 2) * 4));
+        HIP_TRY(hipMemset(ctx->attn_cnt, 0, kAttnCntWords * 4));
     }
     if (floats <= ctx->attn_part_floats) return M1MOE_OK;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -86,8 +93,9 @@ struct m1moe_dec {
     int32_t pf_cap = 0;
     float *pf_res = nullptr, *pf_res2 = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr;
     float* pf_part = nullptr;  // split-K partials of the prefill GEMMs (kGemmPartFloats)
-    uint32_t* cnt = nullptr;   // [4 + num_heads]: (unused), lm_head, attention groups,
-                               // the attention's launch number and finish count
+    uint32_t* cnt = nullptr;   // [dec_cnt_words]: (unused) x 2, attention groups, the
+                               // attention's launch number, then (dec_fin_offset) its
+                               // finish counts and (dec_lm_offset) lm_head's
     float* ssq = nullptr;      // o_proj's per-workgroup sums of squares
     float* rope = nullptr;     // [max_seq][head_dim / 2] (cos, sin) of every position
     float* am_val = nullptr;   // lm_head's per-workgroup best logit
@@ -217,7 +225,7 @@ int32_t m1moe_attention_decode(m1moe_ctx_t ctx, const float* d_q, const float* d
     a.kv_head = head_dim;
     a.scale = 1.0f / sqrtf((float)head_dim);
     a.gen = ctx->attn_cnt + kAttnCounters;
-    a.fin = ctx->attn_cnt + kAttnCounters + 1;
+    a.fin = ctx->attn_cnt + kAttnCounters + 32;
     a.spin_limit = kAttnSpinLimit;
     a.sync_merge = attention_grid_fits(a) ? 1 : 0;
     return launched(launch_attention(a, ctx->stream), "attention");
@@ -295,7 +303,7 @@ int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* s, m1moe_dec_t*
         (rc = dec_alloc(d, (void**)&d->attn, qd * 4, "attention output")) ||
         (rc = dec_alloc(d, (void**)&d->logits, V * 4, "logits")) ||
         (rc = dec_alloc(d, (void**)&d->part, part * 4, "attention scratch")) ||
-        (rc = dec_alloc(d, (void**)&d->cnt, (4 + (uint64_t)s->num_heads) * 4, "counters")) ||
+        (rc = dec_alloc(d, (void**)&d->cnt, dec_cnt_words(s->num_heads) * 4, "counters")) ||
         (rc = dec_alloc(d, (void**)&d->ssq, (uint64_t)matvec_workgroups(d->h) * 4, "o_proj sums")) ||
         (rc = dec_alloc(d, (void**)&d->rope, ms * hd * 4, "RoPE table")) ||
         (rc = dec_alloc(d, (void**)&d->am_val, (uint64_t)matvec_workgroups(s->vocab) * 4, "argmax scratch")) ||
@@ -304,7 +312,7 @@ int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* s, m1moe_dec_t*
         return rc;
     }
     if (hipMemset(d->pos, 0, 16) != hipSuccess ||
-        hipMemset(d->cnt, 0, (4 + (size_t)s->num_heads) * 4) != hipSuccess ||
+        hipMemset(d->cnt, 0, dec_cnt_words(s->num_heads) * 4) != hipSuccess ||
         launch_rope_table(d->rope, s->max_seq, s->head_dim, s->rope_theta, moe->stream) != 0 ||
         hipStreamSynchronize(moe->stream) != hipSuccess) {
         m1moe_dec_destroy(d);
@@ -407,7 +415,7 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
     at.rope_theta = dec->sh.rope_theta;
     at.eps = eps;
     at.gen = dec->cnt + 2 + dec->sh.num_heads;
-    at.fin = dec->cnt + 3 + dec->sh.num_heads;
+    at.fin = dec->cnt + dec_fin_offset(dec->sh.num_heads);
     at.spin_limit = kAttnSpinLimit;
     at.sync_merge = attention_grid_fits(at) ? 1 : 0;
     at.rope = dec->rope;
@@ -468,7 +476,7 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
     MvArgs f = mv_one(dec->lm_head, dec->res, nullptr, d_logits ? d_logits : dec->logits, V, h);
     f.norm_w = dec->final_norm;
     f.eps = eps;
-    f.counter = dec->cnt + 1;
+    f.counter = dec->cnt + dec_lm_offset(dec->sh.num_heads);
     f.am_val = dec->am_val;
     f.am_idx = dec->am_idx;
     f.tok_out = tok_out;
@@ -678,7 +686,7 @@ int32_t dec_prefill_piece(m1moe_dec_t dec, const int32_t* d_tokens, int32_t T,
                       d_logits ? d_logits : dec->logits, dec->sh.vocab, h);
     f.norm_w = dec->final_norm;
     f.eps = eps;
-    f.counter = dec->cnt + 1;
+    f.counter = dec->cnt + dec_lm_offset(dec->sh.num_heads);
     f.am_val = dec->am_val;
     f.am_idx = dec->am_idx;
     f.tok_out = d_token_out;

@@ -65,9 +65,9 @@ __device__ __forceinline__ int32_t ld_coh(const int32_t* p) {
     return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// True in the workgroup that finishes last of `total`.  Every thread's
-// coherent stores have completed before the barrier, so they are visible to
-// coherent loads once the counter shows the workgroup.
+// True in the workgroup that finishes last of `total` (counter: one word).
+// Every thread's coherent stores have completed before the barrier, so they
+// are visible to coherent loads once the counter shows the workgroup.
 __device__ __forceinline__ bool last_workgroup(uint32_t* counter, uint32_t total, int* s_flag) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -81,6 +81,35 @@ __device__ __forceinline__ bool last_workgroup(uint32_t* counter, uint32_t total
 }
 __device__ __forceinline__ void reset_counter(uint32_t* c) {
     __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Counts workgroup b of `total` out (one thread); true for the last one.
+// Above 64 workgroups in two levels: b counts on part b % 8 (words 32 x),
+// the last of each part on word 256 (kCountWords words in all), so that no
+// address takes more than total / 8 counts (one address taking every
+// workgroup's count serialises them: ~1 us at 264 workgroups).  Each counter
+// is put back to 0 by its last count.
+__device__ __forceinline__ bool count_out(uint32_t* c, uint32_t total, uint32_t b) {
+    const uint32_t np = total > 64u ? 8u : 1u, x = b % np, per = (total + np - 1u - x) / np;
+    if (__hip_atomic_fetch_add(c + 32 * x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+        per - 1u)
+        return false;
+    reset_counter(c + 32 * x);
+    if (np == 1u) return true;
+    if (__hip_atomic_fetch_add(c + 256, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != np - 1u)
+        return false;
+    reset_counter(c + 256);
+    return true;
+}
+
+// last_workgroup over a kCountWords counter (count_out), workgroup blockIdx.x
+// of a one-dimensional grid.
+__device__ __forceinline__ bool last_workgroup_wide(uint32_t* counter, uint32_t total, int* s_flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) *s_flag = count_out(counter, total, blockIdx.x) ? 1 : 0;
+    __syncthreads();
+    return *s_flag != 0;
 }
 
 // (value, index) pairs: the larger value wins, ties to the lower index; NaN
@@ -360,7 +389,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
             st_coh(a.am_val + blockIdx.x, bv);
             st_coh(a.am_idx + blockIdx.x, bi);
         }
-        if (!last_workgroup(a.counter, gridDim.x, &s_flag)) return;
+        if (!last_workgroup_wide(a.counter, gridDim.x, &s_flag)) return;
         bv = -INFINITY;
         bi = 0x7fffffff;
         const int nwg = (int)gridDim.x;
@@ -404,7 +433,6 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
                 *a.tok_out = best;
             }
             if (p < a.max_seq) *a.pos = p + 1;
-            reset_counter(a.counter);
         }
         return;
     }
@@ -899,15 +927,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         // count this workgroup out; the last one advances the launch number
         // (every workgroup read it before counting itself out)
         __syncthreads();
-        if (tid == 0) {
-            const uint32_t total = gridDim.x * gridDim.y;
-            const uint32_t old =
-                __hip_atomic_fetch_add(a.fin, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (old == total - 1) {
-                __hip_atomic_store(a.gen, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                reset_counter(a.fin);
-            }
-        }
+        if (tid == 0 && count_out(a.fin, gridDim.x * gridDim.y, blockIdx.y * gridDim.x + blockIdx.x))
+            __hip_atomic_store(a.gen, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
 

@@ -293,7 +293,7 @@ struct MvArgs {
     const uint16_t* norm_w;
     float eps;
     float* ssq_out;              // [workgroups]
-    uint32_t* counter;
+    uint32_t* counter;           // [kCountWords] (dense.hip count_out)
     float* am_val;               // [workgroups]
     int32_t* am_idx;             // [workgroups]
     int32_t* tok_out;            // single mode: *tok_out; sequence mode: tok_out[p + 1]
@@ -353,7 +353,7 @@ struct AttnArgs {
     int32_t sync_merge;
     const float* rope;           // fused: [max_seq][head_dim / 2] (cos, sin) table, or null
     uint32_t* gen;
-    uint32_t* fin;
+    uint32_t* fin;               // [kCountWords] (dense.hip count_out)
     int32_t cus;                 // compute units of the device
     int32_t spin_limit;
 };
@@ -440,6 +440,7 @@ bool attention_grid_fits(const AttnArgs& a);
 // The RoPE table of attn_kernel: [max_seq][head_dim / 2] (cos, sin) pairs.
 int launch_rope_table(float* table, int max_seq, int head_dim, float theta, void* stream);
 constexpr int32_t kAttnSpinLimit = 1 << 20;  // bounded waits of the synchronous merge (~1 s)
+constexpr int kCountWords = 32 * 9;   // a two-level completion counter (dense.hip count_out)
 // floats of the partials buffer (room for the u64 pairs of the synchronous merge)
 int attention_partial_floats(int num_heads, int head_dim, int max_positions);
 int launch_attention(const AttnArgs& a, void* stream);

@@ -311,13 +311,15 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
             for (int i = 0; i < RPW; ++i) dst[u][i] = *reinterpret_cast<const uint4*>(wr[i] + c);
         }
     };
+    // two groups in flight from the start (both before the input is staged),
+    // each refilled as soon as it is used
     load(0, cur);
+    if (ngroups > 1) load(1, nxt);
     if (STAGE) mv_stage(a, s_x, s_red);
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
-    for (int gi = 0; gi < ngroups; ++gi) {
-        if (gi + 1 < ngroups) load(gi + 1, nxt);
+    auto use = [&](int gi, const uint4 (&buf)[U][RPW]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int c = gi * 512 * U + 512 * u + 8 * lane;
@@ -334,13 +336,15 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
 #pragma unroll
             for (int i = 0; i < RPW; ++i)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[i] = fmaf(bf16x8_at(cur[u][i], k), xs[k], acc[i]);
+                for (int k = 0; k < 8; ++k) acc[i] = fmaf(bf16x8_at(buf[u][i], k), xs[k], acc[i]);
         }
+    };
+    for (int gi = 0; gi < ngroups; gi += 2) {
+        use(gi, cur);
+        if (gi + 2 < ngroups) load(gi + 2, cur);
         if (gi + 1 < ngroups) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int i = 0; i < RPW; ++i) cur[u][i] = nxt[u][i];
+            use(gi + 1, nxt);
+            if (gi + 3 < ngroups) load(gi + 3, nxt);
         }
     }
     float bv = -INFINITY, ssq = 0.f;

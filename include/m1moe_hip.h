@@ -240,10 +240,12 @@ int32_t m1moe_moe_decode_given_topk(m1moe_ctx_t ctx, int32_t layer,
 /* T tokens at once (prefill): routing per token as m1moe_router_topk, the
  * (token, slot) pairs grouped by expert, gate/up/down as MFMA f16 grouped
  * GEMMs with the 4-bit dequant fused, and a deterministic weighted combine.
- * Results equal T independent m1moe_moe_decode calls up to bf16 operand
- * rounding.  d_x [T x hidden], d_residual f32 [T x hidden] or NULL,
- * d_out f32 [T x hidden], d_topk_idx/d_topk_w [T x top_k] nullable.
- * T <= the context's prefill capacity (4096 tokens). */
+ * Results equal T independent m1moe_moe_decode calls up to f16 operand
+ * rounding (the SwiGLU products in blocks of 32 with a power of two each
+ * where they pass the f16 range; a non-finite one is clamped and reported
+ * by the next m1moe_sync).  d_x [T x hidden], d_residual f32 [T x hidden]
+ * or NULL, d_out f32 [T x hidden], d_topk_idx/d_topk_w [T x top_k]
+ * nullable.  T <= the context's prefill capacity (4096 tokens). */
 int32_t m1moe_moe_prefill(m1moe_ctx_t ctx, int32_t layer, int32_t T,
                           const void* d_x, int32_t x_dtype,
                           const float* d_residual, float* d_out,

@@ -625,20 +625,29 @@ __device__ void attn_merge_share(const AttnArgs& a, int g, int c, int nch, int n
 
 
 // Workgroup (g, c): q heads g*QH .. g*QH+QH-1 (one kv head), positions
-// c*a.chunk .. (c+1)*a.chunk - 1, walked 64 at a time with a running max
+// c*a.chunk .. (c+1)*a.chunk - 1, walked SCH at a time with a running max
 // and sum (the softmax of attnSoftmax, Shaders.metal:245-289, in pieces).
 // Lanes take 8 dims of one position each (HD/8 lanes per position), so every
-// K or V row is one coalesced read shared by the QH heads.
-template <int HD, int QH, bool TWO>
+// K or V row is one coalesced read shared by the QH heads.  V: 0 one set of
+// K/V registers, 64-position sub-chunks; 1 two sets (chunks of several
+// sub-chunks); 2 one wide sub-chunk of up to attn_wide_sub<HD>() positions
+// (chunks of 65..kAttnWideChunk positions, so that the grid fits the CUs).
+template <int HD>
+__host__ __device__ constexpr int attn_wide_sub() { return HD == 64 ? 96 : 80; }
+
+template <int HD, int QH, int V>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+    constexpr bool TWO = V == 1;
+    constexpr int SCH = V == 2 ? attn_wide_sub<HD>() : kAttnChunk;   // positions per sub-chunk
     constexpr int LP = HD / 8;                 // lanes per position
     constexpr int PPI = 64 / LP;               // positions per wave and iteration
-    constexpr int PW = kAttnChunk / 4;         // positions per wave per sub-chunk
+    constexpr int PW = SCH / 4;                // positions per wave per sub-chunk
     constexpr int IT = PW / PPI;               // iterations
+    static_assert(PW % PPI == 0 && SCH <= 128, "whole iterations, at most two positions per softmax lane");
     constexpr int HALF = HD / 2;
     __shared__ __attribute__((aligned(16))) float s_q[QH][HD];
     __shared__ __attribute__((aligned(16))) float s_kv[2][HD];
-    __shared__ float s_p[QH][kAttnChunk];
+    __shared__ float s_p[QH][SCH];
     __shared__ __attribute__((aligned(16))) float s_acc[4][QH][HD];
     __shared__ float s_m[QH], s_l[QH], s_f[QH];
     __shared__ float s_st[2][QH][kAttnMaxChunks];  // merge: chunk max and sum
@@ -717,7 +726,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         // for one sub-chunk only)
         constexpr bool kTwo = TWO && HD <= 128;
         load_rows(c0, A);
-        if (kTwo && c0 + kAttnChunk < c1) load_rows(c0 + kAttnChunk, B);
+        if (kTwo && c0 + SCH < c1) load_rows(c0 + SCH, B);
         // keep both sub-chunks' loads here (the compiler may otherwise sink
         // the second to its first use, a memory round trip later)
         asm volatile("" ::: "memory");
@@ -801,7 +810,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
 
         auto sub = [&](int p0, KVRows& R) {
-            if (mine_new && p >= p0 && p < p0 + kAttnChunk) {
+            if (mine_new && p >= p0 && p < p0 + SCH) {
 #pragma unroll
                 for (int it = 0; it < IT; ++it) {
                     if (p0 + wave * PW + it * PPI + pg != p) continue;
@@ -827,14 +836,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
             __syncthreads();
             // running max and sum per head; lane = position of the sub-chunk
+            // (and lane + 64 in a wide one)
             for (int i = wave; i < QH; i += 4) {
+                constexpr bool W2 = SCH > 64;
                 const float sc = s_p[i][lane];
+                const float sc2 = (W2 && lane + 64 < SCH) ? s_p[i][W2 ? lane + 64 : lane] : -INFINITY;
                 const float m_old = s_m[i];
-                const float m = fmaxf(m_old, wave_max(sc));
+                const float m = fmaxf(m_old, wave_max(fmaxf(sc, sc2)));
                 const float e = sc == -INFINITY ? 0.f : expf(sc - m);
+                const float e2 = sc2 == -INFINITY ? 0.f : expf(sc2 - m);
                 const float f = m_old == -INFINITY ? 0.f : expf(m_old - m);
-                const float l = wave_sum(e);
+                const float l = wave_sum(W2 ? e + e2 : e);
                 s_p[i][lane] = e;
+                if (W2 && lane + 64 < SCH) s_p[i][W2 ? lane + 64 : lane] = e2;
                 if (lane == 0) {
                     s_m[i] = m;
                     s_l[i] = fmaf(s_l[i], f, l);
@@ -859,20 +873,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     for (int e = 0; e < 8; ++e) acc[i][e] = fmaf(w, R.v[it][e], acc[i][e]);
                 }
             }
-            if (p0 + kAttnChunk < c1) __syncthreads();  // s_p is rewritten by the next sub-chunk
+            if (p0 + SCH < c1) __syncthreads();  // s_p is rewritten by the next sub-chunk
         };
         if (!kTwo) {
-            for (int p0 = c0; p0 < c1; p0 += kAttnChunk) {
+            for (int p0 = c0; p0 < c1; p0 += SCH) {
                 sub(p0, A);
-                if (p0 + kAttnChunk < c1) load_rows(p0 + kAttnChunk, A);
+                if (p0 + SCH < c1) load_rows(p0 + SCH, A);
             }
         }
-        for (int p0 = c0; kTwo && p0 < c1; p0 += 2 * kAttnChunk) {
+        for (int p0 = c0; kTwo && p0 < c1; p0 += 2 * SCH) {
             sub(p0, A);
-            if (p0 + 2 * kAttnChunk < c1) load_rows(p0 + 2 * kAttnChunk, A);
-            if (p0 + kAttnChunk < c1) {
-                sub(p0 + kAttnChunk, B);
-                if (p0 + 3 * kAttnChunk < c1) load_rows(p0 + 3 * kAttnChunk, B);
+            if (p0 + 2 * SCH < c1) load_rows(p0 + 2 * SCH, A);
+            if (p0 + SCH < c1) {
+                sub(p0 + SCH, B);
+                if (p0 + 3 * SCH < c1) load_rows(p0 + 3 * SCH, B);
             }
         }
 #pragma unroll
@@ -1084,23 +1098,32 @@ int launch_mv(const MvArgs& a, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
+// The kernel's variant for a chunk of `chunk` positions (attn_kernel's V).
+int attn_variant(int chunk) {
+    return chunk <= kAttnChunk ? 0 : (chunk <= kAttnWideChunk ? 2 : 1);
+}
+
+template <int HD, int V>
+int launch_attn_v(const AttnArgs& a, dim3 grid, hipStream_t st) {
+    switch (a.qh) {
+        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1, V>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2, V>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4, V>), grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8, V>), grid, dim3(256), 0, st, a); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
 template <int HD>
 int launch_attn_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
     // one-sub-chunk workgroups keep no second set of K/V registers, so two of
     // them fit on a CU (more than 256 workgroups then run at once)
-    const bool two = a.chunk > kAttnChunk;
-    switch (a.qh * 2 + (two ? 1 : 0)) {
-        case 2: hipLaunchKernelGGL((attn_kernel<HD, 1, false>), grid, dim3(256), 0, st, a); break;
-        case 3: hipLaunchKernelGGL((attn_kernel<HD, 1, true>), grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((attn_kernel<HD, 2, false>), grid, dim3(256), 0, st, a); break;
-        case 5: hipLaunchKernelGGL((attn_kernel<HD, 2, true>), grid, dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((attn_kernel<HD, 4, false>), grid, dim3(256), 0, st, a); break;
-        case 9: hipLaunchKernelGGL((attn_kernel<HD, 4, true>), grid, dim3(256), 0, st, a); break;
-        case 16: hipLaunchKernelGGL((attn_kernel<HD, 8, false>), grid, dim3(256), 0, st, a); break;
-        case 17: hipLaunchKernelGGL((attn_kernel<HD, 8, true>), grid, dim3(256), 0, st, a); break;
-        default: return (int)hipErrorInvalidValue;
+    switch (attn_variant(a.chunk)) {
+        case 0: return launch_attn_v<HD, 0>(a, grid, st);
+        case 2: return launch_attn_v<HD, 2>(a, grid, st);
+        default: return launch_attn_v<HD, 1>(a, grid, st);
     }
-    return (int)hipGetLastError();
 }
 
 }  // namespace
@@ -1146,16 +1169,23 @@ int attention_chunk_min(int max_positions) {
     return kAttnChunk * ((sub + kAttnMaxChunks - 1) / kAttnMaxChunks);
 }
 
-// When that grid is two or more workgroups per CU, one workgroup per CU
-// taking more sub-chunks instead: measured (32 q / 8 kv heads of 128, 256
-// CUs) 19.8 -> 16.1 us at 4096 positions, 34.5 -> 25.7 us at 8192; below two
-// rounds (2112 positions: 264 workgroups) the 64-position chunks stay
-// (13.5 us, against 14.4 us for 256 workgroups of 66).
+// When that grid has more workgroups than the device has CUs: if chunks
+// of at most kAttnWideChunk positions fit the groups on the CUs, those (one
+// wide sub-chunk each: 2113 positions x 8 groups on 256 CUs, 67-position
+// chunks, 12.4 -> ~9.8 us); else, from two workgroups per CU on, one
+// workgroup per CU taking more 64-position sub-chunks (32 q / 8 kv heads of
+// 128, 256 CUs: 19.8 -> 16.1 us at 4096 positions, 34.5 -> 25.7 us at 8192).
+// Between the two (one round and a bit, wide chunks too short) the 64-position
+// chunks stay: 256 workgroups of 66 positions in two sub-chunks measured 14.4
+// against 13.5 us for 264 of 64.
 int attention_chunk(int max_positions, int groups, int cus) {
     const int c = attention_chunk_min(max_positions);
     const long wgs = (long)groups * ((max_positions + c - 1) / c);
     const int per = std::min(kAttnMaxChunks, groups > 0 ? cus / groups : 0);   // chunks per group
-    if (per < 1 || wgs < 2L * cus) return c;
+    if (per < 1 || wgs <= cus) return c;
+    const int wide = (max_positions + per - 1) / per;
+    if (c == kAttnChunk && wide <= kAttnWideChunk) return wide;
+    if (wgs < 2L * cus) return c;
     const int sub = (max_positions + kAttnChunk - 1) / kAttnChunk;
     return std::max(c, kAttnChunk * ((sub + per - 1) / per));
 }
@@ -1167,46 +1197,46 @@ int attention_partial_floats(int num_heads, int head_dim, int max_positions) {
 }
 
 namespace {
-template <int HD>
-int attn_occupancy_hd(int qh, bool two) {
+template <int HD, int V>
+int attn_occupancy_v(int qh) {
     int n = 0;
     hipError_t e = hipErrorInvalidValue;
-    switch (qh * 2 + (two ? 1 : 0)) {
-        case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 1, false>, 256, 0); break;
-        case 3: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 1, true>, 256, 0); break;
-        case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 2, false>, 256, 0); break;
-        case 5: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 2, true>, 256, 0); break;
-        case 8: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 4, false>, 256, 0); break;
-        case 9: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 4, true>, 256, 0); break;
-        case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 8, false>, 256, 0); break;
-        case 17: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 8, true>, 256, 0); break;
+    switch (qh) {
+        case 1: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 1, V>, 256, 0); break;
+        case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 2, V>, 256, 0); break;
+        case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 4, V>, 256, 0); break;
+        case 8: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, 8, V>, 256, 0); break;
         default: break;
     }
     return e == hipSuccess ? n : 0;
 }
+template <int HD>
+int attn_occupancy_hd(int qh, int v) {
+    return v == 0 ? attn_occupancy_v<HD, 0>(qh) : (v == 2 ? attn_occupancy_v<HD, 2>(qh) : attn_occupancy_v<HD, 1>(qh));
+}
 
-// Workgroups of the attention kernel of (head_dim, qh, two sub-chunk sets)
-// one CU holds, from the occupancy query, kept after the first ask.
-std::atomic<int> g_attn_occ[3][9][2];
+// Workgroups of the attention kernel of (head_dim, qh, variant) one CU
+// holds, from the occupancy query, kept after the first ask.
+std::atomic<int> g_attn_occ[3][9][3];
 
-int attn_blocks_per_cu(int hd, int qh, bool two) {
+int attn_blocks_per_cu(int hd, int qh, int v) {
     const int hi = hd == 64 ? 0 : hd == 128 ? 1 : 2;
-    std::atomic<int>& slot = g_attn_occ[hi][qh][two ? 1 : 0];
-    int v = slot.load(std::memory_order_relaxed);
-    if (v == 0) {
-        v = hd == 64 ? attn_occupancy_hd<64>(qh, two)
-                     : hd == 128 ? attn_occupancy_hd<128>(qh, two) : attn_occupancy_hd<256>(qh, two);
-        v = v > 0 ? v : -1;
-        slot.store(v, std::memory_order_relaxed);
+    std::atomic<int>& slot = g_attn_occ[hi][qh][v];
+    int n = slot.load(std::memory_order_relaxed);
+    if (n == 0) {
+        n = hd == 64 ? attn_occupancy_hd<64>(qh, v)
+                     : hd == 128 ? attn_occupancy_hd<128>(qh, v) : attn_occupancy_hd<256>(qh, v);
+        n = n > 0 ? n : -1;
+        slot.store(n, std::memory_order_relaxed);
     }
-    return v > 0 ? v : 0;
+    return n > 0 ? n : 0;
 }
 }  // namespace
 
 bool attention_grid_fits(const AttnArgs& a) {
     if (a.qh <= 0 || a.qh > 8 || a.cus <= 0) return false;
     const int64_t grid = (int64_t)(a.num_heads / a.qh) * ((a.max_seq + a.chunk - 1) / a.chunk);
-    return (int64_t)attn_blocks_per_cu(a.head_dim, a.qh, a.chunk > kAttnChunk) * a.cus >= grid;
+    return (int64_t)attn_blocks_per_cu(a.head_dim, a.qh, attn_variant(a.chunk)) * a.cus >= grid;
 }
 
 int launch_attention(const AttnArgs& a, void* stream) {

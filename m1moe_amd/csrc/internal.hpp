@@ -310,8 +310,8 @@ struct MvArgs {
 
 // Decode attention of one query position.  Workgroup (g, c): q heads
 // g*qh .. g*qh+qh-1 (one kv head) over positions c*chunk .. (c+1)*chunk - 1
-// (chunk = attention_chunk(max_seq, groups, cus): a multiple of 64, at most
-// kAttnMaxChunks workgroups per kv head).
+// (chunk = attention_chunk(max_seq, groups, cus): a multiple of 64 or 65 ..
+// kAttnWideChunk, at most kAttnMaxChunks workgroups per kv head).
 //   fused = 1: q, k_new, v_new are the raw projections of the current token;
 //     q and k get the per-head RMSNorm (q_norm/k_norm non-null) and RoPE at
 //     p = *pos, the new k/v row is stored at cache row p (flag 32 and no
@@ -358,7 +358,8 @@ struct AttnArgs {
     int32_t spin_limit;
 };
 
-constexpr int kAttnChunk = 64;   // positions per attention workgroup
+constexpr int kAttnChunk = 64;   // positions per attention sub-chunk
+constexpr int kAttnWideChunk = 80;   // chunks of 65 .. this many positions: one wide sub-chunk
 constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
 constexpr int kAttnMaxChunks = 64;   // workgroups per kv head
 constexpr int kAttnDeferChunks = 8;        // deferred merge: at most this many chunks
@@ -431,7 +432,7 @@ int launch_matvec_bf16(const MvArgs& a, void* stream);
 int attention_qh(int hpkv);
 // Positions per attention workgroup for a cache of max_positions, groups
 // (num_heads / qh) workgroups per chunk and cus compute units: a multiple of
-// 64, at most kAttnMaxChunks chunks.
+// 64, or 65 .. kAttnWideChunk; at most kAttnMaxChunks chunks.
 int attention_chunk(int max_positions, int groups, int cus);
 // The whole attention grid of `a` fits on the device at once (a.cus CUs, the
 // occupancy of the kernel instance it launches): the synchronous merge may

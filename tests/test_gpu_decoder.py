@@ -81,12 +81,18 @@ def test_matvec_bf16(ops_ctx, rows, cols, with_res):
                                            (4, 2, 64, 257), (32, 8, 128, 1000), (2, 1, 256, 700),
                                            (16, 16, 128, 4096), (32, 8, 128, 2112),
                                            (32, 4, 128, 2112), (16, 2, 64, 4096),
-                                           (8, 2, 128, 5000), (4, 4, 64, 8300)])
+                                           (8, 2, 128, 5000), (4, 4, 64, 8300),
+                                           # one wide sub-chunk per workgroup (65..80
+                                           # positions: the grid fits the CUs)
+                                           (32, 8, 64, 2100), (32, 8, 256, 2100),
+                                           (64, 64, 128, 300)])
 def test_attention_decode(ops_ctx, nh, nkv, hd, sl):
     """The attention building block against the oracle: one chunk, 64-position
-    chunks up to 64 per kv head (4096, and the Mixtral grouping at 2112),
-    multi-sub-chunk chunks past 4096 positions (two K/V register sets),
-    head_dim 64 / 128 / 256."""
+    chunks up to 64 per kv head, chunks of several 64-position sub-chunks
+    (two K/V register sets), chunks of one wide sub-chunk (65..80
+    positions, when 64-position chunks would put more workgroups than CUs:
+    the Mixtral grouping at 2100-2112 positions, 64 single-head groups at
+    300), head_dim 64 / 128 / 256."""
     ctx, ops = ops_ctx
     kvd = nkv * hd
     q = RNG.normal(0, 1, nh * hd).astype(np.float32)

@@ -48,6 +48,9 @@ int32_t ensure_attn_scratch(m1moe_ctx_t ctx, uint64_t floats) {
     ctx->attn_part_floats = 0;
     int32_t rc = device_alloc((void**)&ctx->attn_part, floats * 4, "attention scratch");
     if (rc) return rc;
+    // (zeroed: the synchronous merge accepts a value carrying the current
+    // launch number, and reused device memory may hold one)
+    HIP_TRY(hipMemset(ctx->attn_part, 0, floats * 4));
     ctx->attn_part_floats = floats;
     return M1MOE_OK;
 }
@@ -311,8 +314,11 @@ int32_t m1moe_dec_create(m1moe_ctx_t moe, const m1moe_dec_shape* s, m1moe_dec_t*
         m1moe_dec_destroy(d);
         return rc;
     }
+    // (the partials are zeroed: the synchronous merge accepts a value by its
+    // launch number, which starts at 1, and reused device memory may hold any)
     if (hipMemset(d->pos, 0, 16) != hipSuccess ||
         hipMemset(d->cnt, 0, dec_cnt_words(s->num_heads) * 4) != hipSuccess ||
+        hipMemset(d->part, 0, part * 4) != hipSuccess ||
         launch_rope_table(d->rope, s->max_seq, s->head_dim, s->rope_theta, moe->stream) != 0 ||
         hipStreamSynchronize(moe->stream) != hipSuccess) {
         m1moe_dec_destroy(d);

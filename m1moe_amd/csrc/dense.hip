@@ -284,11 +284,54 @@ __device__ void mv_stage(const MvArgs& a, float* s_x, float* s_red) {
     __syncthreads();
 }
 
+// mv_stage for an input x of at most 1024 XF floats whose loads (x and the
+// norm weights: XF float4 / uint2 per thread) were issued before the weight
+// rows': the same arithmetic in the same order as mv_stage.
+template <int XF>
+__device__ void mv_stage_early(const MvArgs& a, float* s_x, float* s_red, const float4 (&xv)[XF],
+                               const uint2 (&nw)[XF]) {
+    const int n4 = a.cols >> 2;
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < XF; ++k) {
+        const float4 v = xv[k];
+        if (threadIdx.x + 256 * k < n4) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    if (a.x_copy && blockIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < XF; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < n4) reinterpret_cast<float4*>(a.x_copy)[i] = xv[k];
+        }
+    }
+    float rms = 1.f;
+    if (a.norm_w) rms = rsqrtf(block_sum(ss, s_red, 4) / (float)a.cols + a.eps);
+#pragma unroll
+    for (int k = 0; k < XF; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= n4) continue;
+        float4 v = xv[k];
+        if (a.norm_w) {
+            const uint2 b = nw[k];
+            v.x = v.x * rms * bf16_to_f32(b.x & 0xFFFFu);
+            v.y = v.y * rms * bf16_to_f32(b.x >> 16);
+            v.z = v.z * rms * bf16_to_f32(b.y & 0xFFFFu);
+            v.w = v.w * rms * bf16_to_f32(b.y >> 16);
+        }
+        reinterpret_cast<float4*>(s_x)[i] = v;
+    }
+    __syncthreads();
+}
+
 // Workgroup = 4 waves x RPW rows.  Lane l takes columns 8l .. 8l+7 of each
 // 512-column block; U blocks of every row are loaded per group, the next
 // group's loads issued before the current one is used.  The first group is
-// in flight while the input is staged.
-template <int RPW, bool STAGE>
+// in flight while the input is staged.  XF > 0 (inputs of at most 1024 XF
+// floats): the input x, its norm weights and the rows' residuals are
+// requested before the weight rows, so that the input is staged as soon as
+// they land (the loads complete in order) while the weights stream, and the
+// residual is no round trip at the end.
+template <int RPW, bool STAGE, int XF>
 __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     constexpr int U = 8 / RPW;
     extern __shared__ __attribute__((aligned(16))) float s_x[];
@@ -298,6 +341,31 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     __shared__ int s_flag;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r0 = (blockIdx.x * 4 + wave) * RPW;
+    // (XF: the embedded input of layer 0 waits for its token and takes the
+    // staging below; x is requested anyway when the staging turns out to be
+    // the deferred attention merge, whose output buffer it is)
+    constexpr int XN = XF > 0 ? XF : 1;
+    const bool early = STAGE && XF > 0 && !a.embed;
+    float4 xv[XN];
+    uint2 nwv[XN];
+    if (early) {
+#pragma unroll
+        for (int k = 0; k < XN; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            xv[k] = i < (a.cols >> 2) ? reinterpret_cast<const float4*>(a.x)[i] : float4{0.f, 0.f, 0.f, 0.f};
+            nwv[k] = (a.norm_w && i < (a.cols >> 2)) ? reinterpret_cast<const uint2*>(a.norm_w)[i]
+                                                     : uint2{0u, 0u};
+        }
+    }
+    float resv[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        resv[i] = 0.f;
+        if (r0 + i < a.rows) {
+            const RowRef rr = mv_row(a, r0 + i);
+            if (rr.res) resv[i] = *rr.res;
+        }
+    }
     const uint16_t* wr[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) wr[i] = mv_row(a, min(r0 + i, a.rows - 1)).w;
@@ -315,7 +383,13 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     // each refilled as soon as it is used
     load(0, cur);
     if (ngroups > 1) load(1, nxt);
-    if (STAGE) mv_stage(a, s_x, s_red);
+    if (STAGE) {
+        if (early && !(a.attn_part &&
+                       attn_defer_nact(*a.pos, a.max_seq, a.attn_chunk, a.attn_heads) > 0))
+            mv_stage_early<XN>(a, s_x, s_red, xv, nwv);
+        else
+            mv_stage(a, s_x, s_red);
+    }
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
@@ -355,7 +429,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
         const int row = r0 + i;
         if (row < a.rows) {
             const RowRef rr = mv_row(a, row);
-            const float y = rr.res ? *rr.res + v : v;
+            const float y = rr.res ? resv[i] + v : v;
             if (lane == 0) {
                 if (a.counter)
                     st_coh(rr.y, y);  // the last workgroup reads it
@@ -1091,10 +1165,15 @@ int mv_rpw(int rows) { return rows >= 32768 ? 8 : rows >= 8192 ? 4 : rows >= 204
 template <int RPW>
 int launch_mv(const MvArgs& a, hipStream_t st) {
     const unsigned grid = (unsigned)((a.rows + 4 * RPW - 1) / (4 * RPW));
-    if (a.cols <= kMvStageMax)
-        hipLaunchKernelGGL((matvec_kernel<RPW, true>), dim3(grid), dim3(256), (size_t)a.cols * 4, st, a);
+    const size_t lds = (size_t)a.cols * 4;
+    if (a.cols <= 2048)
+        hipLaunchKernelGGL((matvec_kernel<RPW, true, 2>), dim3(grid), dim3(256), lds, st, a);
+    else if (a.cols <= 4096)
+        hipLaunchKernelGGL((matvec_kernel<RPW, true, 4>), dim3(grid), dim3(256), lds, st, a);
+    else if (a.cols <= kMvStageMax)
+        hipLaunchKernelGGL((matvec_kernel<RPW, true, 0>), dim3(grid), dim3(256), lds, st, a);
     else
-        hipLaunchKernelGGL((matvec_kernel<RPW, false>), dim3(grid), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((matvec_kernel<RPW, false, 0>), dim3(grid), dim3(256), 0, st, a);
     return (int)hipGetLastError();
 }
 

@@ -37,15 +37,16 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 def test_swift_binding_names_only_declared_symbols():
-    """The uncompiled SwiftPM binding (no Swift toolchain here) calls only
-    functions and constants the header declares, and links the library's
-    own name."""
+    """The uncompiled SwiftPM binding and the Swift check executable (no
+    Swift toolchain here) call only functions and constants the header
+    declares, and the binding links the library's own name."""
     sw = os.path.join(ROOT, "Sources")
     mm = open(os.path.join(sw, "CM1MoEHIP", "module.modulemap")).read()
     assert 'link "m1moe_hip"' in mm and 'header "shim.h"' in mm
     assert os.path.basename(_lib.LIB_PATH) == "libm1moe_hip.so"
     assert "#include <m1moe_hip.h>" in open(os.path.join(sw, "CM1MoEHIP", "shim.h")).read()
-    swift = re.sub(r"//[^\n]*", "", open(os.path.join(sw, "M1MoE", "HIPMoE.swift")).read())
+    swift = "".join(re.sub(r"//[^\n]*", "", open(os.path.join(sw, *f)).read())
+                    for f in (("M1MoE", "HIPMoE.swift"), ("hipcheck", "main.swift")))
     header = open(HEADER).read()
     calls = set(re.findall(r"\b(m1moe_[a-z0-9_]+)\s*\(", swift))
     calls -= {"m1moe_moe_shape", "m1moe_dec_shape"}     # struct initialisers, checked below

@@ -272,6 +272,24 @@ def main() -> int:
     gbs = bytes_tok / (layer_us * 1e-6) / 1e9
     log(f"{ms_per_step:.4f} ms/step, {layer_us:.3f} us/layer-token, {gbs:.0f} GB/s")
 
+    # BASELINE.md's protocol beside the timed region above (which `value`
+    # comes from): the median of 20 repeats of a few steps each
+    rep_steps = max(1, min(10, args.steps))
+    rep_us = []
+    for _ in range(20):
+        ev0.record()
+        for i in range(rep_steps):
+            graphs[i % G].launch()
+        ev1.record()
+        ctx.sync()
+        rep_us.append(ev0.elapsed_ms(ev1) * 1e3 / (rep_steps * R))
+    rep_us.sort()
+    repeats = {"n": 20, "steps_each": rep_steps,
+               "median_us_per_layer_token": round(float(np.median(rep_us)), 4),
+               "min_us": round(rep_us[0], 4), "max_us": round(rep_us[-1], 4)}
+    log(f"20 repeats of {rep_steps} steps: median {repeats['median_us_per_layer_token']:.3f} "
+        f"us/layer-token (min {rep_us[0]:.3f}, max {rep_us[-1]:.3f})")
+
     cpu = cpu_all = None
     if args.cpu_seconds > 0:
         cpu, cpu_all = cpu_decode_baselines(args, synth, orc, oshape, img0, router0, xs, res)
@@ -310,6 +328,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,
         "parity": {"topk_exact": idx_ok, "rel_l2": rel},
+        "repeats": repeats,
     }
     print(json.dumps(line), flush=True)
     ctx.close()

@@ -380,9 +380,16 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
         }
     };
     // two groups in flight from the start (both before the input is staged),
-    // each refilled as soon as it is used
+    // each refilled as soon as it is used.  (RPW 8, the tall matrices: the
+    // second is requested even where there is none, at the row's clamped
+    // last columns, and the loop below has unconditional refills, so that
+    // every path to a group's use has the same loads in flight in the same
+    // order and the wait before it does not take the newer group too:
+    // 50304 x 2048 45.9 -> 44.0 us.  The shorter matrices, one or two groups
+    // per row, measured slower in that form.)
+    constexpr bool kExactWaits = RPW == 8;
     load(0, cur);
-    if (ngroups > 1) load(1, nxt);
+    if (kExactWaits || ngroups > 1) load(1, nxt);
     if (STAGE) {
         if (early && !(a.attn_part &&
                        attn_defer_nact(*a.pos, a.max_seq, a.attn_chunk, a.attn_heads) > 0))
@@ -393,32 +400,59 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
+    // (kExactWaits: a block past the end is skipped for the whole wave, and
+    // in the last, partial one the lanes past the end keep their sums by a
+    // select, not a branch)
     auto use = [&](int gi, const uint4 (&buf)[U][RPW]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int c = gi * 512 * U + 512 * u + 8 * lane;
-            if (c >= a.cols) continue;
+            const int c0 = gi * 512 * U + 512 * u, c = c0 + 8 * lane;
+            if (kExactWaits ? c0 >= a.cols : c >= a.cols) continue;
+            const bool in = c < a.cols;
+            const int cx = kExactWaits && !in ? a.cols - 8 : c;
             float4 x0, x1;
             if (STAGE) {
-                x0 = *reinterpret_cast<const float4*>(s_x + c);
-                x1 = *reinterpret_cast<const float4*>(s_x + c + 4);
+                x0 = *reinterpret_cast<const float4*>(s_x + cx);
+                x1 = *reinterpret_cast<const float4*>(s_x + cx + 4);
             } else {
-                x0 = *reinterpret_cast<const float4*>(a.x + c);
-                x1 = *reinterpret_cast<const float4*>(a.x + c + 4);
+                x0 = *reinterpret_cast<const float4*>(a.x + cx);
+                x1 = *reinterpret_cast<const float4*>(a.x + cx + 4);
             }
             const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int i = 0; i < RPW; ++i)
+            for (int i = 0; i < RPW; ++i) {
+                float t = acc[i];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[i] = fmaf(bf16x8_at(buf[u][i], k), xs[k], acc[i]);
+                for (int k = 0; k < 8; ++k) t = fmaf(bf16x8_at(buf[u][i], k), xs[k], t);
+                acc[i] = kExactWaits && !in ? acc[i] : t;
+            }
         }
     };
-    for (int gi = 0; gi < ngroups; gi += 2) {
-        use(gi, cur);
-        if (gi + 2 < ngroups) load(gi + 2, cur);
-        if (gi + 1 < ngroups) {
+    if constexpr (kExactWaits) {
+        int gi = 0;
+        for (; gi + 3 < ngroups; gi += 2) {
+            use(gi, cur);
+            load(gi + 2, cur);
             use(gi + 1, nxt);
-            if (gi + 3 < ngroups) load(gi + 3, nxt);
+            load(gi + 3, nxt);
+        }
+        if (gi + 2 < ngroups) {
+            use(gi, cur);
+            load(gi + 2, cur);
+            use(gi + 1, nxt);
+            use(gi + 2, cur);
+        } else {
+            use(gi, cur);
+            if (gi + 1 < ngroups) use(gi + 1, nxt);
+        }
+    } else {
+        for (int gi = 0; gi < ngroups; gi += 2) {
+            use(gi, cur);
+            if (gi + 2 < ngroups) load(gi + 2, cur);
+            if (gi + 1 < ngroups) {
+                use(gi + 1, nxt);
+                if (gi + 3 < ngroups) load(gi + 3, nxt);
+            }
         }
     }
     float bv = -INFINITY, ssq = 0.f;

@@ -61,7 +61,9 @@ def test_rmsnorm(ops_ctx, n):
 
 @pytest.mark.parametrize("rows,cols,with_res", [(1, 8, False), (37, 200, True), (2048, 2048, True),
                                                 (6144, 2048, False), (2048, 4096, True),
-                                                (50304, 2048, False), (3, 65536, False)])
+                                                (50304, 2048, False), (33000, 2560, True),
+                                                (40001, 4096, True), (40001, 4096, False),
+                                                (131075, 1024, False), (3, 65536, False)])
 def test_matvec_bf16(ops_ctx, rows, cols, with_res):
     ctx, ops = ops_ctx
     w = bf16(RNG.normal(0, 1 / np.sqrt(cols), (rows, cols)))

@@ -129,6 +129,7 @@ m1moe::FusedArgs fused_args(m1moe_ctx_t ctx, int32_t layer, const void* x, int32
     a.layer_base = ctx->arena + (uint64_t)layer * g.E * g.expert_bytes;
     a.expert_bytes = g.expert_bytes;
     a.router = ctx->routers + (uint64_t)layer * g.E * g.h;
+    a.next_router = ctx->routers + (uint64_t)((layer + 1) % ctx->shape.num_layers) * g.E * g.h;
     a.bias = ctx->has_bias[layer] ? ctx->biases + (uint64_t)layer * g.E : nullptr;
     a.x = x;
     a.residual = residual;

@@ -834,6 +834,20 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
         st_u32(a.cu_part + ((size_t)((t + (kH / 4) * r) >> 3) * kNG + g) * kRows + (t & 7),
                tagged(pr[r], parity));
     DTR_WG(17);
+    // the next layer's router rows that this workgroup's successor (the same
+    // index, so the same XCD) reads first, requested now so that they wait in
+    // the XCD's L2 (consumed by an empty asm at the end: the loads complete
+    // while the partials are awaited)
+    uint32_t pf = 0u;
+    if (a.next_router) {
+#pragma unroll
+        for (int i = 0; i < kMaxLoc; ++i)
+            if (i < nloc) {
+                const uint2 v =
+                    *reinterpret_cast<const uint2*>(a.next_router + (size_t)(jl + 32 * i) * kH + 4 * t);
+                pf ^= v.x ^ v.y;
+            }
+    }
 
     // the combine weights, off the path to the partial stores (read after the
     // barrier that follows the reduction)
@@ -897,6 +911,7 @@ __global__ __launch_bounds__(kT, 1) void moe_decode_cu_kernel(FusedArgs a) {
     }
     DTR_WG(56);
     if (t == 0) st_u32(a.cu_seen + g, tag);
+    asm volatile("" ::"v"(pf));
     DTR_END();
 }
 

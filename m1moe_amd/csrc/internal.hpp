@@ -44,6 +44,8 @@ struct FusedArgs {
     const uint8_t* layer_base;   // first expert block of the layer
     uint64_t expert_bytes;
     const uint16_t* router;      // [E][h] bf16
+    const uint16_t* next_router; // the next layer's router (read into the XCD's L2 near the
+                                 // end of the launch, for the next layer's launch), or null
     const float* bias;           // [E] or null
     const void* x;               // [h] f32 or bf16
     const float* residual;       // [h] or null

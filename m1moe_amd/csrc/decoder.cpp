@@ -457,6 +457,12 @@ int32_t dec_step(m1moe_dec_t dec, const int32_t* tok_in, int32_t* tok_out, int32
         at.k_norm = qk ? dec->k_norm + (size_t)l * hd : nullptr;
         at.kcache = dec->kcache + l * cache_layer;
         at.vcache = dec->vcache + l * cache_layer;
+        // o_proj's weights into the caches while the attention runs (piece b:
+        // the rows of o_proj's workgroup b)
+        at.pf = reinterpret_cast<const uint8_t*>(dec->wo + (size_t)l * h * qd);
+        at.pf_unit = (int64_t)matvec_rows_per_workgroup(h) * qd * 2;
+        at.pf_bytes = (int64_t)h * qd * 2;
+        at.pf_units = matvec_workgroups(h);
         if ((rc = launched(launch_attention(at, st), "attention"))) return rc;
         // o_proj + residual (:227-233), with the sums of squares of its rows
         MvArgs o = mv_one(dec->wo + (size_t)l * h * qd, dec->attn, dec->res, dec->res2, h, qd);

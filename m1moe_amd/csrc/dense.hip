@@ -743,8 +743,41 @@ __device__ void attn_merge_share(const AttnArgs& a, int g, int c, int nch, int n
 template <int HD>
 __host__ __device__ constexpr int attn_wide_sub() { return HD == 64 ? 96 : 80; }
 
+// The planes z >= 1 of an attention grid: workgroup p of the P in them
+// (linear dispatch number A + p after the A attention workgroups, so XCD
+// p mod 8 when A and P are multiples of 8)
+// reads pieces p, p + P, ... of the next launch's bytes, whose workgroup b
+// runs on XCD b mod 8: each piece lands in the L2 of the XCD that reads it
+// (and in the memory-side cache).  Nothing waits on this plane.
+__device__ void attn_prefetch(const AttnArgs& a) {
+    const int P = (int)(gridDim.x * gridDim.y * (gridDim.z - 1));
+    const int p = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * (blockIdx.z - 1)));
+    uint32_t acc = 0u;
+    for (int b = p; b < a.pf_units; b += P) {
+        const int64_t lo = (int64_t)b * a.pf_unit;
+        const int64_t hi = min(lo + a.pf_unit, a.pf_bytes);
+        const uint4* src = reinterpret_cast<const uint4*>(a.pf + lo);
+        const int n = (int)((hi - lo) >> 4);
+        for (int i0 = 0; i0 < n; i0 += 256 * 16) {
+            uint4 v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int i = i0 + (int)threadIdx.x + 256 * j;
+                v[j] = i < n ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+        }
+    }
+    asm volatile("" ::"v"(acc));
+}
+
 template <int HD, int QH, int V>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+    if (blockIdx.z) {
+        attn_prefetch(a);
+        return;
+    }
     constexpr bool TWO = V == 1;
     constexpr int SCH = V == 2 ? attn_wide_sub<HD>() : kAttnChunk;   // positions per sub-chunk
     constexpr int LP = HD / 8;                 // lanes per position
@@ -1257,6 +1290,8 @@ int matvec_workgroups(int rows) {
     return (rows + per - 1) / per;
 }
 
+int matvec_rows_per_workgroup(int rows) { return 4 * mv_rpw(rows); }
+
 int launch_matvec_bf16(const MvArgs& a, void* stream) {
     if (a.cols % 8 || a.rows <= 0 || a.cols <= 0) return (int)hipErrorInvalidValue;
     if ((a.embed || a.norm_w) && a.cols > kMvStageMax) return (int)hipErrorInvalidValue;
@@ -1359,7 +1394,14 @@ int launch_attention(const AttnArgs& a, void* stream) {
         return (int)hipErrorInvalidValue;
     if (a.kv_pos <= 0 || a.kv_head <= 0) return (int)hipErrorInvalidValue;
     if (a.sync_merge && !(a.gen && a.fin && attention_grid_fits(a))) return (int)hipErrorInvalidValue;
-    const dim3 grid((unsigned)(a.num_heads / a.qh), (unsigned)((a.max_seq + a.chunk - 1) / a.chunk));
+    if (a.pf && (a.pf_unit <= 0 || a.pf_units <= 0 || a.pf_bytes <= 0 || a.pf_unit % 16 ||
+                 a.pf_bytes % 16 || (int64_t)a.pf_units * a.pf_unit < a.pf_bytes))
+        return (int)hipErrorInvalidValue;
+    // (the prefetch planes only where the attention leaves most CUs idle: on a
+    // full grid they compete with it, cfg4 2615 -> 2670 us per token)
+    const unsigned gx = (unsigned)(a.num_heads / a.qh), gy = (unsigned)((a.max_seq + a.chunk - 1) / a.chunk);
+    const bool pf = a.pf && 2 * (int64_t)gx * gy <= a.cus;
+    const dim3 grid(gx, gy, pf ? 1u + (unsigned)kAttnPfPlanes : 1u);
     switch (a.head_dim) {
         case 64: return launch_attn_hd<64>(a, grid, st);
         case 128: return launch_attn_hd<128>(a, grid, st);

@@ -358,9 +358,18 @@ struct AttnArgs {
     uint32_t* fin;               // [kCountWords] (dense.hip count_out)
     int32_t cus;                 // compute units of the device
     int32_t spin_limit;
+    // optional: bytes the next launch streams (the decoder's o_proj weights),
+    // read by a second plane of workgroups (grid z = 1) into the caches while
+    // the attention runs: pf_units pieces of pf_unit bytes (piece b is what
+    // workgroup b of that launch reads, so it goes to that XCD's L2), pf_bytes
+    // in all; null: no second plane
+    const uint8_t* pf;
+    int64_t pf_unit, pf_bytes;
+    int32_t pf_units;
 };
 
 constexpr int kAttnChunk = 64;   // positions per attention sub-chunk
+constexpr int kAttnPfPlanes = 1;  // prefetch planes of an attention grid (AttnArgs::pf)
 constexpr int kAttnWideChunk = 80;   // chunks of 65 .. this many positions: one wide sub-chunk
 constexpr int kAttnMaxQH = 8;    // q heads per attention workgroup
 constexpr int kAttnMaxChunks = 64;   // workgroups per kv head
@@ -429,6 +438,7 @@ int launch_set_i32(int32_t* p, int32_t v, void* stream);
 int launch_rmsnorm(const float* x, const uint16_t* w, float* out, int n, float eps, void* stream);
 // Workgroups of a matvec launch (the size of am_val / am_idx).
 int matvec_workgroups(int rows);
+int matvec_rows_per_workgroup(int rows);
 int launch_matvec_bf16(const MvArgs& a, void* stream);
 // q heads per attention workgroup (0: unsupported hpkv).
 int attention_qh(int hpkv);

@@ -151,6 +151,10 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="cfg1/cfg4: launch every step's kernels from the host instead of "
                          "replaying the captured one-step graph (for kernel traces)")
+    ap.add_argument("--repeats", type=int, default=20,
+                    help="cfg0/cfg2: repeats of a few steps each after the timed region, "
+                         "their median reported beside it (0: none; the kernel-trace "
+                         "profiles run without them)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES bytes (to scale HBM "
                          "byte counters against a plain copy of known size), then exit")
@@ -272,11 +276,11 @@ def main() -> int:
     gbs = bytes_tok / (layer_us * 1e-6) / 1e9
     log(f"{ms_per_step:.4f} ms/step, {layer_us:.3f} us/layer-token, {gbs:.0f} GB/s")
 
-    # BASELINE.md's protocol beside the timed region above (which `value`
-    # comes from): the median of 20 repeats of a few steps each
+    # the measurement protocol of the baseline beside the timed region above
+    # (which `value` comes from): the median of 20 repeats of a few steps each
     rep_steps = max(1, min(10, args.steps))
     rep_us = []
-    for _ in range(20):
+    for _ in range(max(0, args.repeats)):
         ev0.record()
         for i in range(rep_steps):
             graphs[i % G].launch()
@@ -284,11 +288,14 @@ def main() -> int:
         ctx.sync()
         rep_us.append(ev0.elapsed_ms(ev1) * 1e3 / (rep_steps * R))
     rep_us.sort()
-    repeats = {"n": 20, "steps_each": rep_steps,
-               "median_us_per_layer_token": round(float(np.median(rep_us)), 4),
-               "min_us": round(rep_us[0], 4), "max_us": round(rep_us[-1], 4)}
-    log(f"20 repeats of {rep_steps} steps: median {repeats['median_us_per_layer_token']:.3f} "
-        f"us/layer-token (min {rep_us[0]:.3f}, max {rep_us[-1]:.3f})")
+    repeats = None
+    if rep_us:
+        repeats = {"n": len(rep_us), "steps_each": rep_steps,
+                   "median_us_per_layer_token": round(float(np.median(rep_us)), 4),
+                   "min_us": round(rep_us[0], 4), "max_us": round(rep_us[-1], 4)}
+        log(f"{len(rep_us)} repeats of {rep_steps} steps: median "
+            f"{repeats['median_us_per_layer_token']:.3f} us/layer-token (min {rep_us[0]:.3f}, "
+            f"max {rep_us[-1]:.3f})")
 
     cpu = cpu_all = None
     if args.cpu_seconds > 0:

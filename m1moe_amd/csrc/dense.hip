@@ -380,16 +380,9 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
         }
     };
     // two groups in flight from the start (both before the input is staged),
-    // each refilled as soon as it is used.  (RPW 8, the tall matrices: the
-    // second is requested even where there is none, at the row's clamped
-    // last columns, and the loop below has unconditional refills, so that
-    // every path to a group's use has the same loads in flight in the same
-    // order and the wait before it does not take the newer group too:
-    // 50304 x 2048 45.9 -> 44.0 us.  The shorter matrices, one or two groups
-    // per row, measured slower in that form.)
-    constexpr bool kExactWaits = RPW == 8;
+    // each refilled as soon as it is used
     load(0, cur);
-    if (kExactWaits || ngroups > 1) load(1, nxt);
+    if (ngroups > 1) load(1, nxt);
     if (STAGE) {
         if (early && !(a.attn_part &&
                        attn_defer_nact(*a.pos, a.max_seq, a.attn_chunk, a.attn_heads) > 0))
@@ -400,59 +393,32 @@ __global__ __launch_bounds__(256) void matvec_kernel(MvArgs a) {
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
-    // (kExactWaits: a block past the end is skipped for the whole wave, and
-    // in the last, partial one the lanes past the end keep their sums by a
-    // select, not a branch)
     auto use = [&](int gi, const uint4 (&buf)[U][RPW]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int c0 = gi * 512 * U + 512 * u, c = c0 + 8 * lane;
-            if (kExactWaits ? c0 >= a.cols : c >= a.cols) continue;
-            const bool in = c < a.cols;
-            const int cx = kExactWaits && !in ? a.cols - 8 : c;
+            const int c = gi * 512 * U + 512 * u + 8 * lane;
+            if (c >= a.cols) continue;
             float4 x0, x1;
             if (STAGE) {
-                x0 = *reinterpret_cast<const float4*>(s_x + cx);
-                x1 = *reinterpret_cast<const float4*>(s_x + cx + 4);
+                x0 = *reinterpret_cast<const float4*>(s_x + c);
+                x1 = *reinterpret_cast<const float4*>(s_x + c + 4);
             } else {
-                x0 = *reinterpret_cast<const float4*>(a.x + cx);
-                x1 = *reinterpret_cast<const float4*>(a.x + cx + 4);
+                x0 = *reinterpret_cast<const float4*>(a.x + c);
+                x1 = *reinterpret_cast<const float4*>(a.x + c + 4);
             }
             const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int i = 0; i < RPW; ++i) {
-                float t = acc[i];
+            for (int i = 0; i < RPW; ++i)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) t = fmaf(bf16x8_at(buf[u][i], k), xs[k], t);
-                acc[i] = kExactWaits && !in ? acc[i] : t;
-            }
+                for (int k = 0; k < 8; ++k) acc[i] = fmaf(bf16x8_at(buf[u][i], k), xs[k], acc[i]);
         }
     };
-    if constexpr (kExactWaits) {
-        int gi = 0;
-        for (; gi + 3 < ngroups; gi += 2) {
-            use(gi, cur);
-            load(gi + 2, cur);
+    for (int gi = 0; gi < ngroups; gi += 2) {
+        use(gi, cur);
+        if (gi + 2 < ngroups) load(gi + 2, cur);
+        if (gi + 1 < ngroups) {
             use(gi + 1, nxt);
-            load(gi + 3, nxt);
-        }
-        if (gi + 2 < ngroups) {
-            use(gi, cur);
-            load(gi + 2, cur);
-            use(gi + 1, nxt);
-            use(gi + 2, cur);
-        } else {
-            use(gi, cur);
-            if (gi + 1 < ngroups) use(gi + 1, nxt);
-        }
-    } else {
-        for (int gi = 0; gi < ngroups; gi += 2) {
-            use(gi, cur);
-            if (gi + 2 < ngroups) load(gi + 2, cur);
-            if (gi + 1 < ngroups) {
-                use(gi + 1, nxt);
-                if (gi + 3 < ngroups) load(gi + 3, nxt);
-            }
+            if (gi + 3 < ngroups) load(gi + 3, nxt);
         }
     }
     float bv = -INFINITY, ssq = 0.f;
@@ -1227,7 +1193,12 @@ __global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
 // Rows per wave: more rows per workgroup for taller matrices (each workgroup
 // stages, and may normalise, the whole input; lm_head of a 50k vocabulary
 // reads 1% faster at 8 than at 4).
-int mv_rpw(int rows) { return rows >= 32768 ? 8 : rows >= 8192 ? 4 : rows >= 2048 ? 2 : 1; }
+// Rows per wave by row count.  Tall matrices (the lm_heads) take 3: 12 rows
+// per workgroup, three workgroups per CU at once, the grid many rounds deep
+// (50304 x 2048: 44.1 us at 8 rows per wave, whose 1572 workgroups of two
+// per CU left a last round of 36; 38.1-39.2 at 4, 36.1 at 3, 36.3 at 2;
+// 32000 x 4096: 46.6 at 4, 45.9-46.2 at 3).
+int mv_rpw(int rows) { return rows >= 8192 ? 3 : rows >= 2048 ? 2 : 1; }
 
 template <int RPW>
 int launch_mv(const MvArgs& a, hipStream_t st) {
@@ -1297,8 +1268,7 @@ int launch_matvec_bf16(const MvArgs& a, void* stream) {
     if ((a.embed || a.norm_w) && a.cols > kMvStageMax) return (int)hipErrorInvalidValue;
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (mv_rpw(a.rows)) {
-        case 8: return launch_mv<8>(a, st);
-        case 4: return launch_mv<4>(a, st);
+        case 3: return launch_mv<3>(a, st);
         case 2: return launch_mv<2>(a, st);
         default: return launch_mv<1>(a, st);
     }
